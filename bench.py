@@ -1,0 +1,233 @@
+"""Benchmark of the minGRU / minLM training hot path on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line:
+  value      = minLM training tokens/sec (cfg3: vocab 256, dim 1024, depth 8,
+               ff_mult 4, expansion 1.0, batch 8, seq 2048, bf16 activations,
+               fp32 master weights, Schedule-Free AdamW step), counted as
+               train.py:745 does (batch * chunk tokens per step).
+  roofline   = the scan backward kernel on cfg2 (B16 T8192 H2048 bf16, the
+               scan microbenchmark BASELINE.json names), HBM-bound; achieved =
+               12 B/element (algorithmic bytes) * 2^28 / its average launch time.
+  scan       = cfg2 forward, backward and forward+backward figures.
+  cpu_baseline = the oracle's fp32 restatement of the reference path on the
+               host's cores, on a bounded sample of the cfg3 step.
+Inputs are synthetic and already resident in HBM when the timed region starts.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "train tokens/sec (minLM d1024 L8 seq2048 bf16, 1 GPU); scan HBM GB/s vs peak"
+
+
+def cfg3_matmul_params(dim=1024, depth=8, ff_mult=4, vocab=256, expansion=1.0):
+    di = int(dim * expansion)
+    f = int(dim * ff_mult)
+    per_layer = 2 * di * dim + (dim * di if expansion != 1.0 else 0) + 2 * f * dim
+    return depth * per_layer + vocab * dim
+
+
+def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8):
+    import torch
+
+    from gruboros_amd.mingru.minLM import minLM
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    torch.manual_seed(0)
+    model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0,
+                  compute_dtype=torch.bfloat16).cuda()
+    opt = AdamWScheduleFree(model.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    opt.train()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    ids = torch.randint(0, 256, (B, S), device="cuda", generator=gen)
+
+    def step():
+        loss = model(ids, return_loss=True)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        loss = step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1) / steps
+    flops = 6.0 * cfg3_matmul_params(dim, depth) * B * (S - 1)
+    return {"ms_per_step": ms, "wall_s": wall, "tokens_per_step": B * S, "loss": float(loss),
+            "tflops": flops / (ms * 1e-3) / 1e12, "flops_per_step": flops}
+
+
+def bench_scan(reps=20, B=16, T=8192, Di=2048):
+    import torch
+
+    from gruboros_amd.scan import _launch_bwd, _launch_fwd
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    hidden = torch.randn(B, T, Di, device="cuda", generator=gen).to(torch.bfloat16)
+    gate = torch.randn(B, T, Di, device="cuda", generator=gen).to(torch.bfloat16)
+    x = torch.randn(B, 1, Di, device="cuda", generator=gen)
+    h0 = torch.where(x >= 0, x + 0.5, x.sigmoid()).reshape(B, Di).contiguous()
+    dh = torch.randn(B, T, Di, device="cuda", generator=gen).to(torch.bfloat16)
+    dhid = torch.empty_like(hidden)
+    dgat = torch.empty_like(gate)
+    n = B * T * Di
+
+    def fwd():
+        return _launch_fwd(hidden, gate, h0, torch.bfloat16, need_ckpt=True)
+
+    _, _, ckpt = fwd()
+
+    def bwd():
+        _launch_bwd(hidden, gate, h0, ckpt, dh, None, dhid, dgat, True, torch.bfloat16)
+
+    for _ in range(3):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * reps)]
+    for r in range(reps):
+        evs[3 * r].record()
+        fwd()
+        evs[3 * r + 1].record()
+        bwd()
+        evs[3 * r + 2].record()
+    torch.cuda.synchronize()
+    tf = sum(evs[3 * r].elapsed_time(evs[3 * r + 1]) for r in range(reps)) / reps
+    tb = sum(evs[3 * r + 1].elapsed_time(evs[3 * r + 2]) for r in range(reps)) / reps
+    gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9  # noqa: E731
+    return {
+        "elements": n,
+        "fwd_ms": tf, "bwd_ms": tb, "fwd_bwd_ms": tf + tb,
+        "fwd_GBs": gbs(6 * n, tf), "bwd_GBs": gbs(12 * n, tb), "fwd_bwd_GBs": gbs(18 * n, tf + tb),
+        "fwd_bwd_frac": gbs(18 * n, tf + tb) / HBM_PEAK_GBS,
+        "note": "event times include the look-back workspace clear launched with each kernel",
+    }
+
+
+def cpu_baseline(seconds_budget=20.0, B=1, S=512, dim=1024, depth=8):
+    """The oracle's fp32 restatement of the reference step (mingru/minLM.py:86-155
+    forward + autograd backward) on the host's cores, on a bounded sample of cfg3:
+    one sequence of S tokens per step, same model shape."""
+    import torch
+
+    from oracle import mingru_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=1.0, seed=0)
+    params = {k: v.clone().requires_grad_(True) for k, v in sd.items()}
+    gen = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, 256, (B, S), generator=gen)
+
+    def one():
+        loss, _ = O.minlm_forward(params, ids, depth, return_loss=True, dtype=torch.float32)
+        loss.backward()
+
+    one()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < seconds_budget and len(times) < 10):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > seconds_budget:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": B * S / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"cfg3 model shape (d{dim} L{depth}), batch {B} x seq {S}, fp32 forward+backward "
+                      f"(no optimizer), median of {len(times)} steps; {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--scan-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["train", "scan"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the minGRU hot path is built and "
+              "measured on a single MI355X in this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    from gruboros_amd import _lib
+
+    _lib.lib()
+    print(f"[bench] device {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
+
+    train = scan = None
+    if args.only in (None, "scan"):
+        scan = bench_scan(args.scan_reps)
+        print(f"[bench] scan {json.dumps(scan)}", file=sys.stderr, flush=True)
+    if args.only in (None, "train"):
+        train = bench_train(args.steps, args.warmup)
+        print(f"[bench] train {json.dumps(train)}", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+        print(f"[bench] cpu {json.dumps(cpu)}", file=sys.stderr, flush=True)
+
+    out = {
+        "metric": METRIC,
+        "value": (train["tokens_per_step"] / (train["ms_per_step"] * 1e-3)) if train else None,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": train["ms_per_step"] if train else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random byte ids; random-init weights; scan inputs N(0,1))",
+        "config": {"workload": "cfg3 minLM train step (vocab 256, d1024, L8, ff4, exp1.0, B8, seq2048, "
+                               "SF-AdamW) for value; cfg2 scan B16 T8192 H2048 bf16 for roofline",
+                   "global_batch": 8, "seq_len": 2048, "parallelism": "single GPU"},
+    }
+    if scan:
+        bwd_gbs = scan["bwd_GBs"]
+        out["roofline"] = {"kernel": "scan_bwd_kernel<bf16,bf16> (cfg2)", "bound": "hbm", "achieved": bwd_gbs,
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bwd_gbs / HBM_PEAK_GBS, "traffic": None}
+        out["scan"] = scan
+    if train:
+        out["step_roofline"] = {"bound": "mfma", "achieved": train["tflops"], "peak": BF16_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": train["tflops"] / BF16_PEAK_TFLOPS,
+                                "flops_per_step": train["flops_per_step"]}
+        out["tokens_per_s_predicted"] = 8 * 2047 / (train["ms_per_step"] * 1e-3)
+    if cpu:
+        out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

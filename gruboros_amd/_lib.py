@@ -1,0 +1,84 @@
+"""ctypes binding of libmingru_hip.so (declarations: include/mingru_hip.h).
+
+The library is required: there is no fallback path. Loading it after
+``import torch`` makes it share torch's HIP runtime, so torch streams and
+device pointers can be passed straight through.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+from .build import LIB_PATH
+
+MG_F32 = 0
+MG_BF16 = 1
+
+_c_int, _c_i64, _c_size, _vp, _fp = (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p,
+                                     ctypes.c_void_p)
+
+# name -> (restype, argtypes); mirrors include/mingru_hip.h
+SIGNATURES = {
+    "mg_version": (_c_int, []),
+    "mg_last_error": (ctypes.c_char_p, []),
+    "mg_scan_num_tiles": (_c_int, [_c_int]),
+    "mg_scan_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
+    "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
+                             _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
+    "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _vp,
+                             _vp, _fp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
+}
+
+_LIB = None
+
+
+class MingruHipError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise MingruHipError(
+                f"{LIB_PATH} is missing: build it with `python -m gruboros_amd.build` "
+                "(or __graft_entry__.build()). There is no non-HIP fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().mg_last_error().decode(errors="replace")
+        raise MingruHipError(f"{what or 'libmingru_hip'} failed (code {rc}): {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return MG_F32
+    if dt == torch.bfloat16:
+        return MG_BF16
+    raise MingruHipError(f"unsupported dtype {dt} (float32 and bfloat16 are supported)")
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise MingruHipError(
+                "libmingru_hip kernels run on the GPU only; got a tensor on "
+                f"{t.device}. There is no CPU path in the product; the CPU restatement "
+                "of the reference lives in oracle/ for tests.")

@@ -1,0 +1,134 @@
+// Shared device helpers and host-side error plumbing for libmingru_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "mingru_hip.h"
+
+namespace mg {
+
+// ---------------------------------------------------------------- errors
+
+// Per-thread message of the last failure; returned by mg_last_error().
+char* last_error_buf();
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(last_error_buf(), 512, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MG_OK;
+}
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---------------------------------------------------------------- bf16 / vectors
+
+typedef unsigned short bf16_t;  // raw bfloat16 bits in memory
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
+}
+
+// Four consecutive channels, loaded/stored as one vector access.
+struct f4 { float v[4]; };
+
+template <typename T> struct io4;
+
+template <> struct io4<float> {
+  __device__ __forceinline__ static f4 load(const float* p) {
+    float4 x = *reinterpret_cast<const float4*>(p);
+    return f4{{x.x, x.y, x.z, x.w}};
+  }
+  __device__ __forceinline__ static void store(float* p, const f4& a) {
+    *reinterpret_cast<float4*>(p) = make_float4(a.v[0], a.v[1], a.v[2], a.v[3]);
+  }
+};
+
+template <> struct io4<bf16_t> {
+  __device__ __forceinline__ static f4 load(const bf16_t* p) {
+    uint2 x = *reinterpret_cast<const uint2*>(p);
+    return f4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
+               __uint_as_float(x.y << 16), __uint_as_float(x.y & 0xffff0000u)}};
+  }
+  __device__ __forceinline__ static void store(bf16_t* p, const f4& a) {
+    uint2 x;
+    x.x = static_cast<uint32_t>(f32_to_bf16(a.v[0])) | (static_cast<uint32_t>(f32_to_bf16(a.v[1])) << 16);
+    x.y = static_cast<uint32_t>(f32_to_bf16(a.v[2])) | (static_cast<uint32_t>(f32_to_bf16(a.v[3])) << 16);
+    *reinterpret_cast<uint2*>(p) = x;
+  }
+};
+
+// ---------------------------------------------------------------- gate math
+//
+// minGRU gate math in linear space (reference mingru/minGRU.py:24-28, :56-60):
+//   z = sigmoid(gate)      = exp(-softplus(-gate))   (log_z)
+//   a = 1 - z              = exp(-softplus(gate))    (log_coeffs)
+//   g(x) = x + 0.5 (x >= 0), sigmoid(x) (x < 0)      (exp(log_g(x)))
+// Both z and a are formed from e = exp(-|gate|) so that each keeps full
+// relative precision when it is tiny.
+
+__device__ __forceinline__ void gate_coeffs(float gate, float& a, float& z) {
+  float e = __expf(-fabsf(gate));
+  float r = __builtin_amdgcn_rcpf(1.0f + e);
+  float er = e * r;
+  a = gate >= 0.0f ? er : r;
+  z = gate >= 0.0f ? r : er;
+}
+
+__device__ __forceinline__ float g_tilde(float x) {
+  float e = __expf(fminf(x, 0.0f));
+  return x >= 0.0f ? x + 0.5f : e * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// g(x) and its derivative as autograd of the reference's log_g sees it:
+// 1 for x > 0, 0 at x == 0 (relu'(0) = 0), sigmoid(x)(1 - sigmoid(x)) for x < 0.
+__device__ __forceinline__ void g_tilde_grad(float x, float& gt, float& gp) {
+  float e = __expf(fminf(x, 0.0f));
+  float r = __builtin_amdgcn_rcpf(1.0f + e);
+  gt = x >= 0.0f ? x + 0.5f : e * r;
+  gp = x > 0.0f ? 1.0f : (x == 0.0f ? 0.0f : e * r * r);
+}
+
+// ---------------------------------------------------------------- look-back words
+//
+// One 64-bit word per (time tile, channel) carries a tile's scan state
+// between workgroups. Low half = tag, high half = value (fp32 bits).
+//   tag == 0                : not yet published (workspace is zeroed per call)
+//   tag & 0x80000000        : aggregate; coefficient = bits(tag & 0x7fffffff)
+//   tag == 1                : inclusive prefix; value is the carry itself
+// A coefficient is a product of a_t in [0, 1], so its sign bit is free.
+
+constexpr uint32_t kTagIncl = 1u;
+constexpr uint32_t kTagAggBit = 0x80000000u;
+
+__device__ __forceinline__ void publish_agg(uint64_t* w, float A, float V) {
+  uint64_t x = (static_cast<uint64_t>(__float_as_uint(V)) << 32) |
+               static_cast<uint64_t>(__float_as_uint(A) | kTagAggBit);
+  __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void publish_incl(uint64_t* w, float V) {
+  uint64_t x = (static_cast<uint64_t>(__float_as_uint(V)) << 32) | static_cast<uint64_t>(kTagIncl);
+  __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t poll_word(const uint64_t* w) {
+  return __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mg

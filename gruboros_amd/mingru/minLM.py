@@ -1,0 +1,175 @@
+"""Drop-in mirror of the reference's mingru/minLM.py on MI355X kernels.
+
+Same constructor, module tree, parameter names/shapes/registration order,
+initialisation and forward signature as the reference
+(mingru/minLM.py:17-206), so state dicts, checkpoints, optimizer parameter
+indices and the TBPTT caller (train.py:783-809) carry over unchanged.
+
+Compute: parameters stay fp32 masters; activations run in `compute_dtype`
+(default: the parameters' dtype; bfloat16 for the MI355X training
+configuration) with the residual stream kept in fp32. The minGRU scan runs
+in the fused HIP kernel.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+from torch.nn import Module, ModuleList, RMSNorm
+
+from .minGRU import minGRU, _linear
+
+FP32_EPS = float(torch.finfo(torch.float32).eps)
+
+
+def exists(v):
+    return v is not None
+
+
+def default(v, d):
+    return v if exists(v) else d
+
+
+def FeedForward(dim, mult=4):
+    """Reference mingru/minLM.py:17-23."""
+    dim_inner = int(dim * mult)
+    return nn.Sequential(
+        nn.Linear(dim, dim_inner),
+        nn.GELU(),
+        nn.Linear(dim_inner, dim)
+    )
+
+
+class CausalDepthWiseConv1d(Module):
+    """Reference mingru/minLM.py:27-39 (only built when enable_conv=True; eager torch)."""
+
+    def __init__(self, dim, kernel_size):
+        super().__init__()
+        self.kernel_size = kernel_size
+        self.net = nn.Sequential(
+            nn.Conv1d(dim, dim, kernel_size=kernel_size, groups=dim),
+            nn.Conv1d(dim, dim, kernel_size=1)
+        )
+
+    def forward(self, x):
+        x = x.transpose(1, 2)
+        x = F.pad(x, (self.kernel_size - 1, 0), value=0.)
+        x = self.net(x)
+        return x.transpose(1, 2)
+
+
+def _rms_norm(x, norm, out_dtype):
+    """RMSNorm with the fp32 epsilon whatever the activation dtype
+    (torch.nn.RMSNorm(dim) in the reference, eps=None -> finfo(fp32).eps)."""
+    y = F.rms_norm(x.float(), (x.shape[-1],), norm.weight.float(), eps=FP32_EPS)
+    return y.to(out_dtype)
+
+
+def _ff(x, ff):
+    h = F.gelu(_linear(x, ff[0]))
+    return _linear(h, ff[2])
+
+
+class minLM(Module):
+    """Reference mingru/minLM.py:43-206."""
+
+    def __init__(
+        self,
+        *,
+        num_tokens,
+        dim,
+        depth,
+        ff_mult=4,
+        expansion=1.5,
+        conv_kernel_size=3,
+        use_lstm=None,  # kept for backward compatibility, ignored (as in the reference)
+        enable_conv=False,
+        dropout=0.,
+        compute_dtype=None,
+    ):
+        super().__init__()
+        self.token_emb = nn.Embedding(num_tokens, dim)
+        self.layers = ModuleList([])
+        for _ in range(depth):
+            self.layers.append(ModuleList([
+                CausalDepthWiseConv1d(dim, conv_kernel_size) if enable_conv else None,
+                RMSNorm(dim),
+                minGRU(dim, expansion_factor=expansion),
+                RMSNorm(dim),
+                FeedForward(dim, mult=ff_mult),
+                nn.Dropout(dropout) if dropout > 0. else None
+            ]))
+        self.norm = RMSNorm(dim)
+        self.to_logits = nn.Linear(dim, num_tokens, bias=False)
+        self.can_cache = not enable_conv
+        self.dim = dim
+        self.depth = depth
+        self.compute_dtype = compute_dtype
+        self._initialize_weights()
+
+    def forward(self, x, return_loss=False, return_prev_hiddens=False, prev_hiddens=None):
+        """Reference mingru/minLM.py:86-155."""
+        if return_loss:
+            x, labels = x[:, :-1], x[:, 1:]
+        x = self.token_emb(x)
+        cd = default(self.compute_dtype, x.dtype)
+        x = x.float()  # fp32 residual stream
+
+        if exists(prev_hiddens) and not return_loss:
+            x = x[:, -1:]
+
+        next_prev_hiddens = []
+        prev_hiddens = iter(default(prev_hiddens, []))
+
+        for conv, norm, mingru, ff_norm, ff, dropout in self.layers:
+            if exists(conv):
+                assert len(list(prev_hiddens)) == 0, 'caching not supported for conv version'
+                x = conv(x) + x
+
+            prev_hidden = next(prev_hiddens, None)
+            min_gru_out, next_prev_hidden = mingru(_rms_norm(x, norm, cd), prev_hidden,
+                                                   return_next_prev_hidden=True)
+            x = min_gru_out.float() + x
+            next_prev_hiddens.append(next_prev_hidden)
+
+            x = _ff(_rms_norm(x, ff_norm, cd), ff).float() + x
+
+            if exists(dropout):
+                x = dropout(x)
+
+        embed = _rms_norm(x, self.norm, cd)
+        logits = _linear(embed, self.to_logits)
+
+        if not return_loss:
+            if not return_prev_hiddens:
+                return logits
+            return logits, next_prev_hiddens
+
+        loss = F.cross_entropy(logits.float().transpose(1, 2), labels)
+
+        if not return_prev_hiddens:
+            return loss
+        return loss, next_prev_hiddens
+
+    def _initialize_weights(self):
+        """Reference mingru/minLM.py:157-206: N(0, 0.02/sqrt(dim)) for the embedding,
+        the logits head, every to_hidden_and_gate and every first FF linear;
+        zeros for to_out and the second FF linear (weight and bias), so each
+        block starts as the identity. FF[0].bias keeps nn.Linear's default.
+        The normal draws happen in the reference's order, so a seeded
+        construction reproduces its parameters."""
+        std = 0.02 / math.sqrt(self.dim)
+
+        def normal(t):
+            nn.init.normal_(t, mean=0.0, std=std)
+
+        normal(self.token_emb.weight)
+        normal(self.to_logits.weight)
+        for layer in self.layers:
+            gru, ff = layer[2], layer[4]
+            normal(gru.to_hidden_and_gate.weight)
+            if isinstance(gru.to_out, nn.Linear):
+                nn.init.zeros_(gru.to_out.weight)
+            normal(ff[0].weight)
+            nn.init.zeros_(ff[2].weight)
+            nn.init.zeros_(ff[2].bias)

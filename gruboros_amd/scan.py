@@ -1,0 +1,143 @@
+"""Autograd Functions over the fused gate-math + scan kernels (mg_scan_fwd/bwd).
+
+Reference semantics: mingru/minGRU.py:45-69. Given the two halves of the
+``to_hidden_and_gate`` projection, compute the minGRU hidden sequence
+(`out` before ``to_out``) and ``next_prev_hidden``.
+"""
+import torch
+
+from . import _lib
+from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
+
+
+def _vec_ok(t: torch.Tensor) -> bool:
+    """Last dim dense and the two outer strides multiples of 4 elements."""
+    return t.stride(-1) == 1 and t.stride(0) % 4 == 0 and t.stride(1) % 4 == 0
+
+
+def _prep_h0(h0, B, Di, device):
+    if h0 is None:
+        return None
+    if h0.shape not in ((B, 1, Di), (B, Di)):
+        raise ValueError(f"prev_hidden must be [B,1,Di] = [{B},1,{Di}], got {tuple(h0.shape)}")
+    return h0.reshape(B, Di).to(device=device, dtype=torch.float32).contiguous()
+
+
+def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt):
+    B, T, Di = hidden.shape
+    L = lib()
+    h = torch.empty(B, T, Di, dtype=out_dtype, device=hidden.device)
+    h_last = torch.empty(B, 1, Di, dtype=torch.float32, device=hidden.device)
+    nt = L.mg_scan_num_tiles(T)
+    ckpt = torch.empty(nt, B, Di, dtype=torch.float32, device=hidden.device) if need_ckpt else None
+    wsb = L.mg_scan_workspace_bytes(B, T, Di)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=hidden.device)
+    rc = L.mg_scan_fwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
+                       ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last), ptr(ckpt),
+                       B, T, Di, ptr(ws), wsb, stream_of(hidden))
+    check(rc, "mg_scan_fwd")
+    return h, h_last, ckpt
+
+
+def _launch_bwd(hidden, gate, h0, ckpt, dh, dh_last, dhidden, dgate, want_dh0, out_dtype):
+    B, T, Di = hidden.shape
+    L = lib()
+    dev = hidden.device
+    if dh is None:
+        dh = torch.zeros(B, T, Di, dtype=out_dtype, device=dev)
+    elif not _vec_ok(dh) or dh.dtype not in (torch.float32, torch.bfloat16):
+        dh = dh.contiguous()
+    if dh_last is not None:
+        dh_last = dh_last.reshape(B, Di).to(torch.float32).contiguous()
+    dh0 = torch.empty(B, 1, Di, dtype=torch.float32, device=dev) if want_dh0 else None
+    wsb = L.mg_scan_workspace_bytes(B, T, Di)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
+                       ptr(h0), ptr(ckpt), dtype_code(dh.dtype), ptr(dh), dh.stride(0), dh.stride(1),
+                       ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0), B, T, Di, ptr(ws), wsb, stream_of(hidden))
+    check(rc, "mg_scan_bwd")
+    return dh0
+
+
+class GateScanPacked(torch.autograd.Function):
+    """hg = [hidden | gate] as produced by ``to_hidden_and_gate`` ([B, T, 2*Di]).
+
+    Returns (out [B, T, Di] in hg's dtype, next_prev_hidden [B, 1, Di] fp32).
+    The backward writes d(hg) in one buffer, so the projection's backward
+    consumes it without a concatenation.
+    """
+
+    @staticmethod
+    def forward(ctx, hg, h0):
+        ctx.set_materialize_grads(False)
+        B, T, D2 = hg.shape
+        Di = D2 // 2
+        hidden, gate = hg[..., :Di], hg[..., Di:]
+        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hg.dtype, need_ckpt=True)
+        ctx.save_for_backward(hg, h0, ckpt)
+        return h, h_last
+
+    @staticmethod
+    def backward(ctx, dh, dh_last):
+        hg, h0, ckpt = ctx.saved_tensors
+        B, T, D2 = hg.shape
+        Di = D2 // 2
+        if dh is None and dh_last is None:
+            return None, None
+        dhg = torch.empty_like(hg, memory_format=torch.contiguous_format)
+        want_dh0 = h0 is not None and ctx.needs_input_grad[1]
+        dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, ckpt, dh, dh_last, dhg[..., :Di], dhg[..., Di:],
+                          want_dh0, hg.dtype)
+        return dhg, (dh0.reshape(h0.shape) if want_dh0 else None)
+
+
+class GateScan(torch.autograd.Function):
+    """Separate hidden and gate pre-activations ([B, T, Di] each, same strides)."""
+
+    @staticmethod
+    def forward(ctx, hidden, gate, h0):
+        ctx.set_materialize_grads(False)
+        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hidden.dtype, need_ckpt=True)
+        ctx.save_for_backward(hidden, gate, h0, ckpt)
+        return h, h_last
+
+    @staticmethod
+    def backward(ctx, dh, dh_last):
+        hidden, gate, h0, ckpt = ctx.saved_tensors
+        if dh is None and dh_last is None:
+            return None, None, None
+        # inputs are contiguous (gate_scan ensures it), so the gradients,
+        # which the kernel writes with the inputs' strides, are too
+        dhidden = torch.empty_like(hidden)
+        dgate = torch.empty_like(gate)
+        want_dh0 = h0 is not None and ctx.needs_input_grad[2]
+        dh0 = _launch_bwd(hidden, gate, h0, ckpt, dh, dh_last, dhidden, dgate, want_dh0, hidden.dtype)
+        return dhidden, dgate, (dh0.reshape(h0.shape) if want_dh0 else None)
+
+
+def gate_scan(hidden, gate, prev_hidden=None):
+    """minGRU gate math + scan on separate pre-activation tensors.
+
+    hidden, gate: [B, T, Di] (fp32 or bf16, CUDA). prev_hidden: [B, 1, Di] or None.
+    Returns (out [B, T, Di], next_prev_hidden [B, 1, Di] fp32).
+    """
+    require_cuda(hidden, gate, prev_hidden)
+    if hidden.shape != gate.shape or hidden.dim() != 3:
+        raise ValueError(f"hidden {tuple(hidden.shape)} and gate {tuple(gate.shape)} must both be [B,T,Di]")
+    if hidden.dtype != gate.dtype:
+        raise ValueError("hidden and gate must share a dtype")
+    hidden, gate = hidden.contiguous(), gate.contiguous()
+    B, T, Di = hidden.shape
+    h0 = _prep_h0(prev_hidden, B, Di, hidden.device)
+    return GateScan.apply(hidden, gate, h0)
+
+
+def gate_scan_packed(hg, prev_hidden=None):
+    """minGRU gate math + scan on the packed projection output hg = [hidden | gate]."""
+    require_cuda(hg, prev_hidden)
+    if hg.dim() != 3 or hg.shape[-1] % 2:
+        raise ValueError(f"hg must be [B,T,2*Di], got {tuple(hg.shape)}")
+    hg = hg.contiguous()  # the gradient buffer is written with hg's strides
+    B, T, D2 = hg.shape
+    h0 = _prep_h0(prev_hidden, B, D2 // 2, hg.device)
+    return GateScanPacked.apply(hg, h0)

@@ -1,0 +1,254 @@
+"""CPU oracle for the minGRU / minLM training hot path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker or as the timed CPU baseline.
+The product (gruboros_amd) never calls it.
+
+Two kinds of function live here:
+
+* Restatements of the reference, op for op, in a caller-chosen dtype
+  (float64 for the parity oracle, float32 for "the reference's own
+  precision" and for the CPU baseline). Each cites the reference line it
+  follows (paths relative to the reference tree).
+* Independent evaluations of the same mathematics used to pin the
+  restatements: a brute-force linear recurrence (float64 numpy), the
+  textbook cumulative log-add-exp (numpy.logaddexp.accumulate), and the
+  closed-form adjoint of the scan. The tests compare the restatements with
+  these, so a dropped term, wrong sign or shifted index in either shows up.
+
+Pins (see tests/test_oracle.py): g/log_g and the gate math against closed
+forms and branch special cases; the scan against the linear recurrence,
+logaddexp.accumulate and invariants (convexity bounds, constant input,
+geometric closed form, chunked == unchunked, T one-step updates == scan);
+the backward against torch.autograd.gradcheck and the closed form; RMSNorm
+against torch.nn.functional.rms_norm; the loss against
+torch.nn.functional.cross_entropy. Parity of the seeded initialisation
+order (mingru/minLM.py:157-206) is not pinned: tests share one state dict
+between the oracle and the product instead.
+"""
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+FP32_EPS = float(torch.finfo(torch.float32).eps)
+
+
+# --------------------------------------------------------------------------- gate math
+
+def g(x):
+    """mingru/minGRU.py:24-25."""
+    return torch.where(x >= 0, x + 0.5, x.sigmoid())
+
+
+def log_g(x):
+    """mingru/minGRU.py:27-28."""
+    return torch.where(x >= 0, (F.relu(x) + 0.5).log(), -F.softplus(-x))
+
+
+def heinsen_associative_scan_log(log_coeffs, log_values):
+    """mingru/minGRU.py:16-20 (scan along dim 1)."""
+    a_star = log_coeffs.cumsum(dim=1)
+    log_h0_plus_b_star = (log_values - a_star).logcumsumexp(dim=1)
+    log_h = a_star + log_h0_plus_b_star
+    return log_h.exp()
+
+
+def mingru_scan(hidden, gate, prev_hidden=None):
+    """minGRU.forward after the projection, mingru/minGRU.py:43-69 (to_out excluded).
+
+    hidden, gate: [B, T, Di]; prev_hidden: [B, 1, Di] or None.
+    Returns (out [B, T, Di], next_prev_hidden [B, 1, Di]) in the inputs' dtype.
+    """
+    seq_len = hidden.shape[1]
+    if seq_len == 1:                                           # :47-52
+        hid = g(hidden)
+        gt = gate.sigmoid()
+        out = torch.lerp(prev_hidden, hid, gt) if prev_hidden is not None else hid * gt
+    else:                                                      # :53-67
+        log_coeffs = -F.softplus(gate)
+        log_z = -F.softplus(-gate)
+        log_tilde_h = log_g(hidden)
+        log_values = log_z + log_tilde_h
+        if prev_hidden is not None:
+            log_values = torch.cat((prev_hidden.log(), log_values), dim=1)
+            log_coeffs = F.pad(log_coeffs, (0, 0, 1, 0))
+        out = heinsen_associative_scan_log(log_coeffs, log_values)
+        out = out[:, -seq_len:]
+    next_prev_hidden = out[:, -1:]                             # :69
+    return out, next_prev_hidden
+
+
+# --------------------------------------------------------------------------- independent pins
+
+def _np_sigmoid(x):
+    return np.where(x >= 0, 1.0 / (1.0 + np.exp(-np.abs(x))), np.exp(-np.abs(x)) / (1.0 + np.exp(-np.abs(x))))
+
+
+def np_g(x):
+    """Closed form of g: x + 1/2 for x >= 0, logistic sigmoid for x < 0."""
+    return np.where(x >= 0, x + 0.5, _np_sigmoid(x))
+
+
+def np_g_prime(x):
+    """d g / dx as autograd of the reference's log_g sees it (relu'(0) = 0)."""
+    s = _np_sigmoid(x)
+    return np.where(x > 0, 1.0, np.where(x == 0, 0.0, s * (1.0 - s)))
+
+
+def linear_recurrence(hidden, gate, h0=None):
+    """Brute-force float64 h_t = (1 - z_t) h_{t-1} + z_t g(hidden_t), z = sigmoid(gate).
+
+    numpy arrays [B, T, Di]; h0 [B, Di] or None (zero state). Returns h [B, T, Di].
+    """
+    hidden = np.asarray(hidden, dtype=np.float64)
+    gate = np.asarray(gate, dtype=np.float64)
+    B, T, Di = hidden.shape
+    z = _np_sigmoid(gate)
+    a = _np_sigmoid(-gate)
+    b = z * np_g(hidden)
+    h = np.zeros((B, Di)) if h0 is None else np.asarray(h0, dtype=np.float64).reshape(B, Di).copy()
+    out = np.empty((B, T, Di))
+    for t in range(T):
+        h = a[:, t] * h + b[:, t]
+        out[:, t] = h
+    return out
+
+
+def logaddexp_scan(hidden, gate, h0=None):
+    """Textbook evaluation of the same recurrence in log space with numpy's
+    cumulative logaddexp: log h_t = A_t + logaddexp_{k<=t}(log b_k - A_k),
+    A_t = sum_{k<=t} log a_k, with log h0 as an extra leading term."""
+    hidden = np.asarray(hidden, dtype=np.float64)
+    gate = np.asarray(gate, dtype=np.float64)
+    la = -np.logaddexp(0.0, gate)                       # log(1 - sigmoid(gate))
+    lb = -np.logaddexp(0.0, -gate) + np.log(np_g(hidden))
+    if h0 is not None:
+        B, _, Di = hidden.shape
+        lh0 = np.log(np.asarray(h0, dtype=np.float64).reshape(B, 1, Di))
+        la = np.concatenate([np.zeros_like(lh0), la], axis=1)
+        lb = np.concatenate([lh0, lb], axis=1)
+    A = np.cumsum(la, axis=1)
+    lh = A + np.logaddexp.accumulate(lb - A, axis=1)
+    h = np.exp(lh)
+    return h[:, 1:] if h0 is not None else h
+
+
+def scan_backward_closed_form(hidden, gate, h0, dh, dh_last=None):
+    """Closed-form adjoint of the recurrence (float64 numpy):
+
+      lambda_t = dh_t + a_{t+1} lambda_{t+1}
+      dgate_t = lambda_t z_t (1 - z_t) (g(hidden_t) - h_{t-1})
+      dhidden_t = lambda_t z_t g'(hidden_t)
+      dh0 = a_0 lambda_0
+    Returns (dhidden, dgate, dh0 [B, Di])."""
+    hidden = np.asarray(hidden, dtype=np.float64)
+    gate = np.asarray(gate, dtype=np.float64)
+    dh = np.asarray(dh, dtype=np.float64).copy()
+    B, T, Di = hidden.shape
+    if dh_last is not None:
+        dh[:, -1] += np.asarray(dh_last, dtype=np.float64).reshape(B, Di)
+    h = linear_recurrence(hidden, gate, h0)
+    hp = np.concatenate([(np.zeros((B, 1, Di)) if h0 is None else np.asarray(h0, np.float64).reshape(B, 1, Di)),
+                         h[:, :-1]], axis=1)
+    z = _np_sigmoid(gate)
+    a = _np_sigmoid(-gate)
+    lam = np.zeros((B, T, Di))
+    nxt = np.zeros((B, Di))
+    for t in range(T - 1, -1, -1):
+        lam[:, t] = dh[:, t] + nxt
+        nxt = a[:, t] * lam[:, t]
+    dgate = lam * z * a * (np_g(hidden) - hp)
+    dhidden = lam * z * np_g_prime(hidden)
+    return dhidden, dgate, nxt
+
+
+# --------------------------------------------------------------------------- minLM pieces
+
+def rms_norm(x, weight, eps=FP32_EPS):
+    """torch.nn.RMSNorm(dim) as used at mingru/minLM.py:67,69,74: y = x * rsqrt(mean(x^2) + eps) * w.
+    eps is float32's machine epsilon whatever the activation dtype."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * weight
+
+
+def feed_forward(x, w1, b1, w2, b2):
+    """mingru/minLM.py:17-23: Linear -> exact (erf) GELU -> Linear."""
+    return F.linear(F.gelu(F.linear(x, w1, b1)), w2, b2)
+
+
+def cross_entropy_mean(logits, labels):
+    """mingru/minLM.py:146-149: mean over positions of logsumexp(logits) - logits[label]."""
+    lse = torch.logsumexp(logits, dim=-1)
+    picked = torch.gather(logits, -1, labels.unsqueeze(-1)).squeeze(-1)
+    return (lse - picked).mean()
+
+
+def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0):
+    """Body of mingru/minLM.py:97-138 (embedding -> blocks -> final norm -> logits),
+    conv and dropout disabled. p: state dict already in the working dtype.
+    Returns (logits, next_prev_hiddens)."""
+    x = F.embedding(ids, p["token_emb.weight"])                            # :97
+    hiddens = iter(prev_hiddens or [])
+    nxt = []
+    for i in range(depth):                                                 # :107-135
+        pre = f"layers.{i}."
+        prev = next(hiddens, None)
+        if prev is not None:
+            prev = prev.to(x.dtype)
+        n = rms_norm(x, p[pre + "1.weight"])                               # :121
+        hg = F.linear(n, p[pre + "2.to_hidden_and_gate.weight"])           # minGRU.py:45
+        hidden, gate = hg.chunk(2, dim=-1)
+        out, h_next = mingru_scan(hidden, gate, prev)
+        if expansion != 1.0:
+            out = F.linear(out, p[pre + "2.to_out.weight"])                # minGRU.py:71
+        x = out + x                                                        # :125
+        nxt.append(h_next)
+        x = feed_forward(rms_norm(x, p[pre + "3.weight"]), p[pre + "4.0.weight"], p[pre + "4.0.bias"],
+                         p[pre + "4.2.weight"], p[pre + "4.2.bias"]) + x  # :130
+    embed = rms_norm(x, p["norm.weight"])                                  # :137
+    return F.linear(embed, p["to_logits.weight"]), nxt                     # :138
+
+
+def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expansion=1.0, dtype=torch.float64):
+    """mingru/minLM.py:86-155 with conv and dropout disabled (enable_conv=False, dropout=0).
+
+    params: state dict with the reference's key names (floating tensors are
+    cast to `dtype`). Returns (loss or logits, next_prev_hiddens).
+    """
+    p = {k: (v.to(dtype) if v.is_floating_point() else v) for k, v in params.items()}
+    if return_loss:
+        ids, labels = ids[:, :-1], ids[:, 1:]                              # :94-95
+    if prev_hiddens is not None and not return_loss:
+        ids = ids[:, -1:]                                                  # :101-102 (per-token, so slicing ids == slicing x)
+    logits, nxt = minlm_core(p, ids, depth, prev_hiddens, expansion)
+    if not return_loss:
+        return logits, nxt
+    return cross_entropy_mean(logits, labels), nxt                         # :146-149
+
+
+def make_minlm_state(num_tokens, dim, depth, ff_mult=4, expansion=1.0, seed=0, dtype=torch.float32):
+    """A state dict with the reference's keys, order and shapes
+    (mingru/minLM.py:58-75, minGRU.py:40-41), initialised as
+    mingru/minLM.py:157-206 describes (distributionally; the RNG draw order of
+    the reference is not reproduced)."""
+    gen = torch.Generator().manual_seed(seed)
+    std = 0.02 / math.sqrt(dim)
+    di = int(dim * expansion)
+    f = int(dim * ff_mult)
+    sd = {"token_emb.weight": torch.randn(num_tokens, dim, generator=gen) * std}
+    for i in range(depth):
+        pre = f"layers.{i}."
+        sd[pre + "1.weight"] = torch.ones(dim)
+        sd[pre + "2.to_hidden_and_gate.weight"] = torch.randn(2 * di, dim, generator=gen) * std
+        if expansion != 1.0:
+            sd[pre + "2.to_out.weight"] = torch.zeros(dim, di)
+        sd[pre + "3.weight"] = torch.ones(dim)
+        sd[pre + "4.0.weight"] = torch.randn(f, dim, generator=gen) * std
+        bound = 1.0 / math.sqrt(dim)
+        sd[pre + "4.0.bias"] = (torch.rand(f, generator=gen) * 2 - 1) * bound
+        sd[pre + "4.2.weight"] = torch.zeros(dim, f)
+        sd[pre + "4.2.bias"] = torch.zeros(dim)
+    sd["norm.weight"] = torch.ones(dim)
+    sd["to_logits.weight"] = torch.randn(num_tokens, dim, generator=gen) * std
+    return {k: v.to(dtype) for k, v in sd.items()}

@@ -1,0 +1,76 @@
+"""The C-ABI library loads, exports every symbol include/*.h declares, and
+rejects bad arguments with an error code and message (no GPU work needed:
+argument checks run before anything is enqueued)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from gruboros_amd import _lib
+from gruboros_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(mg_\w+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(LIB_PATH):
+        pytest.fail(f"{LIB_PATH} not built (run __graft_entry__.build())")
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(L):
+    names = declared_symbols()
+    assert "mg_scan_fwd" in names and "mg_version" in names
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/ but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in gruboros_amd/_lib.py"
+
+
+def test_version_and_queries(L):
+    assert L.mg_version() >= 100
+    assert L.mg_scan_num_tiles(1) == 1
+    assert L.mg_scan_num_tiles(128) == 1
+    assert L.mg_scan_num_tiles(129) == 2
+    # header + one 8-byte look-back word per (tile, channel)
+    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + 3 * 2 * 64 * 8
+
+
+def _fwd(L, **kw):
+    args = dict(in_dtype=1, hidden=16, gate=16, in_sb=1024, in_ld=64, h0=None, out_dtype=1, h=16, out_sb=512,
+                out_ld=64, h_last=None, ckpt=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
+    args.update(kw)
+    return L.mg_scan_fwd(*args.values())
+
+
+def test_argument_errors(L):
+    assert _fwd(L, Di=62) == 1
+    assert "multiple of 4" in L.mg_last_error().decode()
+    assert _fwd(L, T=0) == 1
+    assert _fwd(L, wsb=8) == 3
+    assert "workspace" in L.mg_last_error().decode()
+    assert _fwd(L, in_dtype=7) == 2
+    assert _fwd(L, hidden=None) == 1
+    assert _fwd(L, in_ld=66) == 1
+    assert _fwd(L, hidden=18) == 1  # misaligned
+    assert _fwd(L, out_dtype=1, in_dtype=0) == 2  # f32 -> bf16 not offered
+
+
+def test_product_refuses_cpu_tensors():
+    import torch
+    from gruboros_amd.scan import gate_scan
+
+    x = torch.zeros(1, 4, 8)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        gate_scan(x, x)
