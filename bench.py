@@ -69,7 +69,7 @@ def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8):
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / steps
     flops = 6.0 * cfg3_matmul_params(dim, depth) * B * (S - 1)
-    return {"ms_per_step": ms, "wall_s": wall, "tokens_per_step": B * S, "loss": float(loss),
+    return {"ms_per_step": ms, "wall_s": wall, "tokens_per_step": B * S, "loss": float(loss.detach()),
             "tflops": flops / (ms * 1e-3) / 1e12, "flops_per_step": flops}
 
 

@@ -17,8 +17,6 @@ c = weight_k / sum(weight), weight_k = (k+1)^r * lr_max^weight_lr_power:
 eval() moves p to x = (y - (1 - b1) z) / b1 and train() moves it back,
 exactly as the package's mode switch does.
 """
-import math
-
 import torch
 
 

@@ -75,7 +75,7 @@ def _run(hidden, gate, h0, dh, dlast, packed):
         dhid, dgat = hg.grad[..., :Di], hg.grad[..., Di:]
     else:
         dhid, dgat = hd.grad, gt.grad
-    return (out.float().cpu(), nxt.cpu(), dhid.float().cpu(), dgat.float().cpu(),
+    return (out.detach().float().cpu(), nxt.detach().cpu(), dhid.float().cpu(), dgat.float().cpu(),
             (hz.grad.cpu() if hz is not None else None))
 
 
@@ -159,6 +159,7 @@ def test_scan_cfg2_full_size_bf16():
     hd, gt = hidden.clone().requires_grad_(True), gate.clone().requires_grad_(True)
     out, last = gate_scan(hd, gt, h0)
     out.backward(dh)
+    out, last = out.detach(), last.detach()
     torch.cuda.synchronize()
 
     # properties over every channel: positivity, and chunked == full
