@@ -89,12 +89,12 @@ def bench_scan(reps=20, B=16, T=8192, Di=2048):
     n = B * T * Di
 
     def fwd():
-        return _launch_fwd(hidden, gate, h0, torch.bfloat16, need_ckpt=True)
+        return _launch_fwd(hidden, gate, h0, torch.bfloat16)
 
-    _, _, ckpt = fwd()
+    h, _ = fwd()
 
     def bwd():
-        _launch_bwd(hidden, gate, h0, ckpt, dh, None, dhid, dgat, True, torch.bfloat16)
+        _launch_bwd(hidden, gate, h0, h, dh, None, dhid, dgat, True)
 
     for _ in range(3):
         fwd()

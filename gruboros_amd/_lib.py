@@ -21,12 +21,11 @@ _c_int, _c_i64, _c_size, _vp, _fp = (ctypes.c_int, ctypes.c_int64, ctypes.c_size
 SIGNATURES = {
     "mg_version": (_c_int, []),
     "mg_last_error": (ctypes.c_char_p, []),
-    "mg_scan_num_tiles": (_c_int, [_c_int]),
     "mg_scan_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
-    "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
+    "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp,
                              _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
-    "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _vp,
-                             _vp, _fp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
+    "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64,
+                             _vp, _c_i64, _c_i64, _fp, _vp, _vp, _fp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
 }
 
 _LIB = None

@@ -50,6 +50,7 @@ struct f4 { float v[4]; };
 template <typename T> struct io4;
 
 template <> struct io4<float> {
+  __device__ __forceinline__ static f4 fill(float x) { return f4{{x, x, x, x}}; }
   __device__ __forceinline__ static f4 load(const float* p) {
     float4 x = *reinterpret_cast<const float4*>(p);
     return f4{{x.x, x.y, x.z, x.w}};
@@ -60,6 +61,10 @@ template <> struct io4<float> {
 };
 
 template <> struct io4<bf16_t> {
+  __device__ __forceinline__ static f4 fill(float x) {
+    const float r = bf16_to_f32(f32_to_bf16(x));
+    return f4{{r, r, r, r}};
+  }
   __device__ __forceinline__ static f4 load(const bf16_t* p) {
     uint2 x = *reinterpret_cast<const uint2*>(p);
     return f4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
@@ -76,32 +81,56 @@ template <> struct io4<bf16_t> {
 // ---------------------------------------------------------------- gate math
 //
 // minGRU gate math in linear space (reference mingru/minGRU.py:24-28, :56-60):
-//   z = sigmoid(gate)      = exp(-softplus(-gate))   (log_z)
-//   a = 1 - z              = exp(-softplus(gate))    (log_coeffs)
-//   g(x) = x + 0.5 (x >= 0), sigmoid(x) (x < 0)      (exp(log_g(x)))
-// Both z and a are formed from e = exp(-|gate|) so that each keeps full
-// relative precision when it is tiny.
+//   z = sigmoid(gate)  = exp(log_z),       log_z = -softplus(-gate)
+//   a = 1 - z          = exp(log_coeffs),  log_coeffs = -softplus(gate)
+//   g(x) = x + 0.5 (x >= 0), sigmoid(x) (x < 0)   = exp(log_g(x))
+//   v = z g(hidden)    = exp(log_values)
+// With e = exp(-gate), e2 = exp(-|hidden|), P = 1 + e, Q = 1 + e2 and
+// R = 1 / (P Q) (one reciprocal for both sigmoids; Q cancels in z):
+//   z = R Q,  a = e z,  v = (hidden + 0.5) z  (hidden >= 0)  |  e2 R  (hidden < 0).
+// e is clamped at 2^100 (gate < -69.3), so P Q and R stay normal numbers:
+// there z = 2^-100 instead of e^gate, and a rounds to 1. Rows past the end
+// of the sequence are loaded as gate = -inf, hidden = 0, which gives
+// a = 1 and v < 2^-100: the identity step up to that residue.
 
-__device__ __forceinline__ void gate_coeffs(float gate, float& a, float& z) {
-  float e = __expf(-fabsf(gate));
-  float r = __builtin_amdgcn_rcpf(1.0f + e);
-  float er = e * r;
-  a = gate >= 0.0f ? er : r;
-  z = gate >= 0.0f ? r : er;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kMaxExp2 = 100.0f;
+
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+struct GateTerms {
+  float e, e2, P, Q, R;
+};
+
+__device__ __forceinline__ GateTerms gate_terms(float gate, float hid) {
+  GateTerms t;
+  t.e = exp2_raw(fminf(gate * -kLog2e, kMaxExp2));
+  t.e2 = exp2_raw(fabsf(hid) * -kLog2e);  // e^-|hidden|; only used when hidden < 0
+  t.P = 1.0f + t.e;
+  t.Q = 1.0f + t.e2;
+  t.R = __builtin_amdgcn_rcpf(t.P * t.Q);
+  return t;
 }
 
-__device__ __forceinline__ float g_tilde(float x) {
-  float e = __expf(fminf(x, 0.0f));
-  return x >= 0.0f ? x + 0.5f : e * __builtin_amdgcn_rcpf(1.0f + e);
+// Forward coefficients: h_t = a h_{t-1} + v.
+__device__ __forceinline__ void fwd_coeffs(float gate, float hid, float& a, float& v) {
+  const GateTerms t = gate_terms(gate, hid);
+  const float z = t.R * t.Q;
+  a = t.e * z;
+  v = hid >= 0.0f ? (hid + 0.5f) * z : t.e2 * t.R;
 }
 
-// g(x) and its derivative as autograd of the reference's log_g sees it:
-// 1 for x > 0, 0 at x == 0 (relu'(0) = 0), sigmoid(x)(1 - sigmoid(x)) for x < 0.
-__device__ __forceinline__ void g_tilde_grad(float x, float& gt, float& gp) {
-  float e = __expf(fminf(x, 0.0f));
-  float r = __builtin_amdgcn_rcpf(1.0f + e);
-  gt = x >= 0.0f ? x + 0.5f : e * r;
-  gp = x > 0.0f ? 1.0f : (x == 0.0f ? 0.0f : e * r * r);
+// Backward adds z and q = z g'(hidden), with g' as autograd of the
+// reference's log_g sees it: 1 for x > 0, 0 at x == 0 (relu'(0) = 0),
+// sigmoid(x) (1 - sigmoid(x)) for x < 0.
+__device__ __forceinline__ void bwd_coeffs(float gate, float hid, float& a, float& z, float& v, float& q) {
+  const GateTerms t = gate_terms(gate, hid);
+  z = t.R * t.Q;
+  a = t.e * z;
+  const float vneg = t.e2 * t.R;             // z sigmoid(x)
+  v = hid >= 0.0f ? (hid + 0.5f) * z : vneg;
+  const float qneg = vneg * (t.R * t.P);     // z sigmoid(x) (1 - sigmoid(x))
+  q = hid > 0.0f ? z : (hid < 0.0f ? qneg : 0.0f);
 }
 
 // ---------------------------------------------------------------- look-back words

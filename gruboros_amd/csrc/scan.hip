@@ -9,21 +9,20 @@
 // cancellation (the log-space form loses ~|a*| * 2^-24 relative accuracy).
 //
 // Work decomposition (one pass over HBM per direction):
-//   * A tile is kTileRows consecutive time steps x kTileCh consecutive
-//     channels of one batch row; one 256-thread workgroup per tile.
-//   * Thread (cl, s) owns 4 adjacent channels (one 8-byte bf16 / 16-byte
-//     fp32 vector per row) and a run of kSubRows consecutive time steps.
-//     16 lanes cover 64 channels, so every row segment a wave touches is a
-//     full 128-byte line for bf16.
-//   * Each thread scans its run in registers and produces the run's affine
-//     map h -> A h + V. Runs are combined in LDS; the tile's map is handed
-//     to later tiles through look-back words in the workspace (decoupled
-//     look-back). Tiles take tickets from an atomic counter so a tile only
-//     ever waits on tiles that were started before it.
-//   * The backward walks tiles in reverse time order. It needs h_{t-1};
-//     instead of reading the forward output it rebuilds h in fp32 from the
-//     per-tile entry state the forward saved (ckpt), which saves 2 bytes per
-//     element of traffic and keeps h at fp32 accuracy for bf16 outputs.
+//   * A tile is a run of consecutive time steps x 64 consecutive channels of
+//     one batch row; one workgroup per tile. Thread (cl, s) owns 4 adjacent
+//     channels (one 8-byte bf16 / 16-byte fp32 vector per row) and a run of
+//     consecutive time steps; 16 lanes cover 64 channels, so every row
+//     segment a wave touches is a full 128-byte line for bf16.
+//   * Each thread scans its run in registers, giving the run's affine map
+//     h -> A h + V. The runs of a tile are combined by a Hillis-Steele scan
+//     in LDS; the tile's map goes to later tiles through look-back words in
+//     the workspace (decoupled look-back). Each chain of tiles (one channel
+//     block) takes tickets from its own atomic counter, so a tile only ever
+//     waits on tiles of its chain that were started before it.
+//   * The backward walks tiles in reverse time order with the adjoint
+//     recurrence. It needs h_{t-1}: it reads the forward output once per run
+//     (the row before the run) and rebuilds the run's states in fp32 from it.
 
 #include <algorithm>
 
@@ -32,35 +31,52 @@
 namespace mg {
 namespace scan {
 
-constexpr int kVec = 4;                       // channels per thread
-constexpr int kChLanes = 16;                  // threads across channels
-constexpr int kSubs = 16;                     // time runs per tile
-constexpr int kSubRows = 8;                   // time steps per run
-constexpr int kThreads = kChLanes * kSubs;    // 256
-constexpr int kTileRows = kSubs * kSubRows;   // 128
-constexpr int kTileCh = kChLanes * kVec;      // 64
-constexpr size_t kWsHeader = 256;             // ticket counter lives here
+constexpr int kVec = 4;                   // channels per thread
+constexpr int kChLanes = 16;              // threads across channels
+constexpr int kTileCh = kChLanes * kVec;  // 64 channels per tile
+
+// Forward tiles: 16 runs of 8 steps (256 threads, 128 steps). The backward
+// keeps three values per element plus the incoming gradient, so it uses
+// shorter runs: 16 runs of 4 steps (256 threads, 64 steps).
+#ifndef MG_SCAN_BWD_SUBS
+#define MG_SCAN_BWD_SUBS 16
+#define MG_SCAN_BWD_ROWS 4
+#endif
+constexpr int kFwdSubs = 16, kFwdRows = 8;
+constexpr int kBwdSubs = MG_SCAN_BWD_SUBS, kBwdRows = MG_SCAN_BWD_ROWS;
+constexpr int kFwdTileRows = kFwdSubs * kFwdRows;
+constexpr int kBwdTileRows = kBwdSubs * kBwdRows;
 
 struct Geometry {
   int B, T, Di;
-  int nblk_d;   // channel blocks per batch row
-  int ncb;      // channel blocks in total (B * nblk_d)
-  int ntiles;   // time tiles
-  int64_t BD;   // B * Di
+  int nblk_d;    // channel blocks per batch row
+  int ncb;       // chains = channel blocks in total (B * nblk_d)
+  int tile_rows; // time steps per tile (direction dependent)
+  int ntiles;    // time tiles per chain
+  int64_t BD;    // B * Di
 };
 
-__device__ __forceinline__ void tile_coords(const Geometry& g, uint32_t ticket, bool reverse,
-                                            int& k, int& b, int& d) {
-  const int kk = static_cast<int>(ticket / g.ncb);
-  const int cbi = static_cast<int>(ticket % g.ncb);
+// Workspace: one ticket counter per chain, then one look-back word per
+// (tile, channel).
+inline size_t ws_header_bytes(int ncb) { return (static_cast<size_t>(ncb) * 4 + 255) / 256 * 256; }
+
+// Chain and tile of this workgroup. The chain comes from the block index; the
+// tile (time position) from the chain's ticket counter, in start order. The
+// results are wave-uniform, so tile base addresses live in scalar registers.
+__device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters, uint32_t* s_ticket,
+                                          bool reverse, int& k, int& b, int& d0) {
+  const int cbi = static_cast<int>(blockIdx.x % static_cast<uint32_t>(g.ncb));
+  if (threadIdx.x == 0) *s_ticket = atomicAdd(counters + cbi, 1u);
+  __syncthreads();
+  const int kk = static_cast<int>(__builtin_amdgcn_readfirstlane(*s_ticket));
   k = reverse ? (g.ntiles - 1 - kk) : kk;
   b = cbi / g.nblk_d;
-  d = (cbi % g.nblk_d) * kTileCh + (static_cast<int>(threadIdx.x) % kChLanes) * kVec;
+  d0 = (cbi % g.nblk_d) * kTileCh;
 }
 
-// Walk back (forward scan: towards earlier tiles, step = -1; backward scan:
-// towards later tiles, step = +1) until an inclusive prefix is found, folding
-// aggregates on the way. Returns the state entering tile k for 4 channels.
+// Walk from tile k + step in direction `step` (-1: earlier tiles, forward
+// scan; +1: later tiles, backward scan) until an inclusive prefix is found,
+// folding aggregates on the way. Returns the state entering tile k.
 __device__ __forceinline__ f4 look_back(const uint64_t* status, int64_t BD, int64_t c, int k, int step) {
   float accA[kVec], accV[kVec], carry[kVec];
   int kk[kVec];
@@ -95,78 +111,127 @@ __device__ __forceinline__ f4 look_back(const uint64_t* status, int64_t BD, int6
   return f4{{carry[0], carry[1], carry[2], carry[3]}};
 }
 
+// Load one run of rows. hb/gb are tile base pointers (wave-uniform), off is
+// this thread's first element relative to them, ld the row stride; all
+// offsets inside a tile fit in 32 bits. Rows at or past T (and channels past
+// Di) read as gate = -inf, hidden = 0, which the gate math turns into the
+// identity step. Full runs (all but the tail of the sequence) load unmasked.
+template <typename Tin, int kRows>
+__device__ __forceinline__ void load_run(const Tin* hb, const Tin* gb, int off, int ld, bool ok, int nrows,
+                                         f4 (&hv)[kRows], f4 (&gv)[kRows]) {
+  if (ok && nrows >= kRows) {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      hv[i] = io4<Tin>::load(hb + (off + i * ld));
+      gv[i] = io4<Tin>::load(gb + (off + i * ld));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const bool live = ok && i < nrows;
+      hv[i] = live ? io4<Tin>::load(hb + (off + i * ld)) : io4<Tin>::fill(0.0f);
+      gv[i] = live ? io4<Tin>::load(gb + (off + i * ld)) : io4<Tin>::fill(-INFINITY);
+    }
+  }
+}
+
+template <typename Tg, int kRows>
+__device__ __forceinline__ void load_grad(const Tg* pb, int off, int ld, bool ok, int nrows, f4 (&dv)[kRows]) {
+  if (ok && nrows >= kRows) {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) dv[i] = io4<Tg>::load(pb + (off + i * ld));
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+      dv[i] = (ok && i < nrows) ? io4<Tg>::load(pb + (off + i * ld)) : io4<Tg>::fill(0.0f);
+  }
+}
+
+// Run maps of one tile in LDS, double-buffered for the scan across runs.
+template <int kSubs>
+struct RunMaps {
+  f4 A[2][kSubs][kChLanes];
+  f4 V[2][kSubs][kChLanes];
+};
+
+// Inclusive scan of the affine run maps (h -> A h + V) across the kSubs runs
+// of a tile, Hillis-Steele over LDS with one barrier per doubling step. The
+// forward scan composes earlier runs first; the reverse scan (backward pass)
+// composes later runs first. Both use (A, V) <- (A A', A V' + V) with the
+// partner's map (A', V'). Returns the buffer holding the inclusive maps.
+template <int kSubs, bool kReverse>
+__device__ __forceinline__ int scan_runs(RunMaps<kSubs>& m, int s, int cl, f4 A, f4 V) {
+  int buf = 0;
+  m.A[0][s][cl] = A;
+  m.V[0][s][cl] = V;
+  __syncthreads();
+#pragma unroll
+  for (int o = 1; o < kSubs; o <<= 1) {
+    const int src = kReverse ? s + o : s - o;
+    if (kReverse ? src < kSubs : src >= 0) {
+      const f4 pa = m.A[buf][src][cl], pv = m.V[buf][src][cl];
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        V.v[j] = A.v[j] * pv.v[j] + V.v[j];
+        A.v[j] = A.v[j] * pa.v[j];
+      }
+    }
+    buf ^= 1;
+    m.A[buf][s][cl] = A;
+    m.V[buf][s][cl] = V;
+    __syncthreads();
+  }
+  return buf;
+}
+
 // ------------------------------------------------------------------ forward
 
 template <typename Tin, typename Tout>
-__global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
+__global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
     const float* __restrict__ h0, Tout* __restrict__ hout, int64_t out_sb, int64_t out_ld,
-    float* __restrict__ h_last, float* __restrict__ ckpt, Geometry g,
-    uint32_t* __restrict__ counter, uint64_t* __restrict__ status) {
+    float* __restrict__ h_last, Geometry g, uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
+  constexpr int kSubs = kFwdSubs, kRows = kFwdRows;
   __shared__ uint32_t s_ticket;
-  __shared__ f4 s_A[kSubs][kChLanes];
-  __shared__ f4 s_V[kSubs][kChLanes];
+  __shared__ RunMaps<kSubs> s_maps;
   __shared__ f4 s_carry[kChLanes];
 
   const int tid = threadIdx.x;
   const int cl = tid % kChLanes;
   const int s = tid / kChLanes;
-  if (tid == 0) s_ticket = atomicAdd(counter, 1u);
-  __syncthreads();
-  int k, b, d;
-  tile_coords(g, s_ticket, false, k, b, d);
+  int k, b, d0;
+  take_tile(g, counters, &s_ticket, false, k, b, d0);
+  const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
-  const int t0 = k * kTileRows + s * kSubRows;
+  const int t0 = k * kFwdTileRows + s * kRows;
   const int64_t c = static_cast<int64_t>(b) * g.Di + d;
+  const int ild = static_cast<int>(in_ld), old = static_cast<int>(out_ld);
+  const int64_t in_tile = b * in_sb + static_cast<int64_t>(k) * kFwdTileRows * in_ld + d0;
 
-  // Load the run (all loads issued before any math).
-  f4 hv[kSubRows] = {}, gv[kSubRows] = {};
-  const Tin* hp = hidden + b * in_sb + static_cast<int64_t>(t0) * in_ld + d;
-  const Tin* gp = gate + b * in_sb + static_cast<int64_t>(t0) * in_ld + d;
-#pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
-    if (ok && t0 + i < g.T) {
-      hv[i] = io4<Tin>::load(hp + i * in_ld);
-      gv[i] = io4<Tin>::load(gp + i * in_ld);
-    }
-  }
+  f4 hv[kRows], gv[kRows];
+  load_run<Tin, kRows>(hidden + in_tile, gate + in_tile, s * kRows * ild + cl * kVec, ild, ok, g.T - t0, hv, gv);
 
-  // a_t, v_t = z_t g(hidden_t); rows past T are the identity map.
-  float a[kSubRows][kVec], v[kSubRows][kVec];
+  float a[kRows][kVec], v[kRows][kVec];
   f4 A, V;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) { A.v[j] = 1.0f; V.v[j] = 0.0f; }
 #pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
-    const bool live = ok && t0 + i < g.T;
+  for (int i = 0; i < kRows; ++i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      float aa, zz;
-      gate_coeffs(gv[i].v[j], aa, zz);
-      a[i][j] = live ? aa : 1.0f;
-      v[i][j] = live ? zz * g_tilde(hv[i].v[j]) : 0.0f;
+      fwd_coeffs(gv[i].v[j], hv[i].v[j], a[i][j], v[i][j]);
       V.v[j] = a[i][j] * V.v[j] + v[i][j];
       A.v[j] = A.v[j] * a[i][j];
     }
   }
-  s_A[s][cl] = A;
-  s_V[s][cl] = V;
-  __syncthreads();
+  const int buf = scan_runs<kSubs, false>(s_maps, s, cl, A, V);
 
   if (s == 0 && ok) {
-    f4 TA, TV;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) { TA.v[j] = 1.0f; TV.v[j] = 0.0f; }
-    for (int q = 0; q < kSubs; ++q) {
-      const f4 qa = s_A[q][cl], qv = s_V[q][cl];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) { TV.v[j] = qa.v[j] * TV.v[j] + qv.v[j]; TA.v[j] *= qa.v[j]; }
-    }
+    const f4 TA = s_maps.A[buf][kSubs - 1][cl], TV = s_maps.V[buf][kSubs - 1][cl];
     uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c;
     f4 carry;
     if (k == 0) {
-      if (h0) carry = io4<float>::load(h0 + c);
-      else { for (int j = 0; j < kVec; ++j) carry.v[j] = 0.0f; }
+      carry = h0 ? io4<float>::load(h0 + c) : io4<float>::fill(0.0f);
     } else {
 #pragma unroll
       for (int j = 0; j < kVec; ++j) publish_agg(st + j, TA.v[j], TV.v[j]);
@@ -177,158 +242,109 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(
       for (int j = 0; j < kVec; ++j) publish_incl(st + j, TA.v[j] * carry.v[j] + TV.v[j]);
     }
     s_carry[cl] = carry;
-    if (ckpt) io4<float>::store(ckpt + static_cast<int64_t>(k) * g.BD + c, carry);
   }
   __syncthreads();
   if (!ok) return;
 
-  // State entering this run, then replay it.
   f4 h = s_carry[cl];
-  for (int q = 0; q < s; ++q) {
-    const f4 qa = s_A[q][cl], qv = s_V[q][cl];
+  if (s > 0) {
+    const f4 pa = s_maps.A[buf][s - 1][cl], pv = s_maps.V[buf][s - 1][cl];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) h.v[j] = qa.v[j] * h.v[j] + qv.v[j];
+    for (int j = 0; j < kVec; ++j) h.v[j] = pa.v[j] * h.v[j] + pv.v[j];
   }
-  Tout* op = hout + b * out_sb + static_cast<int64_t>(t0) * out_ld + d;
+  Tout* ob = hout + (b * out_sb + static_cast<int64_t>(k) * kFwdTileRows * out_ld + d0);
+  const int out_off = s * kRows * old + cl * kVec;
 #pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
+  for (int i = 0; i < kRows; ++i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) h.v[j] = a[i][j] * h.v[j] + v[i][j];
-    if (t0 + i < g.T) io4<Tout>::store(op + i * out_ld, h);
+    if (t0 + i < g.T) io4<Tout>::store(ob + (out_off + i * old), h);
     if (h_last && t0 + i == g.T - 1) io4<float>::store(h_last + c, h);
   }
 }
 
 // ------------------------------------------------------------------ backward
 
-template <typename Tin, typename Tg>
-__global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
+template <typename Tin, typename Th>
+__global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
-    const float* __restrict__ ckpt, const Tg* __restrict__ dh, int64_t g_sb, int64_t g_ld,
-    const float* __restrict__ dh_last, Tin* __restrict__ dhidden, Tin* __restrict__ dgate,
-    float* __restrict__ dh0, Geometry g, uint32_t* __restrict__ counter,
-    uint64_t* __restrict__ status) {
+    const float* __restrict__ h0, const Th* __restrict__ hout, int64_t out_sb, int64_t out_ld,
+    const Th* __restrict__ dh, int64_t g_sb, int64_t g_ld, const float* __restrict__ dh_last,
+    Tin* __restrict__ dhidden, Tin* __restrict__ dgate, float* __restrict__ dh0, Geometry g,
+    uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
+  constexpr int kSubs = kBwdSubs, kRows = kBwdRows;
   __shared__ uint32_t s_ticket;
-  __shared__ f4 s_A[kSubs][kChLanes];
-  __shared__ f4 s_V[kSubs][kChLanes];
+  __shared__ RunMaps<kSubs> s_maps;
   __shared__ f4 s_carry[kChLanes];
 
   const int tid = threadIdx.x;
   const int cl = tid % kChLanes;
   const int s = tid / kChLanes;
-  if (tid == 0) s_ticket = atomicAdd(counter, 1u);
-  __syncthreads();
-  int k, b, d;
-  tile_coords(g, s_ticket, true, k, b, d);
+  int k, b, d0;
+  take_tile(g, counters, &s_ticket, true, k, b, d0);
+  const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
-  const int t0 = k * kTileRows + s * kSubRows;
+  const int t0 = k * kBwdTileRows + s * kRows;
   const int64_t c = static_cast<int64_t>(b) * g.Di + d;
+  const int ild = static_cast<int>(in_ld), gld = static_cast<int>(g_ld);
+  const int64_t in_tile = b * in_sb + static_cast<int64_t>(k) * kBwdTileRows * in_ld + d0;
+  const int in_off = s * kRows * ild + cl * kVec;
 
-  f4 hv[kSubRows] = {}, gv[kSubRows] = {}, dv[kSubRows] = {};
-  const int64_t in_off = b * in_sb + static_cast<int64_t>(t0) * in_ld + d;
-  const Tin* hp = hidden + in_off;
-  const Tin* gp = gate + in_off;
-  const Tg* dp = dh + b * g_sb + static_cast<int64_t>(t0) * g_ld + d;
-#pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
-    if (ok && t0 + i < g.T) {
-      hv[i] = io4<Tin>::load(hp + i * in_ld);
-      gv[i] = io4<Tin>::load(gp + i * in_ld);
-      dv[i] = io4<Tg>::load(dp + i * g_ld);
-    }
+  f4 hv[kRows], gv[kRows], dv[kRows];
+  load_run<Tin, kRows>(hidden + in_tile, gate + in_tile, in_off, ild, ok, g.T - t0, hv, gv);
+  load_grad<Th, kRows>(dh + (b * g_sb + static_cast<int64_t>(k) * kBwdTileRows * g_ld + d0),
+                       s * kRows * gld + cl * kVec, gld, ok, g.T - t0, dv);
+  // h_{t0-1}: the forward output of the row before the run (h0 or 0 at t = 0).
+  f4 hc = io4<float>::fill(0.0f);
+  if (ok && t0 < g.T) {
+    if (t0 > 0) hc = io4<Th>::load(hout + (b * out_sb + static_cast<int64_t>(t0 - 1) * out_ld + d));
+    else if (h0) hc = io4<float>::load(h0 + c);
   }
-  f4 hc = {};  // state entering the tile (saved by the forward)
-  if (ok) hc = io4<float>::load(ckpt + static_cast<int64_t>(k) * g.BD + c);
-  if (ok && dh_last && t0 <= g.T - 1 && g.T - 1 < t0 + kSubRows) {
+  if (ok && dh_last && t0 <= g.T - 1 && g.T - 1 < t0 + kRows) {
     const f4 dl = io4<float>::load(dh_last + c);
-    const int i = g.T - 1 - t0;
 #pragma unroll
-    for (int ii = 0; ii < kSubRows; ++ii)
-      if (ii == i) {
+    for (int i = 0; i < kRows; ++i)
+      if (t0 + i == g.T - 1) {
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) dv[ii].v[j] += dl.v[j];
+        for (int j = 0; j < kVec; ++j) dv[i].v[j] += dl.v[j];
       }
   }
 
-  // Per element: a (recurrence coefficient), v = z g~ (forward input),
-  // z, q = z g'(hidden), gh (incoming gradient). v and z are folded into
-  // dgate's factor once h_{t-1} is known.
-  float a[kSubRows][kVec], v[kSubRows][kVec], z[kSubRows][kVec], q[kSubRows][kVec], gh[kSubRows][kVec];
-  f4 A, V;
+  // Per element: a, q = z g'(hidden) (dhidden's factor) and
+  // p = a z (g~ - h_{t-1}) (dgate's factor), with h_{t-1} rebuilt along the
+  // run in fp32.
+  float a[kRows][kVec], q[kRows][kVec], p[kRows][kVec];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) { A.v[j] = 1.0f; V.v[j] = 0.0f; }
-#pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
-    const bool live = ok && t0 + i < g.T;
+  for (int i = 0; i < kRows; ++i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      float aa, zz, gt, gp_;
-      gate_coeffs(gv[i].v[j], aa, zz);
-      g_tilde_grad(hv[i].v[j], gt, gp_);
-      a[i][j] = live ? aa : 1.0f;
-      z[i][j] = live ? zz : 0.0f;
-      v[i][j] = live ? zz * gt : 0.0f;
-      q[i][j] = live ? zz * gp_ : 0.0f;
-      gh[i][j] = live ? dv[i].v[j] : 0.0f;
-      V.v[j] = a[i][j] * V.v[j] + v[i][j];
-      A.v[j] = A.v[j] * a[i][j];
-    }
-  }
-  s_A[s][cl] = A;
-  s_V[s][cl] = V;
-  __syncthreads();
-
-  // Rebuild h_{t-1} for the run; keep dgate's factor a z (g~ - h_{t-1})
-  // = a (v - z h_{t-1}) in v.
-  if (ok) {
-    for (int qq = 0; qq < s; ++qq) {
-      const f4 qa = s_A[qq][cl], qv = s_V[qq][cl];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) hc.v[j] = qa.v[j] * hc.v[j] + qv.v[j];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kSubRows; ++i) {
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const float hprev = hc.v[j];
-      hc.v[j] = a[i][j] * hprev + v[i][j];
-      v[i][j] = a[i][j] * (v[i][j] - z[i][j] * hprev);
+      float zz, vv;
+      bwd_coeffs(gv[i].v[j], hv[i].v[j], a[i][j], zz, vv, q[i][j]);
+      p[i][j] = a[i][j] * (vv - zz * hc.v[j]);
+      hc.v[j] = a[i][j] * hc.v[j] + vv;
     }
   }
 
-  // Reverse run map mu -> A mu + M with mu_t = a_t lambda_t,
-  // lambda_t = gh_t + mu_{t+1}.
-  f4 M;
+  // Reverse run map mu -> A mu + M, mu_t = a_t lambda_t, lambda_t = gh_t + mu_{t+1}.
+  f4 A, M;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) { A.v[j] = 1.0f; M.v[j] = 0.0f; }
 #pragma unroll
-  for (int i = kSubRows - 1; i >= 0; --i) {
+  for (int i = kRows - 1; i >= 0; --i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      M.v[j] = a[i][j] * (gh[i][j] + M.v[j]);
+      M.v[j] = a[i][j] * (dv[i].v[j] + M.v[j]);
       A.v[j] = A.v[j] * a[i][j];
     }
   }
-  __syncthreads();  // forward run maps no longer needed
-  s_A[s][cl] = A;
-  s_V[s][cl] = M;
-  __syncthreads();
+  const int buf = scan_runs<kSubs, true>(s_maps, s, cl, A, M);
 
   if (s == 0 && ok) {
-    f4 TA, TM;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) { TA.v[j] = 1.0f; TM.v[j] = 0.0f; }
-    for (int qq = kSubs - 1; qq >= 0; --qq) {
-      const f4 qa = s_A[qq][cl], qm = s_V[qq][cl];
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) { TM.v[j] = qa.v[j] * TM.v[j] + qm.v[j]; TA.v[j] *= qa.v[j]; }
-    }
+    const f4 TA = s_maps.A[buf][0][cl], TM = s_maps.V[buf][0][cl];
     uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c;
     f4 carry;
     if (k == g.ntiles - 1) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) carry.v[j] = 0.0f;
+      carry = io4<float>::fill(0.0f);
     } else {
 #pragma unroll
       for (int j = 0; j < kVec; ++j) publish_agg(st + j, TA.v[j], TM.v[j]);
@@ -344,26 +360,26 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(
   if (!ok) return;
 
   f4 mu = s_carry[cl];
-  for (int qq = kSubs - 1; qq > s; --qq) {
-    const f4 qa = s_A[qq][cl], qm = s_V[qq][cl];
+  if (s + 1 < kSubs) {
+    const f4 pa = s_maps.A[buf][s + 1][cl], pm = s_maps.V[buf][s + 1][cl];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) mu.v[j] = qa.v[j] * mu.v[j] + qm.v[j];
+    for (int j = 0; j < kVec; ++j) mu.v[j] = pa.v[j] * mu.v[j] + pm.v[j];
   }
-  Tin* dhp = dhidden + in_off;
-  Tin* dgp = dgate + in_off;
+  Tin* dhb = dhidden + in_tile;
+  Tin* dgb = dgate + in_tile;
 #pragma unroll
-  for (int i = kSubRows - 1; i >= 0; --i) {
+  for (int i = kRows - 1; i >= 0; --i) {
     f4 og, oh;
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float lam = gh[i][j] + mu.v[j];
-      og.v[j] = lam * v[i][j];
+      const float lam = dv[i].v[j] + mu.v[j];
+      og.v[j] = lam * p[i][j];
       oh.v[j] = lam * q[i][j];
       mu.v[j] = a[i][j] * lam;
     }
     if (t0 + i < g.T) {
-      io4<Tin>::store(dgp + i * in_ld, og);
-      io4<Tin>::store(dhp + i * in_ld, oh);
+      io4<Tin>::store(dgb + (in_off + i * ild), og);
+      io4<Tin>::store(dhb + (in_off + i * ild), oh);
     }
   }
   if (dh0 && t0 == 0) io4<float>::store(dh0 + c, mu);
@@ -377,26 +393,38 @@ __global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {
     p[i] = make_uint4(0, 0, 0, 0);
 }
 
-inline size_t ws_bytes(int B, int T, int Di) {
-  const int nt = (T + kTileRows - 1) / kTileRows;
-  return kWsHeader + static_cast<size_t>(nt) * B * Di * sizeof(uint64_t);
-}
-
-inline int check_common(const char* fn, int B, int T, int Di, void* ws, size_t ws_size,
-                        Geometry& g) {
-  if (B < 1 || T < 1 || Di < 4) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
-  if (Di % kVec) return fail(MG_ERR_ARG, "%s: Di=%d must be a multiple of 4", fn, Di);
-  const size_t need = ws_bytes(B, T, Di);
-  if (!ws || ws_size < need)
-    return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, ws_size, need);
-  if (!aligned(ws, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
+inline void make_geometry(int B, int T, int Di, int tile_rows, Geometry& g) {
   g.B = B; g.T = T; g.Di = Di;
   g.nblk_d = (Di + kTileCh - 1) / kTileCh;
   g.ncb = B * g.nblk_d;
-  g.ntiles = (T + kTileRows - 1) / kTileRows;
+  g.tile_rows = tile_rows;
+  g.ntiles = (T + tile_rows - 1) / tile_rows;
   g.BD = static_cast<int64_t>(B) * Di;
+}
+
+inline size_t ws_bytes(const Geometry& g) {
+  return ws_header_bytes(g.ncb) + static_cast<size_t>(g.ntiles) * g.BD * sizeof(uint64_t);
+}
+
+// One workspace size serves both directions.
+inline size_t ws_bytes_any(int B, int T, int Di) {
+  Geometry f, b;
+  make_geometry(B, T, Di, kFwdTileRows, f);
+  make_geometry(B, T, Di, kBwdTileRows, b);
+  return std::max(ws_bytes(f), ws_bytes(b));
+}
+
+inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, void* ws, size_t ws_size,
+                        Geometry& g) {
+  if (B < 1 || T < 1 || Di < 4) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
+  if (Di % kVec) return fail(MG_ERR_ARG, "%s: Di=%d must be a multiple of 4", fn, Di);
+  make_geometry(B, T, Di, tile_rows, g);
   const int64_t nblocks = static_cast<int64_t>(g.ncb) * g.ntiles;
   if (nblocks > 0x7fffffff) return fail(MG_ERR_ARG, "%s: problem too large (%lld tiles)", fn, (long long)nblocks);
+  const size_t need = ws_bytes(g);
+  if (!ws || ws_size < need)
+    return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, ws_size, need);
+  if (!aligned(ws, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
   return MG_OK;
 }
 
@@ -406,6 +434,9 @@ inline int check_tensor(const char* fn, const char* name, const void* p, int dty
   if (sb % kVec || ld % kVec || sb < 0 || ld < 0)
     return fail(MG_ERR_ARG, "%s: %s strides (%lld, %lld) must be non-negative multiples of 4", fn, name,
                 (long long)sb, (long long)ld);
+  // offsets inside one tile are 32-bit
+  if (static_cast<int64_t>(std::max(kFwdTileRows, kBwdTileRows)) * ld + kTileCh > 0x7fffffffLL)
+    return fail(MG_ERR_ARG, "%s: %s row stride %lld too large", fn, name, (long long)ld);
   if (!aligned(p, dtype == MG_F32 ? 16 : 8)) return fail(MG_ERR_ARG, "%s: %s misaligned", fn, name);
   return MG_OK;
 }
@@ -416,32 +447,36 @@ inline int check_f32vec(const char* fn, const char* name, const void* p) {
 }
 
 inline void zero_ws(void* ws, const Geometry& g, hipStream_t st) {
-  const int64_t n16 = static_cast<int64_t>(ws_bytes(g.B, g.T, g.Di) / 16);
+  const int64_t n16 = static_cast<int64_t>(ws_bytes(g) / 16);
   const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
   hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, st, static_cast<uint4*>(ws), n16);
 }
 
-template <typename Tin, typename Tout>
-void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0, void* h,
-                int64_t out_sb, int64_t out_ld, float* h_last, float* ckpt, const Geometry& g, void* ws,
-                hipStream_t st) {
-  auto* counter = static_cast<uint32_t*>(ws);
-  auto* status = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsHeader);
-  hipLaunchKernelGGL((scan_fwd_kernel<Tin, Tout>), dim3(g.ncb * g.ntiles), dim3(kThreads), 0, st,
-                     static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
-                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, counter, status);
+inline uint32_t* ws_counters(void* ws) { return static_cast<uint32_t*>(ws); }
+inline uint64_t* ws_status(void* ws, const Geometry& g) {
+  return reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + ws_header_bytes(g.ncb));
 }
 
-template <typename Tin, typename Tg>
-void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* ckpt,
-                const void* dh, int64_t g_sb, int64_t g_ld, const float* dh_last, void* dhidden, void* dgate,
-                float* dh0, const Geometry& g, void* ws, hipStream_t st) {
-  auto* counter = static_cast<uint32_t*>(ws);
-  auto* status = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsHeader);
-  hipLaunchKernelGGL((scan_bwd_kernel<Tin, Tg>), dim3(g.ncb * g.ntiles), dim3(kThreads), 0, st,
-                     static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, ckpt,
-                     static_cast<const Tg*>(dh), g_sb, g_ld, dh_last, static_cast<Tin*>(dhidden),
-                     static_cast<Tin*>(dgate), dh0, g, counter, status);
+template <typename Tin, typename Tout>
+void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0, void* h,
+                int64_t out_sb, int64_t out_ld, float* h_last, const Geometry& g, void* ws, hipStream_t st) {
+  zero_ws(ws, g, st);
+  hipLaunchKernelGGL((scan_fwd_kernel<Tin, Tout>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kFwdSubs), 0, st,
+                     static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
+                     static_cast<Tout*>(h), out_sb, out_ld, h_last, g, ws_counters(ws), ws_status(ws, g));
+}
+
+template <typename Tin, typename Th>
+void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0,
+                const void* h, int64_t out_sb, int64_t out_ld, const void* dh, int64_t g_sb, int64_t g_ld,
+                const float* dh_last, void* dhidden, void* dgate, float* dh0, const Geometry& g, void* ws,
+                hipStream_t st) {
+  zero_ws(ws, g, st);
+  hipLaunchKernelGGL((scan_bwd_kernel<Tin, Th>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kBwdSubs), 0, st,
+                     static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
+                     static_cast<const Th*>(h), out_sb, out_ld, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
+                     static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), dh0, g, ws_counters(ws),
+                     ws_status(ws, g));
 }
 
 }  // namespace scan
@@ -449,67 +484,65 @@ void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_
 
 using namespace mg;
 
-extern "C" int mg_scan_num_tiles(int T) { return T < 1 ? 0 : (T + scan::kTileRows - 1) / scan::kTileRows; }
-
 extern "C" size_t mg_scan_workspace_bytes(int B, int T, int Di) {
-  if (B < 1 || T < 1 || Di < 1) return scan::kWsHeader;
-  return scan::ws_bytes(B, T, Di);
+  if (B < 1 || T < 1 || Di < 1) return 256;
+  return scan::ws_bytes_any(B, T, Di);
 }
 
 extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
                            const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
-                           float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+                           float* h_last, int B, int T, int Di, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   const char* fn = "mg_scan_fwd";
   scan::Geometry g;
   int rc;
-  if ((rc = scan::check_common(fn, B, T, Di, workspace, workspace_bytes, g))) return rc;
+  if ((rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, workspace, workspace_bytes, g))) return rc;
   if ((rc = scan::check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "h_last", h_last))) return rc;
-  if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  scan::zero_ws(workspace, g, st);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
-    scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
+    scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
   else if (in_dtype == MG_F32 && out_dtype == MG_F32)
-    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
+    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
   else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
-    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
+    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
   else
     return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
   return check_launch(fn);
 }
 
 extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
-                           const float* h0, const float* ckpt, int g_dtype, const void* dh, int64_t g_sb,
-                           int64_t g_ld, const float* dh_last, void* dhidden, void* dgate, float* dh0, int B,
-                           int T, int Di, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)h0;  // the entry state of tile 0 (h0 or 0) is already in ckpt
+                           const float* h0, int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
+                           const void* dh, int64_t g_sb, int64_t g_ld, const float* dh_last, void* dhidden,
+                           void* dgate, float* dh0, int B, int T, int Di, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   const char* fn = "mg_scan_bwd";
   scan::Geometry g;
   int rc;
-  if ((rc = scan::check_common(fn, B, T, Di, workspace, workspace_bytes, g))) return rc;
+  if ((rc = scan::check_common(fn, B, T, Di, scan::kBwdTileRows, workspace, workspace_bytes, g))) return rc;
   if ((rc = scan::check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "dh", dh, g_dtype, g_sb, g_ld))) return rc;
+  if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
+  if ((rc = scan::check_tensor(fn, "dh", dh, out_dtype, g_sb, g_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dhidden", dhidden, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dgate", dgate, in_dtype, in_sb, in_ld))) return rc;
-  if (!ckpt) return fail(MG_ERR_ARG, "%s: ckpt is NULL (run mg_scan_fwd with ckpt first)", fn);
-  if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
+  if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh_last", dh_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh0", dh0))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  scan::zero_ws(workspace, g, st);
-  if (in_dtype == MG_BF16 && g_dtype == MG_BF16)
-    scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, ckpt, dh, g_sb, g_ld, dh_last, dhidden, dgate, dh0, g, workspace, st);
-  else if (in_dtype == MG_F32 && g_dtype == MG_F32)
-    scan::launch_bwd<float, float>(hidden, gate, in_sb, in_ld, ckpt, dh, g_sb, g_ld, dh_last, dhidden, dgate, dh0, g, workspace, st);
-  else if (in_dtype == MG_BF16 && g_dtype == MG_F32)
-    scan::launch_bwd<bf16_t, float>(hidden, gate, in_sb, in_ld, ckpt, dh, g_sb, g_ld, dh_last, dhidden, dgate, dh0, g, workspace, st);
+  if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
+    scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+                                     dhidden, dgate, dh0, g, workspace, st);
+  else if (in_dtype == MG_F32 && out_dtype == MG_F32)
+    scan::launch_bwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+                                   dhidden, dgate, dh0, g, workspace, st);
+  else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
+    scan::launch_bwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+                                    dhidden, dgate, dh0, g, workspace, st);
   else
-    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d g_dtype=%d unsupported", fn, in_dtype, g_dtype);
+    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
   return check_launch(fn);
 }

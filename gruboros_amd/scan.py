@@ -23,38 +23,37 @@ def _prep_h0(h0, B, Di, device):
     return h0.reshape(B, Di).to(device=device, dtype=torch.float32).contiguous()
 
 
-def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt):
+def _launch_fwd(hidden, gate, h0, out_dtype):
     B, T, Di = hidden.shape
     L = lib()
     h = torch.empty(B, T, Di, dtype=out_dtype, device=hidden.device)
     h_last = torch.empty(B, 1, Di, dtype=torch.float32, device=hidden.device)
-    nt = L.mg_scan_num_tiles(T)
-    ckpt = torch.empty(nt, B, Di, dtype=torch.float32, device=hidden.device) if need_ckpt else None
     wsb = L.mg_scan_workspace_bytes(B, T, Di)
     ws = torch.empty(wsb, dtype=torch.uint8, device=hidden.device)
     rc = L.mg_scan_fwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
-                       ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last), ptr(ckpt),
+                       ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last),
                        B, T, Di, ptr(ws), wsb, stream_of(hidden))
     check(rc, "mg_scan_fwd")
-    return h, h_last, ckpt
+    return h, h_last
 
 
-def _launch_bwd(hidden, gate, h0, ckpt, dh, dh_last, dhidden, dgate, want_dh0, out_dtype):
+def _launch_bwd(hidden, gate, h0, h, dh, dh_last, dhidden, dgate, want_dh0):
     B, T, Di = hidden.shape
     L = lib()
     dev = hidden.device
     if dh is None:
-        dh = torch.zeros(B, T, Di, dtype=out_dtype, device=dev)
-    elif not _vec_ok(dh) or dh.dtype not in (torch.float32, torch.bfloat16):
-        dh = dh.contiguous()
+        dh = torch.zeros(B, T, Di, dtype=h.dtype, device=dev)
+    elif dh.dtype != h.dtype or not _vec_ok(dh):
+        dh = dh.to(h.dtype).contiguous()
     if dh_last is not None:
         dh_last = dh_last.reshape(B, Di).to(torch.float32).contiguous()
     dh0 = torch.empty(B, 1, Di, dtype=torch.float32, device=dev) if want_dh0 else None
     wsb = L.mg_scan_workspace_bytes(B, T, Di)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
-                       ptr(h0), ptr(ckpt), dtype_code(dh.dtype), ptr(dh), dh.stride(0), dh.stride(1),
-                       ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0), B, T, Di, ptr(ws), wsb, stream_of(hidden))
+                       ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1),
+                       ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0),
+                       B, T, Di, ptr(ws), wsb, stream_of(hidden))
     check(rc, "mg_scan_bwd")
     return dh0
 
@@ -73,21 +72,20 @@ class GateScanPacked(torch.autograd.Function):
         B, T, D2 = hg.shape
         Di = D2 // 2
         hidden, gate = hg[..., :Di], hg[..., Di:]
-        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hg.dtype, need_ckpt=True)
-        ctx.save_for_backward(hg, h0, ckpt)
+        h, h_last = _launch_fwd(hidden, gate, h0, hg.dtype)
+        ctx.save_for_backward(hg, h0, h)
         return h, h_last
 
     @staticmethod
     def backward(ctx, dh, dh_last):
-        hg, h0, ckpt = ctx.saved_tensors
+        hg, h0, h = ctx.saved_tensors
         B, T, D2 = hg.shape
         Di = D2 // 2
         if dh is None and dh_last is None:
             return None, None
         dhg = torch.empty_like(hg, memory_format=torch.contiguous_format)
         want_dh0 = h0 is not None and ctx.needs_input_grad[1]
-        dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, ckpt, dh, dh_last, dhg[..., :Di], dhg[..., Di:],
-                          want_dh0, hg.dtype)
+        dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, h, dh, dh_last, dhg[..., :Di], dhg[..., Di:], want_dh0)
         return dhg, (dh0.reshape(h0.shape) if want_dh0 else None)
 
 
@@ -97,13 +95,13 @@ class GateScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, gate, h0):
         ctx.set_materialize_grads(False)
-        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hidden.dtype, need_ckpt=True)
-        ctx.save_for_backward(hidden, gate, h0, ckpt)
+        h, h_last = _launch_fwd(hidden, gate, h0, hidden.dtype)
+        ctx.save_for_backward(hidden, gate, h0, h)
         return h, h_last
 
     @staticmethod
     def backward(ctx, dh, dh_last):
-        hidden, gate, h0, ckpt = ctx.saved_tensors
+        hidden, gate, h0, h = ctx.saved_tensors
         if dh is None and dh_last is None:
             return None, None, None
         # inputs are contiguous (gate_scan ensures it), so the gradients,
@@ -111,7 +109,7 @@ class GateScan(torch.autograd.Function):
         dhidden = torch.empty_like(hidden)
         dgate = torch.empty_like(gate)
         want_dh0 = h0 is not None and ctx.needs_input_grad[2]
-        dh0 = _launch_bwd(hidden, gate, h0, ckpt, dh, dh_last, dhidden, dgate, want_dh0, hidden.dtype)
+        dh0 = _launch_bwd(hidden, gate, h0, h, dh, dh_last, dhidden, dgate, want_dh0)
         return dhidden, dgate, (dh0.reshape(h0.shape) if want_dh0 else None)
 
 

@@ -62,38 +62,37 @@ const char* mg_last_error(void);
  *   are passed as hidden = base, gate = base + Di, in_ld = 2*Di,
  *   in_sb = T*2*Di.
  * Requirements: Di % 4 == 0, strides % 4 == 0, pointers 8-byte aligned
- *   (bf16) or 16-byte aligned (fp32).
- * ckpt (nullable): fp32 [mg_scan_num_tiles(T), B, Di]; receives the state
- *   entering each time tile. mg_scan_bwd needs it.
+ *   (bf16) or 16-byte aligned (fp32), 128 * row stride < 2^31.
  * h_last (nullable): fp32 [B, Di], receives h_{T-1}.
+ * Supported (in_dtype, out_dtype): (BF16, BF16), (F32, F32), (BF16, F32).
  * ---------------------------------------------------------------------- */
-int mg_scan_num_tiles(int T);
-size_t mg_scan_workspace_bytes(int B, int T, int Di);
+size_t mg_scan_workspace_bytes(int B, int T, int Di);  /* serves fwd and bwd */
 
 int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
                 const float* h0,
                 int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
-                float* h_last, float* ckpt,
+                float* h_last,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
 
-/* Backward of mg_scan_fwd (autograd of reference mingru/minGRU.py:16-20,
- * :53-69 through gate and hidden; the closed form is
- *   lambda_t = dh_t + a_{t+1} lambda_{t+1},
+/* Backward of mg_scan_fwd: autograd of reference mingru/minGRU.py:16-20,
+ * :53-69 through gate, hidden and prev_hidden, in closed form:
+ *   lambda_t  = dh_t + a_{t+1} lambda_{t+1},
  *   dgate_t   = lambda_t z_t (1 - z_t) (g(hidden_t) - h_{t-1}),
  *   dhidden_t = lambda_t z_t g'(hidden_t)   (g'(0) = 0, as relu'(0) = 0),
- *   dh0       = a_0 lambda_0).
- * h_{t-1} is recomputed in fp32 from ckpt (written by mg_scan_fwd with the
- * same B, T, Di, hidden, gate, h0); the forward output is not read.
- * dh: element (b,t,d) at b*g_sb + t*g_ld + d, dtype out_dtype of the forward.
+ *   dh0       = a_0 lambda_0.
+ * h: the forward's output (same layout, dtype out_dtype); h_{t-1} is read
+ * from it once per 4-step run and rebuilt in fp32 inside the run.
+ * dh: gradient of h, dtype out_dtype, element (b,t,d) at b*g_sb + t*g_ld + d.
  * dh_last (nullable): fp32 [B, Di], gradient of h_last, added to dh_{T-1}.
  * dhidden/dgate: same layout and dtype as hidden/gate (in_sb, in_ld).
  * dh0 (nullable): fp32 [B, Di]. */
 int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
-                const float* h0, const float* ckpt,
-                int g_dtype, const void* dh, int64_t g_sb, int64_t g_ld,
+                const float* h0,
+                int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
+                const void* dh, int64_t g_sb, int64_t g_ld,
                 const float* dh_last,
                 void* dhidden, void* dgate, float* dh0,
                 int B, int T, int Di,

@@ -40,16 +40,15 @@ def test_every_declared_symbol_is_exported(L):
 
 def test_version_and_queries(L):
     assert L.mg_version() >= 100
-    assert L.mg_scan_num_tiles(1) == 1
-    assert L.mg_scan_num_tiles(128) == 1
-    assert L.mg_scan_num_tiles(129) == 2
-    # header + one 8-byte look-back word per (tile, channel)
-    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + 3 * 2 * 64 * 8
+    # per-chain ticket counters (rounded to 256 B) + one 8-byte look-back word per
+    # (tile, channel), for the direction with the shorter tiles (64 steps)
+    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + 5 * 2 * 64 * 8
+    assert L.mg_scan_workspace_bytes(16, 8192, 2048) == 2048 + 128 * 16 * 2048 * 8
 
 
 def _fwd(L, **kw):
     args = dict(in_dtype=1, hidden=16, gate=16, in_sb=1024, in_ld=64, h0=None, out_dtype=1, h=16, out_sb=512,
-                out_ld=64, h_last=None, ckpt=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
+                out_ld=64, h_last=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
     args.update(kw)
     return L.mg_scan_fwd(*args.values())
 
