@@ -89,12 +89,12 @@ def bench_scan(reps=20, B=16, T=8192, Di=2048):
     n = B * T * Di
 
     def fwd():
-        return _launch_fwd(hidden, gate, h0, torch.bfloat16)
+        return _launch_fwd(hidden, gate, h0, torch.bfloat16, need_ckpt=True)
 
-    h, _ = fwd()
+    h, _, ckpt = fwd()
 
     def bwd():
-        _launch_bwd(hidden, gate, h0, h, dh, None, dhid, dgat, True)
+        _launch_bwd(hidden, gate, h0, h, ckpt, dh, None, dhid, dgat, True)
 
     for _ in range(3):
         fwd()

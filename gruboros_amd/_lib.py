@@ -22,10 +22,21 @@ SIGNATURES = {
     "mg_version": (_c_int, []),
     "mg_last_error": (ctypes.c_char_p, []),
     "mg_scan_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
-    "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp,
+    "mg_scan_ckpt_elems": (_c_size, [_c_int, _c_int, _c_int]),
+    "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
                              _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
-    "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64,
+    "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp,
                              _vp, _c_i64, _c_i64, _fp, _vp, _vp, _fp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
+    "mg_add_rmsnorm_fwd": (_c_int, [_fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int,
+                                    ctypes.c_float, _vp]),
+    "mg_add_rmsnorm_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int]),
+    "mg_add_rmsnorm_bwd": (_c_int, [_fp, _fp, _fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int, _vp,
+                                    _c_size, _vp]),
+    "mg_cross_entropy_partials": (_c_int, [_c_i64]),
+    "mg_cross_entropy_fwd_bwd": (_c_int, [_c_int, _vp, _vp, _c_int, _vp, _fp, _vp, _c_i64, _c_int, ctypes.c_float,
+                                          _vp]),
+    "mg_sf_adamw_chunk_elems": (_c_i64, []),
+    "mg_sf_adamw_step": (_c_int, [_vp, _c_int, _c_i64] + [ctypes.c_float] * 8 + [_vp]),
 }
 
 _LIB = None

@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <type_traits>
+
 #include "mingru_hip.h"
 
 namespace mg {
@@ -44,39 +46,85 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
-// Four consecutive channels, loaded/stored as one vector access.
-struct f4 { float v[4]; };
+// N consecutive channels of one row, loaded/stored as one vector access
+// (N = 4: 8-byte bf16 / 16-byte fp32; N = 8: 16-byte bf16 / 2 x 16-byte fp32).
+template <int N>
+struct fv {
+  float v[N];
+};
+using f4 = fv<4>;
 
-template <typename T> struct io4;
+template <typename T, int N> struct iov;
 
-template <> struct io4<float> {
-  __device__ __forceinline__ static f4 fill(float x) { return f4{{x, x, x, x}}; }
-  __device__ __forceinline__ static f4 load(const float* p) {
-    float4 x = *reinterpret_cast<const float4*>(p);
-    return f4{{x.x, x.y, x.z, x.w}};
+template <int N> struct iov<float, N> {
+  static_assert(N % 4 == 0, "fp32 vectors are multiples of float4");
+  __device__ __forceinline__ static fv<N> fill(float x) {
+    fv<N> r;
+#pragma unroll
+    for (int j = 0; j < N; ++j) r.v[j] = x;
+    return r;
   }
-  __device__ __forceinline__ static void store(float* p, const f4& a) {
-    *reinterpret_cast<float4*>(p) = make_float4(a.v[0], a.v[1], a.v[2], a.v[3]);
+  __device__ __forceinline__ static fv<N> load(const float* p) {
+    fv<N> r;
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const float4 x = reinterpret_cast<const float4*>(p)[q];
+      r.v[4 * q] = x.x; r.v[4 * q + 1] = x.y; r.v[4 * q + 2] = x.z; r.v[4 * q + 3] = x.w;
+    }
+    return r;
+  }
+  __device__ __forceinline__ static void store(float* p, const fv<N>& a) {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q)
+      reinterpret_cast<float4*>(p)[q] = make_float4(a.v[4 * q], a.v[4 * q + 1], a.v[4 * q + 2], a.v[4 * q + 3]);
+  }
+  // Streaming store (non-temporal hint): for outputs no later kernel step rereads soon.
+  __device__ __forceinline__ static void store_nt(float* p, const fv<N>& a) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) __builtin_nontemporal_store(a.v[j], p + j);
   }
 };
 
-template <> struct io4<bf16_t> {
-  __device__ __forceinline__ static f4 fill(float x) {
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+template <int N> struct iov<bf16_t, N> {
+  static_assert(N == 4 || N == 8, "bf16 vectors are 8 or 16 bytes");
+  using raw = typename std::conditional<N == 4, uint2, uint4>::type;
+  __device__ __forceinline__ static fv<N> fill(float x) {
     const float r = bf16_to_f32(f32_to_bf16(x));
-    return f4{{r, r, r, r}};
+    fv<N> o;
+#pragma unroll
+    for (int j = 0; j < N; ++j) o.v[j] = r;
+    return o;
   }
-  __device__ __forceinline__ static f4 load(const bf16_t* p) {
-    uint2 x = *reinterpret_cast<const uint2*>(p);
-    return f4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
-               __uint_as_float(x.y << 16), __uint_as_float(x.y & 0xffff0000u)}};
+  __device__ __forceinline__ static fv<N> load(const bf16_t* p) {
+    const raw x = *reinterpret_cast<const raw*>(p);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&x);
+    fv<N> o;
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) {
+      o.v[2 * q] = __uint_as_float(w[q] << 16);
+      o.v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+    }
+    return o;
   }
-  __device__ __forceinline__ static void store(bf16_t* p, const f4& a) {
-    uint2 x;
-    x.x = static_cast<uint32_t>(f32_to_bf16(a.v[0])) | (static_cast<uint32_t>(f32_to_bf16(a.v[1])) << 16);
-    x.y = static_cast<uint32_t>(f32_to_bf16(a.v[2])) | (static_cast<uint32_t>(f32_to_bf16(a.v[3])) << 16);
-    *reinterpret_cast<uint2*>(p) = x;
+  __device__ __forceinline__ static void store(bf16_t* p, const fv<N>& a) {
+    raw x;
+    uint32_t* w = reinterpret_cast<uint32_t*>(&x);
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) w[q] = pack_bf16x2(a.v[2 * q], a.v[2 * q + 1]);
+    *reinterpret_cast<raw*>(p) = x;
+  }
+  __device__ __forceinline__ static void store_nt(bf16_t* p, const fv<N>& a) {
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q)
+      __builtin_nontemporal_store(pack_bf16x2(a.v[2 * q], a.v[2 * q + 1]), reinterpret_cast<uint32_t*>(p) + q);
   }
 };
+
+template <typename T> using io4 = iov<T, 4>;
 
 // ---------------------------------------------------------------- gate math
 //

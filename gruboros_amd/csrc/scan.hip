@@ -21,8 +21,11 @@
 //     block) takes tickets from its own atomic counter, so a tile only ever
 //     waits on tiles of its chain that were started before it.
 //   * The backward walks tiles in reverse time order with the adjoint
-//     recurrence. It needs h_{t-1}: it reads the forward output once per run
-//     (the row before the run) and rebuilds the run's states in fp32 from it.
+//     recurrence. It needs h_{t-1}: it reads the state entering each 4-step
+//     run once (the forward's fp32 checkpoint when the output is bf16, else
+//     the fp32 output itself) and rebuilds the run's states in fp32 from it.
+//     (A bf16-rounded state would not do: at small gates dgate depends on
+//     g(hidden) - h_{t-1}, a difference of two nearly equal numbers.)
 
 #include <algorithm>
 
@@ -45,6 +48,10 @@ constexpr int kTileCh = kChLanes * kVec;  // 64 channels per tile
 constexpr int kFwdSubs = 16, kFwdRows = 8;
 constexpr int kBwdSubs = MG_SCAN_BWD_SUBS, kBwdRows = MG_SCAN_BWD_ROWS;
 constexpr int kFwdTileRows = kFwdSubs * kFwdRows;
+// fp32 state checkpoints (optional forward output, backward input): the state
+// after every kCkptRows-th step, i.e. the state entering each backward run.
+constexpr int kCkptRows = 4;
+static_assert(kBwdRows == kCkptRows && kFwdRows % kCkptRows == 0, "checkpoint spacing");
 constexpr int kBwdTileRows = kBwdSubs * kBwdRows;
 
 struct Geometry {
@@ -190,7 +197,8 @@ template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
     const float* __restrict__ h0, Tout* __restrict__ hout, int64_t out_sb, int64_t out_ld,
-    float* __restrict__ h_last, Geometry g, uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
+    float* __restrict__ h_last, float* __restrict__ ckpt, Geometry g, uint32_t* __restrict__ counters,
+    uint64_t* __restrict__ status) {
   constexpr int kSubs = kFwdSubs, kRows = kFwdRows;
   __shared__ uint32_t s_ticket;
   __shared__ RunMaps<kSubs> s_maps;
@@ -258,8 +266,10 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
   for (int i = 0; i < kRows; ++i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) h.v[j] = a[i][j] * h.v[j] + v[i][j];
-    if (t0 + i < g.T) io4<Tout>::store(ob + (out_off + i * old), h);
+    if (t0 + i < g.T) io4<Tout>::store_nt(ob + (out_off + i * old), h);
     if (h_last && t0 + i == g.T - 1) io4<float>::store(h_last + c, h);
+    if (ckpt && (i + 1) % kCkptRows == 0 && t0 + i < g.T)
+      io4<float>::store(ckpt + static_cast<int64_t>((t0 + i) / kCkptRows) * g.BD + c, h);
   }
 }
 
@@ -269,7 +279,8 @@ template <typename Tin, typename Th>
 __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
     const float* __restrict__ h0, const Th* __restrict__ hout, int64_t out_sb, int64_t out_ld,
-    const Th* __restrict__ dh, int64_t g_sb, int64_t g_ld, const float* __restrict__ dh_last,
+    const float* __restrict__ ckpt, const Th* __restrict__ dh, int64_t g_sb, int64_t g_ld,
+    const float* __restrict__ dh_last,
     Tin* __restrict__ dhidden, Tin* __restrict__ dgate, float* __restrict__ dh0, Geometry g,
     uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
   constexpr int kSubs = kBwdSubs, kRows = kBwdRows;
@@ -294,11 +305,15 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   load_run<Tin, kRows>(hidden + in_tile, gate + in_tile, in_off, ild, ok, g.T - t0, hv, gv);
   load_grad<Th, kRows>(dh + (b * g_sb + static_cast<int64_t>(k) * kBwdTileRows * g_ld + d0),
                        s * kRows * gld + cl * kVec, gld, ok, g.T - t0, dv);
-  // h_{t0-1}: the forward output of the row before the run (h0 or 0 at t = 0).
+  // h_{t0-1}: the fp32 checkpoint when given, else the forward output of the
+  // row before the run (exact for fp32 outputs); h0 (or 0) at t = 0.
   f4 hc = io4<float>::fill(0.0f);
   if (ok && t0 < g.T) {
-    if (t0 > 0) hc = io4<Th>::load(hout + (b * out_sb + static_cast<int64_t>(t0 - 1) * out_ld + d));
-    else if (h0) hc = io4<float>::load(h0 + c);
+    if (t0 > 0)
+      hc = ckpt ? io4<float>::load(ckpt + static_cast<int64_t>(t0 / kCkptRows - 1) * g.BD + c)
+                : io4<Th>::load(hout + (b * out_sb + static_cast<int64_t>(t0 - 1) * out_ld + d));
+    else if (h0)
+      hc = io4<float>::load(h0 + c);
   }
   if (ok && dh_last && t0 <= g.T - 1 && g.T - 1 < t0 + kRows) {
     const f4 dl = io4<float>::load(dh_last + c);
@@ -378,8 +393,8 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
       mu.v[j] = a[i][j] * lam;
     }
     if (t0 + i < g.T) {
-      io4<Tin>::store(dgb + (in_off + i * ild), og);
-      io4<Tin>::store(dhb + (in_off + i * ild), oh);
+      io4<Tin>::store_nt(dgb + (in_off + i * ild), og);
+      io4<Tin>::store_nt(dhb + (in_off + i * ild), oh);
     }
   }
   if (dh0 && t0 == 0) io4<float>::store(dh0 + c, mu);
@@ -459,22 +474,24 @@ inline uint64_t* ws_status(void* ws, const Geometry& g) {
 
 template <typename Tin, typename Tout>
 void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0, void* h,
-                int64_t out_sb, int64_t out_ld, float* h_last, const Geometry& g, void* ws, hipStream_t st) {
+                int64_t out_sb, int64_t out_ld, float* h_last, float* ckpt, const Geometry& g, void* ws,
+                hipStream_t st) {
   zero_ws(ws, g, st);
   hipLaunchKernelGGL((scan_fwd_kernel<Tin, Tout>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kFwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
-                     static_cast<Tout*>(h), out_sb, out_ld, h_last, g, ws_counters(ws), ws_status(ws, g));
+                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_counters(ws), ws_status(ws, g));
 }
 
 template <typename Tin, typename Th>
 void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0,
-                const void* h, int64_t out_sb, int64_t out_ld, const void* dh, int64_t g_sb, int64_t g_ld,
+                const void* h, int64_t out_sb, int64_t out_ld, const float* ckpt, const void* dh, int64_t g_sb,
+                int64_t g_ld,
                 const float* dh_last, void* dhidden, void* dgate, float* dh0, const Geometry& g, void* ws,
                 hipStream_t st) {
   zero_ws(ws, g, st);
   hipLaunchKernelGGL((scan_bwd_kernel<Tin, Th>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kBwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
-                     static_cast<const Th*>(h), out_sb, out_ld, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
+                     static_cast<const Th*>(h), out_sb, out_ld, ckpt, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
                      static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), dh0, g, ws_counters(ws),
                      ws_status(ws, g));
 }
@@ -484,6 +501,11 @@ void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_
 
 using namespace mg;
 
+extern "C" size_t mg_scan_ckpt_elems(int B, int T, int Di) {
+  if (B < 1 || T < 1 || Di < 1) return 0;
+  return static_cast<size_t>((T + scan::kCkptRows - 1) / scan::kCkptRows) * B * Di;
+}
+
 extern "C" size_t mg_scan_workspace_bytes(int B, int T, int Di) {
   if (B < 1 || T < 1 || Di < 1) return 256;
   return scan::ws_bytes_any(B, T, Di);
@@ -491,8 +513,8 @@ extern "C" size_t mg_scan_workspace_bytes(int B, int T, int Di) {
 
 extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
                            const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
-                           float* h_last, int B, int T, int Di, void* workspace, size_t workspace_bytes,
-                           void* stream) {
+                           float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   const char* fn = "mg_scan_fwd";
   scan::Geometry g;
   int rc;
@@ -502,13 +524,14 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "h_last", h_last))) return rc;
+  if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
-    scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
+    scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
   else if (in_dtype == MG_F32 && out_dtype == MG_F32)
-    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
+    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
   else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
-    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, g, workspace, st);
+    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
   else
     return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
   return check_launch(fn);
@@ -516,7 +539,8 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
 
 extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
                            const float* h0, int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
-                           const void* dh, int64_t g_sb, int64_t g_ld, const float* dh_last, void* dhidden,
+                           const float* ckpt, const void* dh, int64_t g_sb, int64_t g_ld, const float* dh_last,
+                           void* dhidden,
                            void* dgate, float* dh0, int B, int T, int Di, void* workspace,
                            size_t workspace_bytes, void* stream) {
   const char* fn = "mg_scan_bwd";
@@ -532,15 +556,16 @@ extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh_last", dh_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh0", dh0))) return rc;
+  if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
-    scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+    scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
                                      dhidden, dgate, dh0, g, workspace, st);
   else if (in_dtype == MG_F32 && out_dtype == MG_F32)
-    scan::launch_bwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+    scan::launch_bwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
                                    dhidden, dgate, dh0, g, workspace, st);
   else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
-    scan::launch_bwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, dh, g_sb, g_ld, dh_last,
+    scan::launch_bwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
                                     dhidden, dgate, dh0, g, workspace, st);
   else
     return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);

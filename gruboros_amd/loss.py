@@ -1,0 +1,68 @@
+"""Loss head: logits projection + mean cross-entropy (reference
+mingru/minLM.py:138, :146-149), with the log-softmax, the loss and the
+logits gradient computed in one pass by mg_cross_entropy_fwd_bwd.
+"""
+import torch
+
+from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
+from .linear import _mm_f32, bf16_copy
+
+
+def _ce(logits2d, labels1d, grad_dtype):
+    N, V = logits2d.shape
+    L = lib()
+    P = L.mg_cross_entropy_partials(N)
+    dl = torch.empty(N, V, dtype=grad_dtype, device=logits2d.device)
+    part = torch.empty(P, dtype=torch.float32, device=logits2d.device)
+    rc = L.mg_cross_entropy_fwd_bwd(dtype_code(logits2d.dtype), ptr(logits2d), ptr(labels1d), dtype_code(grad_dtype),
+                                    ptr(dl), ptr(part), None, N, V, 1.0 / N, stream_of(logits2d))
+    check(rc, "mg_cross_entropy_fwd_bwd")
+    return part.sum() / N, dl
+
+
+class LogitsCrossEntropy(torch.autograd.Function):
+    """mean_n CE(embed_n @ W^T, label_n); embed bf16 [N, D], W fp32 master [V, D]."""
+
+    @staticmethod
+    def forward(ctx, embed, w, wb, labels):
+        logits = _mm_f32(embed, wb.t())               # [N, V] fp32
+        loss, dl = _ce(logits, labels, torch.bfloat16)
+        ctx.save_for_backward(embed, wb, dl)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        embed, wb, dl = ctx.saved_tensors
+        dl = dl * g  # upstream gradient (1/grad_accum in the reference loop); stays bf16
+        de = torch.mm(dl, wb) if ctx.needs_input_grad[0] else None
+        dw = _mm_f32(dl.t(), embed) if ctx.needs_input_grad[1] else None
+        return de, dw, None, None
+
+
+class CrossEntropyFromLogits(torch.autograd.Function):
+    """mean_n CE(logits_n, label_n) for fp32 logits [N, V] (the fp32 path)."""
+
+    @staticmethod
+    def forward(ctx, logits, labels):
+        loss, dl = _ce(logits, labels, torch.float32)
+        ctx.save_for_backward(dl)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        (dl,) = ctx.saved_tensors
+        return dl * g, None
+
+
+def logits_cross_entropy(embed, to_logits, labels):
+    """Mean cross-entropy of to_logits(embed) against labels (int64), like
+    F.cross_entropy(logits.transpose(1, 2), labels) in the reference."""
+    require_cuda(embed, labels)
+    D = embed.shape[-1]
+    e2 = embed.reshape(-1, D)
+    lab = labels.reshape(-1).contiguous()
+    w = to_logits.weight
+    if embed.dtype == torch.bfloat16 and w.dtype == torch.float32:
+        return LogitsCrossEntropy.apply(e2.contiguous(), w, bf16_copy(w), lab)
+    logits = torch.nn.functional.linear(e2, w)
+    return CrossEntropyFromLogits.apply(logits.float().contiguous(), lab)

@@ -11,6 +11,7 @@ import torch
 import torch.nn.functional as F
 from torch.nn import Identity, Linear, Module
 
+from ..linear import linear as _linear
 from ..scan import gate_scan_packed
 
 
@@ -39,18 +40,6 @@ def g(x):
 def log_g(x):
     """Reference mingru/minGRU.py:27-28."""
     return torch.where(x >= 0, (F.relu(x) + 0.5).log(), -F.softplus(-x))
-
-
-def _linear(x, layer):
-    """Linear in the activation dtype: fp32 master weights are cast per call
-    (autograd returns their gradients in fp32)."""
-    w = layer.weight
-    if w.dtype != x.dtype:
-        w = w.to(x.dtype)
-    b = layer.bias
-    if b is not None and b.dtype != x.dtype:
-        b = b.to(x.dtype)
-    return F.linear(x, w, b)
 
 
 class minGRU(Module):

@@ -17,9 +17,10 @@ import torch.nn.functional as F
 from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
-from .minGRU import minGRU, _linear
-
-FP32_EPS = float(torch.finfo(torch.float32).eps)
+from ..linear import linear as _linear
+from ..loss import logits_cross_entropy
+from ..norm import add_rms_norm, rms_norm
+from .minGRU import minGRU
 
 
 def exists(v):
@@ -56,13 +57,6 @@ class CausalDepthWiseConv1d(Module):
         x = F.pad(x, (self.kernel_size - 1, 0), value=0.)
         x = self.net(x)
         return x.transpose(1, 2)
-
-
-def _rms_norm(x, norm, out_dtype):
-    """RMSNorm with the fp32 epsilon whatever the activation dtype
-    (torch.nn.RMSNorm(dim) in the reference, eps=None -> finfo(fp32).eps)."""
-    y = F.rms_norm(x.float(), (x.shape[-1],), norm.weight.float(), eps=FP32_EPS)
-    return y.to(out_dtype)
 
 
 def _ff(x, ff):
@@ -111,45 +105,70 @@ class minLM(Module):
         """Reference mingru/minLM.py:86-155."""
         if return_loss:
             x, labels = x[:, :-1], x[:, 1:]
-        x = self.token_emb(x)
-        cd = default(self.compute_dtype, x.dtype)
-        x = x.float()  # fp32 residual stream
-
         if exists(prev_hiddens) and not return_loss:
-            x = x[:, -1:]
+            x = x[:, -1:]  # single-step decoding (reference :101-102; per-token ops commute with the slice)
 
-        next_prev_hiddens = []
-        prev_hiddens = iter(default(prev_hiddens, []))
-
-        for conv, norm, mingru, ff_norm, ff, dropout in self.layers:
-            if exists(conv):
-                assert len(list(prev_hiddens)) == 0, 'caching not supported for conv version'
-                x = conv(x) + x
-
-            prev_hidden = next(prev_hiddens, None)
-            min_gru_out, next_prev_hidden = mingru(_rms_norm(x, norm, cd), prev_hidden,
-                                                   return_next_prev_hidden=True)
-            x = min_gru_out.float() + x
-            next_prev_hiddens.append(next_prev_hidden)
-
-            x = _ff(_rms_norm(x, ff_norm, cd), ff).float() + x
-
-            if exists(dropout):
-                x = dropout(x)
-
-        embed = _rms_norm(x, self.norm, cd)
-        logits = _linear(embed, self.to_logits)
+        embed, next_prev_hiddens = self._trunk(x, prev_hiddens)
 
         if not return_loss:
+            logits = _linear(embed, self.to_logits)
             if not return_prev_hiddens:
                 return logits
             return logits, next_prev_hiddens
 
-        loss = F.cross_entropy(logits.float().transpose(1, 2), labels)
+        # reference: F.cross_entropy(to_logits(embed).transpose(1, 2), labels)
+        loss = logits_cross_entropy(embed, self.to_logits, labels)
 
         if not return_prev_hiddens:
             return loss
         return loss, next_prev_hiddens
+
+    def logits_and_hiddens(self, ids, prev_hiddens=None):
+        """Logits for every position of `ids` and the next prev_hiddens
+        (reference mingru/minLM.py:97-138, the body shared by all forward modes)."""
+        embed, hiddens = self._trunk(ids, prev_hiddens)
+        return _linear(embed, self.to_logits), hiddens
+
+    def _trunk(self, ids, prev_hiddens):
+        """Embedding, blocks and final norm (reference :97-137): (embed, next_prev_hiddens)."""
+        x = self.token_emb(ids)
+        cd = default(self.compute_dtype, x.dtype)
+        x = x.float()  # fp32 residual stream
+
+        next_prev_hiddens = []
+        prev_hiddens = iter(default(prev_hiddens, []))
+
+        # Pre-norm blocks with each residual add fused into the norm that
+        # follows it (reference :107-135): n is the normalized input of the
+        # next branch, x the fp32 residual stream, pending the branch output
+        # still to be added to x.
+        n = None
+        pending = None
+        for conv, norm, mingru, ff_norm, ff, dropout in self.layers:
+            if exists(conv):
+                if pending is not None:
+                    x, pending = x + pending.float(), None
+                x = conv(x) + x
+            if pending is None:
+                n = rms_norm(x, norm.weight, cd)
+            else:
+                x, n = add_rms_norm(x, pending, norm.weight, cd)
+
+            prev_hidden = next(prev_hiddens, None)
+            min_gru_out, next_prev_hidden = mingru(n, prev_hidden, return_next_prev_hidden=True)
+            next_prev_hiddens.append(next_prev_hidden)
+
+            x, n2 = add_rms_norm(x, min_gru_out, ff_norm.weight, cd)
+            pending = _ff(n2, ff)
+
+            if exists(dropout):
+                x, pending = dropout(x + pending.float()), None
+
+        if pending is None:
+            embed = rms_norm(x, self.norm.weight, cd)
+        else:
+            _, embed = add_rms_norm(x, pending, self.norm.weight, cd)
+        return embed, next_prev_hiddens
 
     def _initialize_weights(self):
         """Reference mingru/minLM.py:157-206: N(0, 0.02/sqrt(dim)) for the embedding,

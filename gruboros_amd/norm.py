@@ -1,0 +1,108 @@
+"""Autograd Functions over the fused residual-add + RMSNorm kernels
+(mg_add_rmsnorm_fwd / mg_add_rmsnorm_bwd).
+
+Reference semantics: torch.nn.RMSNorm(dim) as used by mingru/minLM.py:67,
+:69, :74 (eps=None -> float32 machine epsilon) and the residual adds at
+mingru/minLM.py:125 and :130. The residual stream is kept in fp32; the
+normalized output is produced in the activation dtype.
+"""
+import torch
+
+from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
+
+FP32_EPS = float(torch.finfo(torch.float32).eps)
+
+
+def _rows(t):
+    D = t.shape[-1]
+    return t.numel() // D, D
+
+
+def _fwd(x, delta, w, out_dtype):
+    N, D = _rows(x)
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    rstd = torch.empty(N, dtype=torch.float32, device=x.device)
+    x_out = torch.empty_like(x) if delta is not None else None
+    rc = lib().mg_add_rmsnorm_fwd(ptr(x), dtype_code(delta.dtype) if delta is not None else 0, ptr(delta), ptr(w),
+                                  ptr(x_out), dtype_code(out_dtype), ptr(y), ptr(rstd), N, D, FP32_EPS,
+                                  stream_of(x))
+    check(rc, "mg_add_rmsnorm_fwd")
+    return x_out, y, rstd
+
+
+def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta):
+    N, D = _rows(xn)
+    dev = xn.device
+    if dy is None:
+        dy = torch.zeros(xn.shape, dtype=torch.float32, device=dev)
+    elif not dy.is_contiguous():
+        dy = dy.contiguous()
+    if dres is not None:
+        dres = dres.to(torch.float32).contiguous()
+    dx = torch.empty(xn.shape, dtype=torch.float32, device=dev) if want_dx else None
+    ddelta = torch.empty(xn.shape, dtype=delta_dtype, device=dev) if want_ddelta else None
+    dw = torch.empty(D, dtype=torch.float32, device=dev)
+    L = lib()
+    wsb = L.mg_add_rmsnorm_bwd_workspace_bytes(N, D)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    rc = L.mg_add_rmsnorm_bwd(ptr(xn), ptr(w), ptr(rstd), dtype_code(dy.dtype), ptr(dy), ptr(dres), ptr(dx),
+                              dtype_code(delta_dtype) if want_ddelta else 0, ptr(ddelta), ptr(dw), N, D,
+                              ptr(ws), wsb, stream_of(xn))
+    check(rc, "mg_add_rmsnorm_bwd")
+    return dx, ddelta, dw
+
+
+class RMSNormFn(torch.autograd.Function):
+    """y = x * w / sqrt(mean(x^2) + eps) over the last dim; x fp32, y in out_dtype."""
+
+    @staticmethod
+    def forward(ctx, x, w, out_dtype):
+        _, y, rstd = _fwd(x, None, w, out_dtype)
+        ctx.save_for_backward(x, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, rstd = ctx.saved_tensors
+        dx, _, dw = _bwd(x, w, rstd, dy, None, ctx.needs_input_grad[0], None, False)
+        return dx, (dw if ctx.needs_input_grad[1] else None), None
+
+
+class AddRMSNormFn(torch.autograd.Function):
+    """(x + delta, rmsnorm(x + delta) * w): the residual add fused with the next norm."""
+
+    @staticmethod
+    def forward(ctx, x, delta, w, out_dtype):
+        x_out, y, rstd = _fwd(x, delta, w, out_dtype)
+        ctx.save_for_backward(x_out, w, rstd)
+        ctx.delta_dtype = delta.dtype
+        return x_out, y
+
+    @staticmethod
+    def backward(ctx, dx_out, dy):
+        xn, w, rstd = ctx.saved_tensors
+        want_dx, want_dd = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dx, dd, dw = _bwd(xn, w, rstd, dy, dx_out, want_dx, ctx.delta_dtype, want_dd)
+        return dx, dd, (dw if ctx.needs_input_grad[2] else None), None
+
+
+def _check(x, w, delta=None):
+    require_cuda(x, w, delta)
+    if x.dtype != torch.float32:
+        raise ValueError(f"the residual stream must be float32, got {x.dtype}")
+    if w.dtype != torch.float32 or w.dim() != 1 or w.shape[0] != x.shape[-1]:
+        raise ValueError(f"weight must be float32 [{x.shape[-1]}], got {w.dtype} {tuple(w.shape)}")
+    if delta is not None and delta.shape != x.shape:
+        raise ValueError(f"delta {tuple(delta.shape)} must match x {tuple(x.shape)}")
+
+
+def rms_norm(x, w, out_dtype=None):
+    """RMSNorm of an fp32 tensor over its last dim with fp32 epsilon; output in out_dtype."""
+    _check(x, w)
+    return RMSNormFn.apply(x.contiguous(), w, out_dtype or x.dtype)
+
+
+def add_rms_norm(x, delta, w, out_dtype=None):
+    """Returns (x + delta, rms_norm(x + delta, w)); x fp32, delta fp32 or bf16."""
+    _check(x, w, delta)
+    return AddRMSNormFn.apply(x.contiguous(), delta.contiguous(), w, out_dtype or x.dtype)

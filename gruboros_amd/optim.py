@@ -16,8 +16,14 @@ c = weight_k / sum(weight), weight_k = (k+1)^r * lr_max^weight_lr_power:
     z   <- z - lr u
 eval() moves p to x = (y - (1 - b1) z) / b1 and train() moves it back,
 exactly as the package's mode switch does.
+
+step() runs the whole update as one mg_sf_adamw_step launch (all parameter
+tensors, one pass over p, g, z, v), which also refreshes the bf16 copies of
+the weights used by the bf16 linear layers (gruboros_amd.linear).
 """
 import torch
+
+from ._lib import check, lib, require_cuda, stream_of
 
 
 class AdamWScheduleFree(torch.optim.Optimizer):
@@ -70,29 +76,38 @@ class AdamWScheduleFree(torch.optim.Optimizer):
             group["weight_sum"] = group["weight_sum"] + weight
             ckp1 = weight / group["weight_sum"] if group["weight_sum"] != 0 else 0.0
             y_lr = lr * (b1 * (1 - ckp1) - 1)
-            ps, gs, zs, vs = [], [], [], []
+            rows, keep = [], []
+            chunk = lib().mg_sf_adamw_chunk_elems()
+            nchunks = 0
             for p in group["params"]:
                 if p.grad is None:
                     continue
+                require_cuda(p)
+                if p.dtype != torch.float32 or not p.is_contiguous():
+                    raise TypeError("AdamWScheduleFree: parameters must be contiguous float32")
                 st = self.state[p]
                 if "z" not in st:
                     st["z"] = p.detach().clone(memory_format=torch.preserve_format)
                     st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                ps.append(p)
-                gs.append(p.grad)
-                zs.append(st["z"])
-                vs.append(st["exp_avg_sq"])
-            if ps:
-                torch._foreach_mul_(vs, b2)
-                torch._foreach_addcmul_(vs, gs, gs, value=1 - b2)
-                denom = torch._foreach_div(vs, bc2)
-                torch._foreach_sqrt_(denom)
-                torch._foreach_add_(denom, group["eps"])
-                u = torch._foreach_div(gs, denom)
-                if group["weight_decay"] != 0:
-                    torch._foreach_add_(u, ps, alpha=group["weight_decay"])
-                torch._foreach_lerp_(ps, zs, ckp1)
-                torch._foreach_add_(ps, u, alpha=y_lr)
-                torch._foreach_sub_(zs, u, alpha=lr)
+                g = p.grad if (p.grad.is_contiguous() and p.grad.dtype == torch.float32) else \
+                    p.grad.float().contiguous()
+                keep.append(g)  # a converted copy must outlive the enqueue below
+                pb = 0
+                cache = getattr(p, "_mg_bf16", None)
+                if cache is not None and cache[0] == p._version and cache[1].shape == p.shape:
+                    pb = cache[1].data_ptr()
+                n = p.numel()
+                rows.append([p.data_ptr(), g.data_ptr(), st["z"].data_ptr(), st["exp_avg_sq"].data_ptr(), pb, n,
+                             nchunks])
+                nchunks += (n + chunk - 1) // chunk
+            if rows:
+                dev = group["params"][0].device
+                host = torch.tensor(rows, dtype=torch.int64).pin_memory()
+                table = host.to(dev, non_blocking=True)
+                rc = lib().mg_sf_adamw_step(table.data_ptr(), len(rows), nchunks, b2, 1 - b2, bc2, group["eps"],
+                                            group["weight_decay"], ckp1, y_lr, lr,
+                                            stream_of(group["params"][0]))
+                check(rc, "mg_sf_adamw_step")
+            del keep
             group["k"] = k + 1
         return loss

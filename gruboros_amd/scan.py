@@ -23,21 +23,27 @@ def _prep_h0(h0, B, Di, device):
     return h0.reshape(B, Di).to(device=device, dtype=torch.float32).contiguous()
 
 
-def _launch_fwd(hidden, gate, h0, out_dtype):
+def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt=False):
+    """Runs mg_scan_fwd; returns (h, h_last, ckpt). ckpt (fp32 states every 4
+    steps) is produced when asked for and h is not fp32: the backward needs
+    fp32 states."""
     B, T, Di = hidden.shape
     L = lib()
     h = torch.empty(B, T, Di, dtype=out_dtype, device=hidden.device)
     h_last = torch.empty(B, 1, Di, dtype=torch.float32, device=hidden.device)
+    ckpt = None
+    if need_ckpt and out_dtype != torch.float32:
+        ckpt = torch.empty(L.mg_scan_ckpt_elems(B, T, Di), dtype=torch.float32, device=hidden.device)
     wsb = L.mg_scan_workspace_bytes(B, T, Di)
     ws = torch.empty(wsb, dtype=torch.uint8, device=hidden.device)
     rc = L.mg_scan_fwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
-                       ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last),
+                       ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last), ptr(ckpt),
                        B, T, Di, ptr(ws), wsb, stream_of(hidden))
     check(rc, "mg_scan_fwd")
-    return h, h_last
+    return h, h_last, ckpt
 
 
-def _launch_bwd(hidden, gate, h0, h, dh, dh_last, dhidden, dgate, want_dh0):
+def _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0):
     B, T, Di = hidden.shape
     L = lib()
     dev = hidden.device
@@ -51,7 +57,7 @@ def _launch_bwd(hidden, gate, h0, h, dh, dh_last, dhidden, dgate, want_dh0):
     wsb = L.mg_scan_workspace_bytes(B, T, Di)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
-                       ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1),
+                       ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1), ptr(ckpt),
                        ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0),
                        B, T, Di, ptr(ws), wsb, stream_of(hidden))
     check(rc, "mg_scan_bwd")
@@ -72,20 +78,21 @@ class GateScanPacked(torch.autograd.Function):
         B, T, D2 = hg.shape
         Di = D2 // 2
         hidden, gate = hg[..., :Di], hg[..., Di:]
-        h, h_last = _launch_fwd(hidden, gate, h0, hg.dtype)
-        ctx.save_for_backward(hg, h0, h)
+        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hg.dtype, need_ckpt=True)
+        ctx.save_for_backward(hg, h0, h, ckpt)
         return h, h_last
 
     @staticmethod
     def backward(ctx, dh, dh_last):
-        hg, h0, h = ctx.saved_tensors
+        hg, h0, h, ckpt = ctx.saved_tensors
         B, T, D2 = hg.shape
         Di = D2 // 2
         if dh is None and dh_last is None:
             return None, None
         dhg = torch.empty_like(hg, memory_format=torch.contiguous_format)
         want_dh0 = h0 is not None and ctx.needs_input_grad[1]
-        dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, h, dh, dh_last, dhg[..., :Di], dhg[..., Di:], want_dh0)
+        dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, h, ckpt, dh, dh_last, dhg[..., :Di], dhg[..., Di:],
+                          want_dh0)
         return dhg, (dh0.reshape(h0.shape) if want_dh0 else None)
 
 
@@ -95,13 +102,13 @@ class GateScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, gate, h0):
         ctx.set_materialize_grads(False)
-        h, h_last = _launch_fwd(hidden, gate, h0, hidden.dtype)
-        ctx.save_for_backward(hidden, gate, h0, h)
+        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hidden.dtype, need_ckpt=True)
+        ctx.save_for_backward(hidden, gate, h0, h, ckpt)
         return h, h_last
 
     @staticmethod
     def backward(ctx, dh, dh_last):
-        hidden, gate, h0, h = ctx.saved_tensors
+        hidden, gate, h0, h, ckpt = ctx.saved_tensors
         if dh is None and dh_last is None:
             return None, None, None
         # inputs are contiguous (gate_scan ensures it), so the gradients,
@@ -109,7 +116,7 @@ class GateScan(torch.autograd.Function):
         dhidden = torch.empty_like(hidden)
         dgate = torch.empty_like(gate)
         want_dh0 = h0 is not None and ctx.needs_input_grad[2]
-        dh0 = _launch_bwd(hidden, gate, h0, h, dh, dh_last, dhidden, dgate, want_dh0)
+        dh0 = _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0)
         return dhidden, dgate, (dh0.reshape(h0.shape) if want_dh0 else None)
 
 

@@ -64,15 +64,19 @@ const char* mg_last_error(void);
  * Requirements: Di % 4 == 0, strides % 4 == 0, pointers 8-byte aligned
  *   (bf16) or 16-byte aligned (fp32), 128 * row stride < 2^31.
  * h_last (nullable): fp32 [B, Di], receives h_{T-1}.
+ * ckpt (nullable): fp32 [ceil(T/4), B, Di]; ckpt[j] receives h_{4j+3}, the
+ *   state entering step 4j+4. mg_scan_bwd reads it instead of h when h is
+ *   bf16 (required there for fp32-accurate gradients).
  * Supported (in_dtype, out_dtype): (BF16, BF16), (F32, F32), (BF16, F32).
  * ---------------------------------------------------------------------- */
+size_t mg_scan_ckpt_elems(int B, int T, int Di);
 size_t mg_scan_workspace_bytes(int B, int T, int Di);  /* serves fwd and bwd */
 
 int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
                 const float* h0,
                 int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
-                float* h_last,
+                float* h_last, float* ckpt,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
 
@@ -82,8 +86,9 @@ int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
  *   dgate_t   = lambda_t z_t (1 - z_t) (g(hidden_t) - h_{t-1}),
  *   dhidden_t = lambda_t z_t g'(hidden_t)   (g'(0) = 0, as relu'(0) = 0),
  *   dh0       = a_0 lambda_0.
- * h: the forward's output (same layout, dtype out_dtype); h_{t-1} is read
- * from it once per 4-step run and rebuilt in fp32 inside the run.
+ * h: the forward's output (same layout, dtype out_dtype). h_{t-1} is read
+ * once per 4-step run, from ckpt when given (the forward's fp32 checkpoints)
+ * else from h, and rebuilt in fp32 inside the run.
  * dh: gradient of h, dtype out_dtype, element (b,t,d) at b*g_sb + t*g_ld + d.
  * dh_last (nullable): fp32 [B, Di], gradient of h_last, added to dh_{T-1}.
  * dhidden/dgate: same layout and dtype as hidden/gate (in_sb, in_ld).
@@ -92,11 +97,95 @@ int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
                 const float* h0,
                 int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
+                const float* ckpt,
                 const void* dh, int64_t g_sb, int64_t g_ld,
                 const float* dh_last,
                 void* dhidden, void* dgate, float* dh0,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused residual add + RMSNorm (pre-norm blocks of minLM).
+ *
+ * Replaces reference mingru/minLM.py:119-125 (norm(x) before minGRU and the
+ * residual add after it), :130 (ff_norm(x), residual add), :137 (final
+ * norm), with torch.nn.RMSNorm(dim) (:67, :69, :74): y = x * w /
+ * sqrt(mean(x^2) + eps). The reference's eps=None means torch.finfo(fp32).eps
+ * = 2^-23 for its fp32 activations; callers pass that eps.
+ *
+ * Rows of D contiguous elements (D % 4 == 0, D <= 4096), N rows.
+ * Forward:  xn = x + delta (delta nullable: xn = x, x_out unused),
+ *           x_out = xn (fp32), y = xn * rstd * w (y_dtype), rstd[row] (nullable).
+ * Backward: dx = rstd * (dy*w - xn*rstd * mean(dy*w * xn*rstd)) + dres
+ *           (dres nullable), written to dx (fp32, nullable) and to ddelta
+ *           (ddelta_dtype, nullable); dw = sum over rows of dy * xn * rstd
+ *           (written, not accumulated). xn is the forward's x_out (or x when
+ *           the forward had no delta). workspace: fp32 partial rows,
+ *           mg_add_rmsnorm_bwd_workspace_bytes(N, D) bytes.
+ * ---------------------------------------------------------------------- */
+int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* delta,
+                       const float* w, float* x_out, int y_dtype, void* y,
+                       float* rstd, int64_t N, int D, float eps, void* stream);
+
+size_t mg_add_rmsnorm_bwd_workspace_bytes(int64_t N, int D);
+
+int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* rstd,
+                       int dy_dtype, const void* dy, const float* dres,
+                       float* dx, int ddelta_dtype, void* ddelta, float* dw,
+                       int64_t N, int D, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-entropy loss head, forward and gradient in one pass.
+ *
+ * Replaces reference mingru/minLM.py:146-149 (F.cross_entropy over the
+ * transposed logits, mean reduction) and its autograd backward (log-softmax
+ * backward). logits: [N, V] row-major (fp32 or bf16), labels: int64 [N].
+ * Writes dlogits ([N, V], fp32 or bf16) = (softmax(logits) - onehot(label)) * scale
+ * and loss_part[p] = sum of the per-row losses of partition p, for
+ * p < mg_cross_entropy_partials(N) (mean loss = sum(loss_part) / N).
+ * bad_label (nullable, int, zeroed by the caller): set to 1 if a label is
+ * outside [0, V). V % 4 == 0, V <= 1024.
+ * ---------------------------------------------------------------------- */
+int mg_cross_entropy_partials(int64_t N);
+int mg_cross_entropy_fwd_bwd(int logits_dtype, const void* logits,
+                             const int64_t* labels, int dlogits_dtype,
+                             void* dlogits, float* loss_part, int* bad_label,
+                             int64_t N, int V, float scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Schedule-Free AdamW step over many parameter tensors in one launch.
+ *
+ * Replaces schedulefree.AdamWScheduleFree.step (called at reference
+ * train.py:808; package pinned at requirements.txt:44) in train mode, per
+ * element, with y = the parameter, z the base iterate, v the second moment:
+ *   v <- beta2 v + (1 - beta2) g^2
+ *   u  = g / (sqrt(v / bias_correction2) + eps) + weight_decay * y
+ *   y <- (1 - ckp1) y + ckp1 z + y_lr u;   z <- z - lr u
+ * and, when p_bf16 is set, p_bf16 <- bf16(y). The scalars (ckp1 = c_{k+1},
+ * y_lr = lr (beta1 (1 - ckp1) - 1), bias_correction2 = 1 - beta2^(k+1)) are
+ * the package's per-step values, computed by the caller in double precision
+ * (one_minus_beta2 too: 1 - 0.999 rounded once, as the package's addcmul
+ * value, not 1 - fp32(0.999)).
+ * tensors: device array of ntensors mg_sf_tensor; tensor t owns chunks
+ * [chunk_start_t, chunk_start_{t+1}) of mg_sf_adamw_chunk_elems() elements;
+ * nchunks = the total.
+ * ---------------------------------------------------------------------- */
+typedef struct mg_sf_tensor {
+  float* p;
+  const float* g;
+  float* z;
+  float* v;
+  uint16_t* p_bf16; /* nullable */
+  int64_t n;
+  int64_t chunk_start;
+} mg_sf_tensor;
+
+int64_t mg_sf_adamw_chunk_elems(void);
+int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
+                     float beta2, float one_minus_beta2,
+                     float bias_correction2, float eps, float weight_decay,
+                     float ckp1, float y_lr, float lr, void* stream);
 
 #ifdef __cplusplus
 }

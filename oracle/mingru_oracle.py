@@ -184,10 +184,42 @@ def cross_entropy_mean(logits, labels):
     return (lse - picked).mean()
 
 
-def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0):
+class _RoundBF16(torch.autograd.Function):
+    """Identity that rounds its value (forward) and its gradient (backward)
+    to bfloat16 and back: marks where a bf16-activation implementation stores
+    a tensor in bf16."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.to(torch.bfloat16).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+class _RoundGradBF16(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return x.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=False):
     """Body of mingru/minLM.py:97-138 (embedding -> blocks -> final norm -> logits),
     conv and dropout disabled. p: state dict already in the working dtype.
-    Returns (logits, next_prev_hiddens)."""
+    Returns (logits, next_prev_hiddens).
+
+    bf16_points=True evaluates the same mathematics (in p's dtype) with every
+    tensor rounded to bf16 where a bf16-activation implementation with fp32
+    residual stream, fp32 scan state and fp32 logits stores it: the GEMM
+    weights and biases, the normalized block inputs, the GEMM, scan and GELU
+    outputs, and the gradients of all of those and of the logits."""
+    r = _RoundBF16.apply if bf16_points else (lambda t: t)
+    rg = _RoundGradBF16.apply if bf16_points else (lambda t: t)
     x = F.embedding(ids, p["token_emb.weight"])                            # :97
     hiddens = iter(prev_hiddens or [])
     nxt = []
@@ -196,21 +228,25 @@ def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0):
         prev = next(hiddens, None)
         if prev is not None:
             prev = prev.to(x.dtype)
-        n = rms_norm(x, p[pre + "1.weight"])                               # :121
-        hg = F.linear(n, p[pre + "2.to_hidden_and_gate.weight"])           # minGRU.py:45
+        n = r(rms_norm(x, p[pre + "1.weight"]))                            # :121
+        hg = r(F.linear(n, r(p[pre + "2.to_hidden_and_gate.weight"])))     # minGRU.py:45
         hidden, gate = hg.chunk(2, dim=-1)
         out, h_next = mingru_scan(hidden, gate, prev)
+        out = r(out)
         if expansion != 1.0:
-            out = F.linear(out, p[pre + "2.to_out.weight"])                # minGRU.py:71
+            out = r(F.linear(out, r(p[pre + "2.to_out.weight"])))          # minGRU.py:71
         x = out + x                                                        # :125
         nxt.append(h_next)
-        x = feed_forward(rms_norm(x, p[pre + "3.weight"]), p[pre + "4.0.weight"], p[pre + "4.0.bias"],
-                         p[pre + "4.2.weight"], p[pre + "4.2.bias"]) + x  # :130
-    embed = rms_norm(x, p["norm.weight"])                                  # :137
-    return F.linear(embed, p["to_logits.weight"]), nxt                     # :138
+        n2 = r(rms_norm(x, p[pre + "3.weight"]))
+        f1 = r(F.linear(n2, r(p[pre + "4.0.weight"]), r(p[pre + "4.0.bias"])))
+        f3 = r(F.linear(r(F.gelu(f1)), r(p[pre + "4.2.weight"]), r(p[pre + "4.2.bias"])))
+        x = f3 + x                                                         # :130 (FeedForward :17-23)
+    embed = r(rms_norm(x, p["norm.weight"]))                               # :137
+    return rg(F.linear(embed, r(p["to_logits.weight"]))), nxt              # :138
 
 
-def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expansion=1.0, dtype=torch.float64):
+def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expansion=1.0, dtype=torch.float64,
+                  bf16_points=False):
     """mingru/minLM.py:86-155 with conv and dropout disabled (enable_conv=False, dropout=0).
 
     params: state dict with the reference's key names (floating tensors are
@@ -221,7 +257,7 @@ def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expan
         ids, labels = ids[:, :-1], ids[:, 1:]                              # :94-95
     if prev_hiddens is not None and not return_loss:
         ids = ids[:, -1:]                                                  # :101-102 (per-token, so slicing ids == slicing x)
-    logits, nxt = minlm_core(p, ids, depth, prev_hiddens, expansion)
+    logits, nxt = minlm_core(p, ids, depth, prev_hiddens, expansion, bf16_points)
     if not return_loss:
         return logits, nxt
     return cross_entropy_mean(logits, labels), nxt                         # :146-149

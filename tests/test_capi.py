@@ -48,7 +48,7 @@ def test_version_and_queries(L):
 
 def _fwd(L, **kw):
     args = dict(in_dtype=1, hidden=16, gate=16, in_sb=1024, in_ld=64, h0=None, out_dtype=1, h=16, out_sb=512,
-                out_ld=64, h_last=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
+                out_ld=64, h_last=None, ckpt=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
     args.update(kw)
     return L.mg_scan_fwd(*args.values())
 

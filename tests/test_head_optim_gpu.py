@@ -1,0 +1,146 @@
+"""GPU parity of the loss head (mg_cross_entropy_fwd_bwd, reference
+mingru/minLM.py:146-149), the fused Schedule-Free AdamW step
+(mg_sf_adamw_step, checked against oracle/sf_adamw.py) and the bf16 linear
+layers with cached weight copies.
+
+Tolerances: fp32 1e-5 relative (loss, logits gradient); bf16 activations
+2e-2; optimizer state fp32 1e-6 relative after several steps.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import sf_adamw as S
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+@pytest.mark.parametrize("V", [256, 260, 64, 1000])
+@pytest.mark.parametrize("scale", [1.0, 30.0])
+def test_cross_entropy_fp32(V, scale):
+    from gruboros_amd.loss import CrossEntropyFromLogits
+
+    gen = torch.Generator().manual_seed(V)
+    N = 777
+    logits = torch.randn(N, V, generator=gen, dtype=torch.float64) * scale
+    labels = torch.randint(0, V, (N,), generator=gen)
+    labels[:3] = torch.tensor([0, V - 1, 0])
+    lg = logits.float().to(DEV).requires_grad_(True)
+    loss = CrossEntropyFromLogits.apply(lg, labels.to(DEV))
+    (loss * 0.25).backward()
+    lr = logits.clone().requires_grad_(True)
+    ref = F.cross_entropy(lr, labels)
+    (ref * 0.25).backward()
+    assert abs(float(loss) - float(ref)) / float(ref) < 1e-5
+    assert _rel(lg.grad, lr.grad) < 1e-5
+
+
+def test_logits_cross_entropy_bf16_matches_reference_head():
+    """embed bf16 [B, T, D] through to_logits + CE vs the fp64 reference head."""
+    from gruboros_amd.loss import logits_cross_entropy
+
+    torch.manual_seed(0)
+    B, T, D, V = 4, 127, 256, 256
+    head = torch.nn.Linear(D, V, bias=False).to(DEV)
+    embed = torch.randn(B, T, D, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    labels = torch.randint(0, V, (B, T), device=DEV)
+    loss = logits_cross_entropy(embed, head, labels)
+    loss.backward()
+    e64 = embed.detach().double().cpu().requires_grad_(True)
+    w64 = head.weight.detach().double().cpu().requires_grad_(True)
+    ref = F.cross_entropy(F.linear(e64, w64).transpose(1, 2), labels.cpu())
+    ref.backward()
+    assert abs(float(loss) - float(ref)) / float(ref) < 2e-2
+    assert _rel(embed.grad, e64.grad) < 2e-2
+    assert _rel(head.weight.grad, w64.grad) < 2e-2
+    assert head.weight.grad.dtype == torch.float32
+
+
+def test_cross_entropy_flags_bad_labels():
+    from gruboros_amd import _lib
+
+    L = _lib.lib()
+    N, V = 16, 256
+    logits = torch.randn(N, V, device=DEV)
+    labels = torch.zeros(N, dtype=torch.int64, device=DEV)
+    labels[5] = V + 3
+    dl = torch.empty(N, V, device=DEV)
+    part = torch.empty(L.mg_cross_entropy_partials(N), device=DEV)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    rc = L.mg_cross_entropy_fwd_bwd(0, _lib.ptr(logits), _lib.ptr(labels), 0, _lib.ptr(dl), _lib.ptr(part),
+                                    _lib.ptr(bad), N, V, 1.0 / N, _lib.stream_of(logits))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(bad) == 1
+
+
+@pytest.mark.parametrize("wd", [0.0, 0.01])
+def test_sf_adamw_fused_matches_restatement(wd):
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    torch.manual_seed(1)
+    shapes = [(1000, 33), (257,), (4, 4), (8192, 3), (7,)]
+    ps = [torch.nn.Parameter(torch.randn(s, device=DEV)) for s in shapes]
+    ref_ps = [p.detach().double().cpu().clone() for p in ps]
+    opt = AdamWScheduleFree(ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2)
+    opt.train()
+    ref = S.RefAdamWScheduleFree(ref_ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2)
+    for step in range(5):
+        grads = [torch.randn(s, device=DEV) for s in shapes]
+        for p, g in zip(ps, grads):
+            p.grad = g
+        opt.step()
+        ref.step([g.double().cpu() for g in grads])
+    for i, p in enumerate(ps):
+        st = opt.state[p]
+        assert _rel(p, ref.params[i]) < 1e-6
+        assert _rel(st["z"], ref.z[i]) < 1e-6
+        assert _rel(st["exp_avg_sq"], ref.v[i]) < 1e-6
+    # eval()/train() mode switches of the package: x = (y - (1 - b1) z) / b1 and back
+    y = ps[0].detach().clone()
+    opt.eval()
+    torch.testing.assert_close(ps[0], (y - 0.1 * opt.state[ps[0]]["z"]) / 0.9, rtol=1e-5, atol=1e-6)
+    opt.train()
+    torch.testing.assert_close(ps[0], y, rtol=1e-5, atol=1e-6)
+
+
+def test_bf16_weight_copy_follows_the_master():
+    from gruboros_amd.linear import bf16_copy, linear
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    torch.manual_seed(2)
+    layer = torch.nn.Linear(64, 32).to(DEV)
+    x = torch.randn(5, 64, device=DEV).to(torch.bfloat16)
+    wb = bf16_copy(layer.weight)
+    torch.testing.assert_close(wb, layer.weight.detach().to(torch.bfloat16))
+    # in-place change by the caller (e.g. gossip blend) -> copy re-made
+    with torch.no_grad():
+        layer.weight.mul_(0.5).add_(1.0)
+    torch.testing.assert_close(bf16_copy(layer.weight), layer.weight.detach().to(torch.bfloat16))
+    # optimizer step writes master and copy together
+    opt = AdamWScheduleFree(layer.parameters(), lr=1e-2)
+    opt.train()
+    y = linear(x, layer)
+    y.float().square().sum().backward()
+    assert layer.weight.grad.dtype == torch.float32 and layer.bias.grad.dtype == torch.float32
+    opt.step()
+    torch.testing.assert_close(bf16_copy(layer.weight), layer.weight.detach().to(torch.bfloat16))
+    # gradients of the bf16 linear vs fp64
+    x64 = x.double().cpu().requires_grad_(True)
+    w64 = layer.weight.detach().double().cpu().requires_grad_(True)
+    b64 = layer.bias.detach().double().cpu().requires_grad_(True)
+    layer.zero_grad()
+    xg = x.clone().requires_grad_(True)
+    out = linear(xg, layer)
+    dy = torch.randn(out.shape, device=DEV)
+    (out.float() * dy).sum().backward()
+    (F.linear(x64, w64, b64) * dy.double().cpu()).sum().backward()
+    assert _rel(xg.grad, x64.grad) < 2e-2
+    assert _rel(layer.weight.grad, w64.grad) < 2e-2
+    assert _rel(layer.bias.grad, b64.grad) < 2e-2

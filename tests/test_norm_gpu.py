@@ -1,0 +1,79 @@
+"""GPU parity of the fused residual-add + RMSNorm kernels against the CPU
+oracle (torch.nn.RMSNorm semantics of mingru/minLM.py:67,69,74 with the fp32
+epsilon; residual adds of :125, :130), forward and autograd backward in fp64.
+
+Tolerances: fp32 output 1e-5 relative; bf16 output 2e-2 (rounding of y to
+bf16 is 2^-9); gradients are norm-relative.
+"""
+import pytest
+import torch
+
+from oracle import mingru_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("delta_dtype", [None, torch.float32, torch.bfloat16], ids=["plain", "dF32", "dBF16"])
+@pytest.mark.parametrize("shape", [(3, 5, 64), (2, 7, 200), (4, 33, 1024), (1, 9, 2048), (2, 3, 768)])
+def test_add_rmsnorm_parity(shape, delta_dtype, out_dtype):
+    from gruboros_amd.norm import add_rms_norm, rms_norm
+
+    gen = torch.Generator().manual_seed(sum(shape))
+    D = shape[-1]
+    x = torch.randn(shape, generator=gen) * 1e-3  # tiny activations: eps matters (minLM init scale)
+    w = torch.randn(D, generator=gen)
+    dy = torch.randn(shape, generator=gen)
+    dres = torch.randn(shape, generator=gen)
+    delta = (torch.randn(shape, generator=gen) * 1e-3).to(delta_dtype) if delta_dtype else None
+
+    xg = x.to(DEV).requires_grad_(True)
+    wg = w.to(DEV).requires_grad_(True)
+    dg = delta.to(DEV).requires_grad_(True) if delta is not None else None
+    if dg is None:
+        y = rms_norm(xg, wg, out_dtype)
+        (y.float() * dy.to(DEV)).sum().backward()
+    else:
+        xo, y = add_rms_norm(xg, dg, wg, out_dtype)
+        ((y.float() * dy.to(DEV)).sum() + (xo * dres.to(DEV)).sum()).backward()
+    assert y.dtype == out_dtype
+
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    dr = delta.double().requires_grad_(True) if delta is not None else None
+    xn = xr + dr if dr is not None else xr
+    yr = O.rms_norm(xn, wr)
+    loss = (yr * dy.to(torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32).double()).sum()
+    if dr is not None:
+        loss = loss + (xn * dres.double()).sum()
+    loss.backward()
+
+    tol = 1e-5 if out_dtype == torch.float32 else 2e-2
+    errs = {"y": _rel(y, yr.detach()), "dx": _rel(xg.grad, xr.grad), "dw": _rel(wg.grad, wr.grad)}
+    if dr is not None:
+        errs["x_out"] = _rel(xo, xn.detach())
+        errs["ddelta"] = _rel(dg.grad, dr.grad)
+    print(shape, delta_dtype, out_dtype, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for k, v in errs.items():
+        lim = 2e-2 if (delta_dtype == torch.bfloat16 and k == "ddelta") else tol
+        assert v <= lim, f"{k}: {v:.3e} > {lim}"
+
+
+def test_rmsnorm_matches_torch_module_fp32():
+    """Against torch.nn.RMSNorm(dim) itself (eps=None), the reference's layer."""
+    from gruboros_amd.norm import rms_norm
+
+    torch.manual_seed(0)
+    m = torch.nn.RMSNorm(1024).to(DEV)
+    with torch.no_grad():
+        m.weight.copy_(torch.randn(1024))
+    x = torch.randn(8, 100, 1024, device=DEV) * 3e-4
+    ref = m(x)
+    out = rms_norm(x, m.weight, torch.float32)
+    torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-6)
