@@ -28,6 +28,18 @@ BF16_PEAK_TFLOPS = 2500.0
 METRIC = "train tokens/sec (minLM d1024 L8 seq2048 bf16, 1 GPU); scan HBM GB/s vs peak"
 
 
+def measured_traffic(kernel, path=os.path.join(ROOT, "profiles", "scan_cfg2_traffic.md")):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (calibrated against a plain copy), or None."""
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cfg3_matmul_params(dim=1024, depth=8, ff_mult=4, vocab=256, expansion=1.0):
     di = int(dim * expansion)
     f = int(dim * ff_mult)
@@ -171,6 +183,9 @@ def main():
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["train", "scan"], default=None)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 1 GiB device copy (torch copy kernel): the known-size "
+                         "reference for FETCH_SIZE/WRITE_SIZE counter scaling")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the minGRU hot path is built and "
@@ -184,6 +199,16 @@ def main():
 
     _lib.lib()
     print(f"[bench] device {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        print("[bench] copy calibration: 3 x 1 GiB device copies (1073741824 B read + written each)",
+              file=sys.stderr, flush=True)
 
     train = scan = None
     if args.only in (None, "scan"):
@@ -217,7 +242,12 @@ def main():
     if scan:
         bwd_gbs = scan["bwd_GBs"]
         out["roofline"] = {"kernel": "scan_bwd_kernel<bf16,bf16> (cfg2)", "bound": "hbm", "achieved": bwd_gbs,
-                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bwd_gbs / HBM_PEAK_GBS, "traffic": None}
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bwd_gbs / HBM_PEAK_GBS,
+                           "traffic": measured_traffic("scan_bwd_kernel"),
+                           "algorithmic_bytes": 12 * scan["elements"],
+                           "note": "achieved = 12 B/element x 2^28 / mean launch time (HIP events on the launch "
+                                   "stream, incl. the ~6 us look-back workspace clear); traffic = calibrated "
+                                   "FETCH_SIZE+WRITE_SIZE bytes per launch (profiles/scan_cfg2_traffic.md)"}
         out["scan"] = scan
     if train:
         out["step_roofline"] = {"bound": "mfma", "achieved": train["tflops"], "peak": BF16_PEAK_TFLOPS,
