@@ -37,6 +37,8 @@ SIGNATURES = {
                                           _vp]),
     "mg_sf_adamw_chunk_elems": (_c_i64, []),
     "mg_sf_adamw_step": (_c_int, [_vp, _c_int, _c_i64] + [ctypes.c_float] * 8 + [_vp]),
+    "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
+                         _c_int, _vp, _c_i64, _c_int, _vp]),
 }
 
 _LIB = None

@@ -1,0 +1,477 @@
+// bf16 matrix products on MFMA (v_mfma_f32_32x32x16_bf16) with fp32
+// accumulation, for the dense layers of the minLM step:
+//   to_hidden_and_gate      reference mingru/minGRU.py:45   (Y = X W^T)
+//   to_out                  reference mingru/minGRU.py:71
+//   FeedForward             reference mingru/minLM.py:17-23 (Linear, GELU, Linear)
+//   to_logits               reference mingru/minLM.py:75,138
+// and their backward products (dX = dY W, dW = dY^T X).
+//
+// C[m, n] = sum_k A(m, k) B(k, n) with each operand in one of two layouts:
+//   K-contiguous : element (row, k) at p + row * ld + k    (X, W as stored)
+//   MN-contiguous: element (row, k) at p + k * ld + row    (dY^T, X^T for dW)
+// The weight of Y = X W^T is the K-contiguous B (rows = output features).
+//
+// Workgroup tile BM x BN x 64 (BM, BN in {128, 256}), four waves in a 2 x 2
+// grid, each owning (BM/2) x (BN/2) as 32 x 32 MFMA blocks. Operand tiles are
+// staged through LDS as [row][64 k] bf16, 128 bytes a row, with the 16-byte
+// chunk c of row r stored at chunk c ^ ((r ^ (r >> 3)) & 7): the fragment
+// reads (32 consecutive rows, one chunk) and both kinds of tile writes hit
+// 8 distinct chunks per 8 lanes. MN-contiguous operands are loaded as 8 x 8
+// blocks (8 k-rows of 16 bytes) and transposed in registers before the LDS
+// write, so every fragment read is one 16-byte LDS load. Two LDS stages: the
+// global loads of tile k+1 are in flight while tile k is multiplied, and
+// one barrier per k-tile orders the stages.
+//
+// The MFMA is fed the B fragment as its first operand and the A fragment as
+// its second, so a lane's accumulator holds C[m][n..n+3] (4 consecutive
+// output columns of one row) and stores are 8- or 16-byte vectors.
+//
+// Epilogues (fused into the store):
+//   NONE       C = acc
+//   BIAS       C = acc + bias[n]
+//   BIAS_GELU  aux = bf16(acc + bias[n]);  C = gelu(aux)      (FeedForward up)
+//   GELU_GRAD  C = acc * gelu'(aux[m][n])                     (its backward)
+// with gelu(x) = x/2 (1 + erf(x / sqrt 2)), the exact form of nn.GELU().
+// fp32 outputs may be split along K over several workgroups that add into C
+// with fp32 atomics (summation order then varies run to run, ~1 ulp).
+
+#include <algorithm>
+#include <type_traits>
+
+#include "mg_common.h"
+
+namespace mg {
+namespace gemm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#ifndef GEMM_WM
+#define GEMM_WM 2
+#endif
+#ifndef GEMM_WN
+#define GEMM_WN 4
+#endif
+constexpr int BK = 64;
+
+struct Params {
+  const bf16_t* A;
+  const bf16_t* B;
+  void* C;
+  const float* bias;
+  bf16_t* aux;
+  int64_t lda, ldb, ldc, ldaux;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int kt_per_split;  // k-tiles per split (gridDim.y splits)
+  uint32_t a_span, b_span;  // bytes from A / B to one past their last element
+};
+
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 3)) & 7); }
+
+// Operand tile loader: R rows x 64 k, into LDS as [R][8 chunks of 8 bf16].
+// Global reads go through a buffer resource spanning exactly the operand, so
+// rows (K-contiguous) or k-rows (MN-contiguous) past the end read as zero
+// without branches; the contiguous dimension is masked with a select.
+struct Operand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t ld2;  // leading dimension in bytes
+};
+
+__device__ __forceinline__ Operand make_operand(const bf16_t* p, int64_t ld, uint32_t span_bytes) {
+  Operand o;
+  o.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), static_cast<short>(0),
+                                             static_cast<int>(span_bytes), 0x00020000);
+  o.ld2 = static_cast<uint32_t>(ld) * 2u;
+  return o;
+}
+
+// A masked-off load is sent past the buffer's end (offsets stay below 2^31
+// for valid elements), where the hardware range check returns zero.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ uint4 load16(const Operand& o, uint32_t off, bool ok) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, ok ? off : kOutOfRange, 0, 0));
+}
+
+template <int R, bool KMAJ, int T>
+struct Loader;
+
+// K-contiguous rows: 8 chunks of 16 bytes per row, T/8 rows per pass.
+template <int R, int T>
+struct Loader<R, true, T> {
+  static constexpr int kN = R * 8 / T;  // 16-byte loads per thread
+  static_assert(kN >= 1 && R * 8 % T == 0, "tile rows vs threads");
+  uint4 v[kN];
+
+  __device__ __forceinline__ void load(const Operand& o, int r0, int rmax, int k0, int K) {
+    const int c = threadIdx.x & 7;
+    const int kk = k0 + c * 8;
+    const uint32_t base = static_cast<uint32_t>(r0 + (threadIdx.x >> 3)) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
+#pragma unroll
+    for (int i = 0; i < kN; ++i) v[i] = load16(o, base + static_cast<uint32_t>(T / 8 * i) * o.ld2, kk < K);
+  }
+  __device__ __forceinline__ void store(uint4* __restrict__ s) const {
+    const int c = threadIdx.x & 7;
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      const int r = (threadIdx.x >> 3) + T / 8 * i;
+      s[r * 8 + swz(r, c)] = v[i];
+    }
+  }
+};
+
+// MN-contiguous rows: thread t loads KG consecutive k-rows of 8 consecutive
+// tile rows (16 bytes each), transposes the KG x 8 block in registers and
+// writes KG k-values (2 KG bytes) into each of its 8 LDS rows.
+template <int R, int T>
+struct Loader<R, false, T> {
+  static constexpr int kRG = R / 8;          // row groups
+  static constexpr int KG = 8 * R / T;       // k-rows per thread
+  static_assert(KG == 2 || KG == 4 || KG == 8, "tile rows vs threads");
+  uint4 v[KG];
+
+  __device__ __forceinline__ void load(const Operand& o, int r0, int rmax, int k0, int) {
+    const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
+    const int r = r0 + rb * 8;
+    const uint32_t base = static_cast<uint32_t>(k0 + kb * KG) * o.ld2 + static_cast<uint32_t>(r) * 2u;
+#pragma unroll
+    for (int i = 0; i < KG; ++i) v[i] = load16(o, base + static_cast<uint32_t>(i) * o.ld2, r < rmax);
+  }
+  __device__ __forceinline__ void store(uint4* __restrict__ s) const {
+    const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
+    const int c = kb * KG / 8, off = (kb * KG % 8) * 2;  // chunk and byte offset of this thread's k-range
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(v);  // w[4 i + d]: k-row i, dword d
+    unsigned char* sb = reinterpret_cast<unsigned char*>(s);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // row rb*8+j gets element j of each of the KG k-rows
+      uint32_t od[KG / 2];
+#pragma unroll
+      for (int q = 0; q < KG / 2; ++q) {
+        const uint32_t lo = w[4 * (2 * q) + j / 2], hi = w[4 * (2 * q + 1) + j / 2];
+        od[q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
+      const int r = rb * 8 + j;
+      unsigned char* dst = sb + (r * 8 + swz(r, c)) * 16 + off;
+      if constexpr (KG == 8) *reinterpret_cast<uint4*>(dst) = make_uint4(od[0], od[1], od[2], od[3]);
+      else if constexpr (KG == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(od[0], od[1]);
+      else *reinterpret_cast<uint32_t*>(dst) = od[0];
+    }
+  }
+};
+
+enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_GELU_GRAD = 3 };
+
+__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+__device__ __forceinline__ float gelu_grad(float x) {
+  return 0.5f * (1.0f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-0.5f * x * x);
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Map the linear workgroup index to a tile. Workgroups are dispatched round
+// robin over the 8 XCDs (each with its own L2); remap so each XCD gets a
+// contiguous range, then walk that range in groups of 8 tile rows so the
+// workgroups sharing an A row band or a B column band sit on one XCD.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int nt = tiles_m * tiles_n;
+  if ((nt & 7) == 0) pid = (pid & 7) * (nt >> 3) + (pid >> 3);
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int group = pid / per_group;
+  const int first = group * GM;
+  const int gsize = min(tiles_m - first, GM);
+  const int in_group = pid - group * per_group;
+  tm = first + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
+  constexpr int T = 64 * WM * WN;
+  constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
+  constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
+  __shared__ uint4 smem[2 * kStage];
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nkt = (p.K + BK - 1) / BK;
+  const int kt0 = blockIdx.y * p.kt_per_split;
+  const int kt1 = min(nkt, kt0 + p.kt_per_split);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int L = lane & 31, half = lane >> 5;
+  f32x16 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  Loader<BM, AK, T> la;
+  Loader<BN, BKM, T> lb;
+  if (kt0 < kt1) {
+    la.load(oa, m0, p.M, kt0 * BK, p.K);
+    lb.load(ob, n0, p.N, kt0 * BK, p.K);
+    la.store(smem);
+    lb.store(smem + BM * 8);
+  }
+  __syncthreads();
+
+  // LDS row of this lane's fragment for block i / j
+  int arow[MB], brow[NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) arow[i] = wm * (BM / WM) + i * 32 + L;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32 + L;
+
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int st = (kt - kt0) & 1;
+    const bool more = kt + 1 < kt1;
+    if (more) {
+      la.load(oa, m0, p.M, (kt + 1) * BK, p.K);
+      lb.load(ob, n0, p.N, (kt + 1) * BK, p.K);
+    }
+    const uint4* As = smem + st * kStage;
+    const uint4* Bs = As + BM * 8;
+    // fragments of k-step s+1 are read while the MFMAs of step s run
+    bf16x8 af[2][MB], bfr[2][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) af[0][i] = __builtin_bit_cast(bf16x8, As[arow[i] * 8 + swz(arow[i], half)]);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bfr[0][j] = __builtin_bit_cast(bf16x8, Bs[brow[j] * 8 + swz(brow[j], half)]);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < BK / 16) {
+        const int c = 2 * (s + 1) + half;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = __builtin_bit_cast(bf16x8, As[arow[i] * 8 + swz(arow[i], c)]);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = __builtin_bit_cast(bf16x8, Bs[brow[j] * 8 + swz(brow[j], c)]);
+      }
+      // keep the reads of step s+1 ahead of the products of step s
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (more) {
+      uint4* nxt = smem + (st ^ 1) * kStage;
+      la.store(nxt);
+      lb.store(nxt + BM * 8);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue, one 32-row block of the wave's (BM/2) x (BN/2) region at a
+  // time: the accumulators go to a wave-private LDS block and come back as
+  // whole 16-byte chunks of rows, so each global store instruction writes
+  // contiguous row segments; bias and GELU are applied on the way out.
+  // Staged as bf16 only for a plain bf16 output, else as fp32 (so the bias
+  // is added before the one rounding to the output type).
+  using S = typename std::conditional<std::is_same<TC, bf16_t>::value && EPI == EPI_NONE, bf16_t, float>::type;
+  constexpr int NW = BN / WN;                // columns per wave
+  constexpr int RB = NW * int(sizeof(S));    // staged bytes per row
+  constexpr int CQ = RB / 16;                // 16-byte chunks per row
+  constexpr int EPC = 16 / int(sizeof(S));   // elements per chunk
+  constexpr int RPI = 64 / CQ;               // rows per read instruction
+  static_assert(32 * RB * WM * WN <= int(sizeof(smem)), "staging fits in the operand stages");
+  unsigned char* stage = reinterpret_cast<unsigned char*>(smem) + wave * 32 * RB;
+  const int row0 = m0 + wm * (BM / WM), col0 = n0 + wn * NW;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = j * 32 + 8 * g + 4 * half;  // column within the wave's region
+        f4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x.v[e] = acc[i][j][4 * g + e];
+        if constexpr (sizeof(S) == 4) {
+          const int q = c / 4;
+          io4<float>::store(reinterpret_cast<float*>(stage + L * RB + ((q ^ (L % CQ)) * 16)), x);
+        } else {
+          const int q = c / 8;
+          io4<bf16_t>::store(reinterpret_cast<bf16_t*>(stage + L * RB + ((q ^ (L % CQ)) * 16) + 8 * half), x);
+        }
+      }
+    }
+    __syncthreads();
+    if (ATOMIC) {
+      // one float per lane, 64 consecutive columns of a row per instruction
+#pragma unroll 4
+      for (int t = 0; t < 32 * NW / 64; ++t) {
+        const int r = t / (NW / 64), c = (t % (NW / 64)) * 64 + lane;
+        const int m = row0 + i * 32 + r, n = col0 + c;
+        const int q = c / 4;
+        const float v = *reinterpret_cast<const float*>(stage + r * RB + ((q ^ (r % CQ)) * 16) + (c % 4) * 4);
+        if (m < p.M && n < p.N) unsafeAtomicAdd(static_cast<float*>(p.C) + static_cast<int64_t>(m) * p.ldc + n, v);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 32 / RPI; ++t) {
+        const int r = t * RPI + lane / CQ, q = lane % CQ;
+        const int m = row0 + i * 32 + r, n = col0 + q * EPC;
+        const uint4 raw = *reinterpret_cast<const uint4*>(stage + r * RB + ((q ^ (r % CQ)) * 16));
+        if (m >= p.M || n >= p.N) continue;
+        TC* cp = static_cast<TC*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
+        if constexpr (sizeof(S) == 4) {
+          f4 x;
+          x.v[0] = __uint_as_float(raw.x); x.v[1] = __uint_as_float(raw.y);
+          x.v[2] = __uint_as_float(raw.z); x.v[3] = __uint_as_float(raw.w);
+          if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) {
+            const float4 b = *reinterpret_cast<const float4*>(p.bias + n);
+            x.v[0] += b.x; x.v[1] += b.y; x.v[2] += b.z; x.v[3] += b.w;
+          }
+          if (EPI == EPI_BIAS_GELU) {
+            // aux = bf16(acc + bias), the pre-activation; C = gelu of it
+            io4<bf16_t>::store(p.aux + static_cast<int64_t>(m) * p.ldaux + n, x);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x.v[e] = gelu(round_bf16(x.v[e]));
+          }
+          if (EPI == EPI_GELU_GRAD) {
+            const f4 pre = io4<bf16_t>::load(p.aux + static_cast<int64_t>(m) * p.ldaux + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x.v[e] *= gelu_grad(pre.v[e]);
+          }
+          io4<TC>::store(cp, x);
+        } else {
+          *reinterpret_cast<uint4*>(cp) = raw;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void zero_f32_kernel(float* __restrict__ p, int64_t rows, int cols, int64_t ld) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x); i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols, c = i - r * cols;
+    p[r * ld + c] = 0.0f;
+  }
+}
+
+constexpr int kCUs = 256;
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
+int launch(const Params& p0, int splits, hipStream_t stream) {
+  Params p = p0;
+  p.tiles_m = (p.M + BM - 1) / BM;
+  p.tiles_n = (p.N + BN - 1) / BN;
+  const int nkt = (p.K + BK - 1) / BK;
+  p.kt_per_split = std::max((nkt + splits - 1) / splits, 1);
+  const int ysplits = std::max((nkt + p.kt_per_split - 1) / p.kt_per_split, 1);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, ATOMIC>), dim3(p.tiles_m * p.tiles_n, ysplits),
+                     dim3(64 * WM * WN), 0, stream, p);
+  return check_launch("mg_gemm");
+}
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
+int dispatch_epi(const Params& p, int epi, int c_dtype, bool atomic, int splits, hipStream_t s) {
+  if (c_dtype == MG_F32) {
+    if (atomic) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, true>(p, splits, s);
+    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, false>(p, 1, s);
+    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, float, false>(p, 1, s);
+  } else {
+    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, bf16_t, false>(p, 1, s);
+    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, false>(p, 1, s);
+    if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, false>(p, 1, s);
+    if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, false>(p, 1, s);
+  }
+  return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
+}
+
+template <int BM, int BN, int WM, int WN>
+int dispatch_layout(const Params& p, bool ak, bool bk, int epi, int c_dtype, bool atomic, int splits,
+                    hipStream_t s) {
+  if (ak && bk) return dispatch_epi<BM, BN, WM, WN, true, true>(p, epi, c_dtype, atomic, splits, s);
+  if (ak && !bk) return dispatch_epi<BM, BN, WM, WN, true, false>(p, epi, c_dtype, atomic, splits, s);
+  if (!ak && !bk) return dispatch_epi<BM, BN, WM, WN, false, false>(p, epi, c_dtype, atomic, splits, s);
+  return dispatch_epi<BM, BN, WM, WN, false, true>(p, epi, c_dtype, atomic, splits, s);
+}
+
+}  // namespace gemm
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, const void* B, int64_t ldb, int M,
+                       int N, int K, int epilogue, const float* bias, void* aux, int64_t ldaux, int c_dtype, void* C,
+                       int64_t ldc, int accumulate, void* stream) {
+  const char* fn = "mg_gemm";
+  if (!A || !B || !C) return fail(MG_ERR_ARG, "%s: null operand", fn);
+  if (M < 0 || N < 0 || K < 0) return fail(MG_ERR_ARG, "%s: negative size", fn);
+  if ((a_layout != MG_KCONTIG && a_layout != MG_MNCONTIG) || (b_layout != MG_KCONTIG && b_layout != MG_MNCONTIG))
+    return fail(MG_ERR_ARG, "%s: bad layout code", fn);
+  if (c_dtype != MG_F32 && c_dtype != MG_BF16) return fail(MG_ERR_DTYPE, "%s: bad output dtype %d", fn, c_dtype);
+  if (epilogue < MG_EPI_NONE || epilogue > MG_EPI_GELU_GRAD) return fail(MG_ERR_ARG, "%s: bad epilogue %d", fn, epilogue);
+  if (N % 8) return fail(MG_ERR_ARG, "%s: N (%d) must be a multiple of 8", fn, N);
+  if ((a_layout == MG_KCONTIG || b_layout == MG_KCONTIG) && K % 8)
+    return fail(MG_ERR_ARG, "%s: K (%d) must be a multiple of 8 for a K-contiguous operand", fn, K);
+  if (a_layout == MG_MNCONTIG && M % 8) return fail(MG_ERR_ARG, "%s: M (%d) must be a multiple of 8 for an MN-contiguous A", fn, M);
+  if (lda % 8 || ldb % 8 || ldc % (c_dtype == MG_F32 ? 4 : 8) || (aux && ldaux % 8))
+    return fail(MG_ERR_ARG, "%s: leading dimensions must span whole 16-byte chunks", fn);
+  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16) || (aux && !aligned(aux, 16)) || (bias && !aligned(bias, 16)))
+    return fail(MG_ERR_ARG, "%s: operands must be 16-byte aligned", fn);
+  if (lda < (a_layout == MG_KCONTIG ? K : M) || ldb < (b_layout == MG_KCONTIG ? K : N) || ldc < N)
+    return fail(MG_ERR_ARG, "%s: leading dimension smaller than the row", fn);
+  if ((epilogue == MG_EPI_BIAS || epilogue == MG_EPI_BIAS_GELU) && !bias)
+    return fail(MG_ERR_ARG, "%s: epilogue needs bias", fn);
+  if ((epilogue == MG_EPI_BIAS_GELU || epilogue == MG_EPI_GELU_GRAD) && (!aux || ldaux < N || c_dtype != MG_BF16))
+    return fail(MG_ERR_ARG, "%s: GELU epilogues need aux (bf16, ldaux >= N) and a bf16 output", fn);
+  if (accumulate && (c_dtype != MG_F32 || epilogue != MG_EPI_NONE))
+    return fail(MG_ERR_ARG, "%s: accumulate needs an fp32 output and no epilogue", fn);
+  if (M == 0 || N == 0) return MG_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  gemm::Params p{};
+  p.A = static_cast<const bf16_t*>(A);
+  p.B = static_cast<const bf16_t*>(B);
+  p.C = C;
+  p.bias = bias;
+  p.aux = static_cast<bf16_t*>(aux);
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc; p.ldaux = ldaux;
+  p.M = M; p.N = N; p.K = K;
+  const bool ak = a_layout == MG_KCONTIG, bk = b_layout == MG_KCONTIG;
+  // bytes spanned by each operand; buffer offsets are 32-bit
+  const int64_t a_span = ak ? (int64_t(M - 1) * lda + K) * 2 : (int64_t(std::max(K, 1) - 1) * lda + M) * 2;
+  const int64_t b_span = bk ? (int64_t(N - 1) * ldb + K) * 2 : (int64_t(std::max(K, 1) - 1) * ldb + N) * 2;
+  if (a_span + 256 * lda * 2 >= (int64_t(1) << 31) || b_span + 256 * ldb * 2 >= (int64_t(1) << 31))
+    return fail(MG_ERR_ARG, "%s: operands must span less than 2 GiB", fn);
+  p.a_span = static_cast<uint32_t>(a_span);
+  p.b_span = static_cast<uint32_t>(b_span);
+
+  // Tile choice: 256 x 256 when that still gives every CU a workgroup,
+  // else 128 x 128. fp32 outputs with few tiles and a long K split K.
+  const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
+  const bool big = t256 >= gemm::kCUs;
+  const int64_t tiles = big ? t256 : t128;
+  const int nkt = (K + gemm::BK - 1) / gemm::BK;
+  int splits = 1;
+  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < gemm::kCUs)
+    splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(gemm::kCUs / tiles, 1), std::max(nkt / 4, 1)));
+  if (K == 0 && accumulate) return MG_OK;
+  const bool atomic = accumulate || splits > 1;
+  if (atomic && !accumulate) {
+    hipLaunchKernelGGL(gemm::zero_f32_kernel, dim3(1024), dim3(256), 0, s, static_cast<float*>(C), int64_t(M), N, ldc);
+    if (int rc = check_launch(fn)) return rc;
+  }
+  return big ? gemm::dispatch_layout<256, 256, GEMM_WM, GEMM_WN>(p, ak, bk, epilogue, c_dtype, atomic, splits, s)
+             : gemm::dispatch_layout<128, 128, 2, 2>(p, ak, bk, epilogue, c_dtype, atomic, splits, s);
+}

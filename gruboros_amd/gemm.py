@@ -1,0 +1,69 @@
+"""bf16 MFMA matrix products of libmingru_hip.so (mg_gemm) for the nn.Linear
+layers of the hot path (reference mingru/minGRU.py:45,71; mingru/minLM.py:17-23,
+:75,:138): forward Y = X W^T (+ bias, + GELU), and the backward products
+dX = dY W and dW = dY^T X (fp32, optionally accumulated).
+
+All tensors are CUDA bf16 (fp32 for bias, dW and fp32 outputs), 2-D with a
+unit inner stride; the functions launch on torch's current stream.
+"""
+import torch
+
+from . import _lib
+
+KCONTIG, MNCONTIG = 0, 1
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD = 0, 1, 2, 3
+
+
+def _rows(t, name):
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise _lib.MingruHipError(f"{name}: expected a 2-D tensor with unit inner stride, got "
+                                  f"shape {tuple(t.shape)} strides {t.stride()}")
+    return t.stride(0)
+
+
+def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False):
+    """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm)."""
+    _lib.require_cuda(a, b, out)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise _lib.MingruHipError(f"mg_gemm operands must be bfloat16 (got {a.dtype}, {b.dtype})")
+    lda, ldb, ldc = _rows(a, "A"), _rows(b, "B"), _rows(out, "C")
+    ldaux = _rows(aux, "aux") if aux is not None else 0
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
+        raise _lib.MingruHipError("mg_gemm bias must be contiguous float32")
+    L = _lib.lib()
+    rc = L.mg_gemm(a_layout, _lib.ptr(a), lda, b_layout, _lib.ptr(b), ldb, M, N, K, epilogue,
+                   _lib.ptr(bias) if bias is not None else None, _lib.ptr(aux) if aux is not None else None, ldaux,
+                   _lib.dtype_code(out.dtype), _lib.ptr(out), ldc, int(accumulate), _lib.stream_of(out))
+    _lib.check(rc, "mg_gemm")
+    return out
+
+
+def linear_fwd(x, w, bias=None, *, gelu_pre=None, out_dtype=torch.bfloat16):
+    """x [N, in] bf16, w [out, in] bf16 -> x w^T (+ bias) [N, out].
+    gelu_pre: if given ([N, out] bf16), receives x w^T + bias and the result is gelu of it."""
+    n, k = x.shape
+    o = w.shape[0]
+    y = torch.empty(n, o, device=x.device, dtype=out_dtype)
+    if gelu_pre is not None:
+        epi = EPI_BIAS_GELU
+    else:
+        epi = EPI_BIAS if bias is not None else EPI_NONE
+    return gemm(x, KCONTIG, w, KCONTIG, n, o, k, y, epilogue=epi, bias=bias, aux=gelu_pre)
+
+
+def linear_dx(dy, w, *, gelu_pre=None):
+    """dy [N, out] bf16, w [out, in] bf16 -> dy w [N, in] bf16; times gelu'(gelu_pre) when given."""
+    n, o = dy.shape
+    k = w.shape[1]
+    dx = torch.empty(n, k, device=dy.device, dtype=torch.bfloat16)
+    return gemm(dy, KCONTIG, w, MNCONTIG, n, k, o, dx,
+                epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre)
+
+
+def linear_dw(dy, x, out=None, accumulate=False):
+    """dy [N, out] bf16, x [N, in] bf16 -> dy^T x [out, in] fp32 (written, or added when accumulate)."""
+    n, o = dy.shape
+    k = x.shape[1]
+    if out is None:
+        out = torch.empty(o, k, device=dy.device, dtype=torch.float32)
+    return gemm(dy, MNCONTIG, x, MNCONTIG, o, k, n, out, accumulate=accumulate)

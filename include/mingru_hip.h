@@ -187,6 +187,49 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
                      float bias_correction2, float eps, float weight_decay,
                      float ckp1, float y_lr, float lr, void* stream);
 
+/* ------------------------------------------------------------------------
+ * bf16 matrix product on MFMA with fp32 accumulation, plus fused epilogues.
+ *
+ * Replaces the nn.Linear products of the hot path and their autograd
+ * backward: to_hidden_and_gate (reference mingru/minGRU.py:45), to_out
+ * (:71), the FeedForward Linear-GELU-Linear (mingru/minLM.py:17-23, :130)
+ * and to_logits (mingru/minLM.py:75, :138).
+ *
+ *   C[m, n] (=|+=) epilogue( sum_k A(m, k) B(k, n) ),  0 <= m < M, n < N, k < K
+ * Operand layouts (bf16):
+ *   MG_KCONTIG : element (row, k) at p + row * ld + k  (A = X [M, K]; B = W [N, K])
+ *   MG_MNCONTIG: element (row, k) at p + k * ld + row  (A = dY as dY^T; B = X as X^T)
+ * so Y = X W^T is (A = X, KCONTIG; B = W, KCONTIG), dX = dY W is
+ * (A = dY, KCONTIG; B = W, MNCONTIG) and dW = dY^T X is (A = dY, MNCONTIG;
+ * B = X, MNCONTIG) with K = number of rows (tokens).
+ * C: [M, N] row-major (ldc), fp32 or bf16 (RNE).
+ * Epilogues:
+ *   MG_EPI_NONE       C = acc
+ *   MG_EPI_BIAS       C = acc + bias[n]                   (bias fp32 [N])
+ *   MG_EPI_BIAS_GELU  aux = bf16(acc + bias[n]); C = gelu(aux)   (bf16 C, aux [M, N] bf16, ldaux)
+ *   MG_EPI_GELU_GRAD  C = acc * gelu'(aux[m][n])                  (bf16 C, aux as written above)
+ *   gelu(x) = x/2 (1 + erf(x/sqrt(2))), nn.GELU()'s exact form.
+ * accumulate = 1 (fp32 C, no epilogue): C += A B. fp32 outputs with few
+ *   output tiles are split along K across workgroups that add with fp32
+ *   atomics; the library zeroes C first unless accumulating.
+ * Requirements: N % 8 == 0; K % 8 == 0 if an operand is K-contiguous;
+ *   M % 8 == 0 if A is MN-contiguous; lda, ldb, ldaux % 8 == 0; ldc % 8 == 0
+ *   (bf16 C) or % 4 == 0 (fp32 C); A, B, C, bias, aux 16-byte aligned; each
+ *   operand spans less than 2 GiB.
+ * ---------------------------------------------------------------------- */
+#define MG_KCONTIG 0
+#define MG_MNCONTIG 1
+#define MG_EPI_NONE 0
+#define MG_EPI_BIAS 1
+#define MG_EPI_BIAS_GELU 2
+#define MG_EPI_GELU_GRAD 3
+
+int mg_gemm(int a_layout, const void* A, int64_t lda,
+            int b_layout, const void* B, int64_t ldb,
+            int M, int N, int K,
+            int epilogue, const float* bias, void* aux, int64_t ldaux,
+            int c_dtype, void* C, int64_t ldc, int accumulate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,139 @@
+"""GPU parity of the bf16 MFMA products (mg_gemm) against float64 products
+of the same bf16 inputs (plain torch on the CPU) and, at full model sizes,
+against torch's float32 product on the GPU.
+
+Tolerances: fp32 outputs 1e-5 relative (Frobenius), per-element within
+1e-5 of the row scale; bf16 outputs are one bf16 rounding of the fp32 value
+(relative 2^-8 per element, plus the fp32 accumulation error).
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _operand(rows, k, layout, gen, scale=1.0, pad=0):
+    """bf16 operand with logical shape [rows, k] stored K- or MN-contiguous (pad = extra leading-dim room)."""
+    from gruboros_amd.gemm import KCONTIG
+
+    logical = (torch.randn(rows, k, generator=gen, dtype=torch.float64) * scale).to(torch.bfloat16)
+    if layout == KCONTIG:
+        store = torch.zeros(rows, k + pad, dtype=torch.bfloat16)
+        store[:, :k] = logical
+        dev = store.to(DEV)[:, :k]
+    else:
+        store = torch.zeros(k, rows + pad, dtype=torch.bfloat16)
+        store[:, :rows] = logical.t()
+        dev = store.to(DEV)[:, :rows]
+    return logical.double(), dev
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+@pytest.mark.parametrize("a_layout,b_layout", [(0, 0), (0, 1), (1, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (37, 64, 200), (128, 256, 64), (300, 520, 1024), (1000, 136, 72),
+                                   (513, 264, 8)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_layouts(a_layout, b_layout, M, N, K, out_dtype):
+    from gruboros_amd.gemm import gemm
+
+    if a_layout == 1 and M % 8:
+        M = (M + 7) // 8 * 8
+    gen = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    a64, a = _operand(M, K, a_layout, gen, pad=8)
+    b64, b = _operand(N, K, b_layout, gen, pad=8)
+    ref = a64 @ b64.t()
+    out = torch.full((M, N + 8), 7.0, device=DEV, dtype=out_dtype)[:, :N]
+    gemm(a, a_layout, b, b_layout, M, N, K, out)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    if out_dtype == torch.float32:
+        assert _rel(got, ref) < 1e-5
+    else:
+        # one rounding to bf16 of a value accurate to ~1e-6
+        err = (got - ref).abs()
+        assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+    # the padding columns of C are untouched
+    assert bool((torch.full((M, 8), 7.0, device=DEV, dtype=out_dtype) ==
+                 out.as_strided((M, 8), (N + 8, 1), out.storage_offset() + N)).all())
+
+
+def test_gemm_epilogues():
+    from gruboros_amd.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD, KCONTIG, MNCONTIG, gemm
+
+    gen = torch.Generator().manual_seed(5)
+    M, N, K = 777, 264, 136
+    a64, a = _operand(M, K, KCONTIG, gen)
+    b64, b = _operand(N, K, KCONTIG, gen, scale=0.2)
+    bias = torch.randn(N, generator=gen, dtype=torch.float64).float()
+    acc = a64 @ b64.t()
+    # bias, fp32 and bf16 outputs
+    for dt in (torch.float32, torch.bfloat16):
+        out = torch.empty(M, N, device=DEV, dtype=dt)
+        gemm(a, KCONTIG, b, KCONTIG, M, N, K, out, epilogue=EPI_BIAS, bias=bias.to(DEV))
+        assert _rel(out, acc + bias.double()) < (1e-5 if dt == torch.float32 else 4e-3)
+    # bias + GELU: aux = bf16(acc + bias), out = gelu(aux)
+    aux = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(a, KCONTIG, b, KCONTIG, M, N, K, out, epilogue=EPI_BIAS_GELU, bias=bias.to(DEV), aux=aux)
+    pre = acc + bias.double()
+    assert _rel(aux, pre) < 4e-3
+    gelu_of_aux = torch.nn.functional.gelu(aux.double().cpu())
+    assert _rel(out, gelu_of_aux) < 4e-3
+    # GELU gradient: out = (dy w) * gelu'(aux)
+    dy64, dy = _operand(M, N, KCONTIG, gen)
+    w64 = b64  # [N, K]; dX = dY W: A = dy (K-contig over N), B(k=n, j) = w[n][j] -> MN-contig
+    dx = torch.empty(M, K, device=DEV, dtype=torch.bfloat16)
+    aux2 = aux[:, :K].contiguous() if K <= N else None
+    gemm(dy, KCONTIG, b, MNCONTIG, M, K, N, dx, epilogue=EPI_GELU_GRAD, aux=aux2)
+    x = aux2.double().cpu().requires_grad_(True)
+    torch.nn.functional.gelu(x).backward(torch.ones_like(x))
+    ref = (dy64 @ w64) * x.grad
+    assert _rel(dx, ref) < 4e-3
+
+
+def test_gemm_accumulate_and_split():
+    """fp32 dW-shaped product (long K): split along K with atomics; accumulate adds to C."""
+    from gruboros_amd.gemm import linear_dw
+
+    gen = torch.Generator().manual_seed(9)
+    T, O, I = 5000, 264, 136
+    dy = (torch.randn(T, O, generator=gen, dtype=torch.float64)).to(torch.bfloat16)
+    x = (torch.randn(T, I, generator=gen, dtype=torch.float64)).to(torch.bfloat16)
+    ref = dy.double().t() @ x.double()
+    out = linear_dw(dy.to(DEV), x.to(DEV))
+    assert _rel(out, ref) < 1e-5
+    base = torch.randn(O, I, generator=gen).float()
+    acc = base.to(DEV)
+    linear_dw(dy.to(DEV), x.to(DEV), out=acc, accumulate=True)
+    assert _rel(acc, ref + base.double()) < 1e-5
+
+
+@pytest.mark.parametrize("which", ["hg_fwd", "hg_dx", "hg_dw", "ff1_fwd", "ff2_dw", "logits_fwd"])
+def test_gemm_model_sizes(which):
+    """cfg3 shapes (16376 tokens, d1024, ff 4096, vocab 256) vs torch's fp32 product on the GPU."""
+    from gruboros_amd.gemm import linear_dw, linear_dx, linear_fwd
+
+    g = torch.Generator(device=DEV).manual_seed(3)
+    T = 16376
+    shapes = {"hg_fwd": (1024, 2048), "hg_dx": (1024, 2048), "hg_dw": (1024, 2048), "ff1_fwd": (1024, 4096),
+              "ff2_dw": (4096, 1024), "logits_fwd": (1024, 256)}
+    fin, fout = shapes[which]
+    x = torch.randn(T, fin, device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn(fout, fin, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    dy = torch.randn(T, fout, device=DEV, generator=g).to(torch.bfloat16)
+    if which.endswith("fwd"):
+        got = linear_fwd(x, w, out_dtype=torch.float32)
+        ref = x.float() @ w.float().t()
+    elif which.endswith("dx"):
+        got = linear_dx(dy, w).float()
+        ref = dy.float() @ w.float()
+    else:
+        got = linear_dw(dy, x)
+        ref = dy.float().t() @ x.float()
+    tol = 1e-5 if got.dtype == torch.float32 and not which.endswith("dx") else 4e-3
+    assert _rel(got, ref) < tol
