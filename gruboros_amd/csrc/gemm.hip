@@ -46,12 +46,6 @@ namespace gemm {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#ifndef GEMM_WM
-#define GEMM_WM 2
-#endif
-#ifndef GEMM_WN
-#define GEMM_WN 4
-#endif
 constexpr int BK = 64;
 
 struct Params {
@@ -97,28 +91,31 @@ __device__ __forceinline__ uint4 load16(const Operand& o, uint32_t off, bool ok)
 template <int R, bool KMAJ, int T>
 struct Loader;
 
-// K-contiguous rows: 8 chunks of 16 bytes per row, T/8 rows per pass.
+// K-contiguous rows go straight from memory into LDS (buffer_load ... lds):
+// one wave instruction fills 64 consecutive 16-byte LDS chunks, i.e. 8 rows;
+// lane l takes the global chunk whose swizzled position is l, so each row is
+// still read as one contiguous 128-byte segment. No registers, no LDS write
+// instructions; completion is waited for with vmcnt before the barrier.
 template <int R, int T>
 struct Loader<R, true, T> {
-  static constexpr int kN = R * 8 / T;  // 16-byte loads per thread
-  static_assert(kN >= 1 && R * 8 % T == 0, "tile rows vs threads");
-  uint4 v[kN];
+  static constexpr int kPerWave = R * 8 / 64 / (T / 64);  // wave instructions per tile and wave
+  static_assert(kPerWave >= 1 && R * 8 % T == 0, "tile rows vs threads");
 
-  __device__ __forceinline__ void load(const Operand& o, int r0, int rmax, int k0, int K) {
-    const int c = threadIdx.x & 7;
-    const int kk = k0 + c * 8;
-    const uint32_t base = static_cast<uint32_t>(r0 + (threadIdx.x >> 3)) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int, int k0, int K) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < kN; ++i) v[i] = load16(o, base + static_cast<uint32_t>(T / 8 * i) * o.ld2, kk < K);
-  }
-  __device__ __forceinline__ void store(uint4* __restrict__ s) const {
-    const int c = threadIdx.x & 7;
-#pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int r = (threadIdx.x >> 3) + T / 8 * i;
-      s[r * 8 + swz(r, c)] = v[i];
+    for (int i = 0; i < kPerWave; ++i) {
+      const int b = wave * kPerWave + i;
+      const int r = b * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);  // global chunk stored at LDS chunk lane & 7
+      const int kk = k0 + c * 8;
+      const uint32_t off = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
+                                               16, kk < K ? off : kOutOfRange, 0, 0, 0);
     }
   }
+  __device__ __forceinline__ void store(uint4*) {}
+  static constexpr int kWrites = 0;
 };
 
 // MN-contiguous rows: thread t loads KG consecutive k-rows of 8 consecutive
@@ -131,16 +128,22 @@ struct Loader<R, false, T> {
   static_assert(KG == 2 || KG == 4 || KG == 8, "tile rows vs threads");
   uint4 v[KG];
 
-  __device__ __forceinline__ void load(const Operand& o, int r0, int rmax, int k0, int) {
+  static constexpr int kWrites = 8;  // LDS write instructions per store
+
+  __device__ __forceinline__ void load(const Operand& o, uint4*, int r0, int rmax, int k0, int) {
     const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
     const int r = r0 + rb * 8;
     const uint32_t base = static_cast<uint32_t>(k0 + kb * KG) * o.ld2 + static_cast<uint32_t>(r) * 2u;
 #pragma unroll
     for (int i = 0; i < KG; ++i) v[i] = load16(o, base + static_cast<uint32_t>(i) * o.ld2, r < rmax);
   }
-  __device__ __forceinline__ void store(uint4* __restrict__ s) const {
+  __device__ __forceinline__ void store(uint4* __restrict__ s) {
     const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
     const int c = kb * KG / 8, off = (kb * KG % 8) * 2;  // chunk and byte offset of this thread's k-range
+    // Pin the transposes here: without this the compiler moves them up to
+    // the loads, which makes the wave wait for the loads before its MFMAs.
+#pragma unroll
+    for (int i = 0; i < KG; ++i) asm volatile("" : "+v"(v[i].x), "+v"(v[i].y), "+v"(v[i].z), "+v"(v[i].w));
     const uint32_t* w = reinterpret_cast<const uint32_t*>(v);  // w[4 i + d]: k-row i, dword d
     unsigned char* sb = reinterpret_cast<unsigned char*>(s);
 #pragma unroll
@@ -219,11 +222,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   Loader<BM, AK, T> la;
   Loader<BN, BKM, T> lb;
   if (kt0 < kt1) {
-    la.load(oa, m0, p.M, kt0 * BK, p.K);
-    lb.load(ob, n0, p.N, kt0 * BK, p.K);
+    la.load(oa, smem, m0, p.M, kt0 * BK, p.K);
+    lb.load(ob, smem + BM * 8, n0, p.N, kt0 * BK, p.K);
     la.store(smem);
     lb.store(smem + BM * 8);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   // LDS row of this lane's fragment for block i / j
@@ -233,16 +237,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
   for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32 + L;
 
+  // One basic block per k-tile, so the scheduler can interleave: the global
+  // loads of tile k+1 are issued first (unconditionally: past the end of K
+  // they read as zero, and the stage they fill is never read), the LDS
+  // fragment reads of step s+1 go ahead of the MFMAs of step s, and the LDS
+  // writes of tile k+1 are spread between the MFMAs of the last step.
   for (int kt = kt0; kt < kt1; ++kt) {
     const int st = (kt - kt0) & 1;
-    const bool more = kt + 1 < kt1;
-    if (more) {
-      la.load(oa, m0, p.M, (kt + 1) * BK, p.K);
-      lb.load(ob, n0, p.N, (kt + 1) * BK, p.K);
-    }
     const uint4* As = smem + st * kStage;
     const uint4* Bs = As + BM * 8;
-    // fragments of k-step s+1 are read while the MFMAs of step s run
+    uint4* nxt = smem + (st ^ 1) * kStage;
+    la.load(oa, nxt, m0, p.M, (kt + 1) * BK, p.K);
+    lb.load(ob, nxt + BM * 8, n0, p.N, (kt + 1) * BK, p.K);
     bf16x8 af[2][MB], bfr[2][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) af[0][i] = __builtin_bit_cast(bf16x8, As[arow[i] * 8 + swz(arow[i], half)]);
@@ -258,20 +264,28 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = __builtin_bit_cast(bf16x8, Bs[brow[j] * 8 + swz(brow[j], c)]);
       }
-      // keep the reads of step s+1 ahead of the products of step s
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+      if (s == BK / 16 - 1) {
+        la.store(nxt);
+        lb.store(nxt + BM * 8);
+        // spread the LDS writes of register-staged operands between the MFMAs
+        constexpr int kW = decltype(la)::kWrites + decltype(lb)::kWrites;
+        if constexpr (kW > 0) {
+#pragma unroll
+          for (int q = 0; q < MB * NB; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x200, (kW + MB * NB - 1) / (MB * NB), 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
-      uint4* nxt = smem + (st ^ 1) * kStage;
-      la.store(nxt);
-      lb.store(nxt + BM * 8);
-    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
@@ -396,13 +410,17 @@ int dispatch_epi(const Params& p, int epi, int c_dtype, bool atomic, int splits,
   return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
 }
 
-template <int BM, int BN, int WM, int WN>
+// 256 x 256 tiles: 8 waves (two per SIMD) when both operands stream straight
+// into LDS; 4 waves (one per SIMD, 512 registers each) when an operand is
+// transposed through registers.
+template <int BM, int BN>
 int dispatch_layout(const Params& p, bool ak, bool bk, int epi, int c_dtype, bool atomic, int splits,
                     hipStream_t s) {
-  if (ak && bk) return dispatch_epi<BM, BN, WM, WN, true, true>(p, epi, c_dtype, atomic, splits, s);
-  if (ak && !bk) return dispatch_epi<BM, BN, WM, WN, true, false>(p, epi, c_dtype, atomic, splits, s);
-  if (!ak && !bk) return dispatch_epi<BM, BN, WM, WN, false, false>(p, epi, c_dtype, atomic, splits, s);
-  return dispatch_epi<BM, BN, WM, WN, false, true>(p, epi, c_dtype, atomic, splits, s);
+  constexpr bool kBig = BM * BN >= 256 * 256;
+  if (ak && bk) return dispatch_epi<BM, BN, 2, kBig ? 4 : 2, true, true>(p, epi, c_dtype, atomic, splits, s);
+  if (ak && !bk) return dispatch_epi<BM, BN, 2, 2, true, false>(p, epi, c_dtype, atomic, splits, s);
+  if (!ak && !bk) return dispatch_epi<BM, BN, 2, 2, false, false>(p, epi, c_dtype, atomic, splits, s);
+  return dispatch_epi<BM, BN, 2, 2, false, true>(p, epi, c_dtype, atomic, splits, s);
 }
 
 }  // namespace gemm
@@ -472,6 +490,6 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     hipLaunchKernelGGL(gemm::zero_f32_kernel, dim3(1024), dim3(256), 0, s, static_cast<float*>(C), int64_t(M), N, ldc);
     if (int rc = check_launch(fn)) return rc;
   }
-  return big ? gemm::dispatch_layout<256, 256, GEMM_WM, GEMM_WN>(p, ak, bk, epilogue, c_dtype, atomic, splits, s)
-             : gemm::dispatch_layout<128, 128, 2, 2>(p, ak, bk, epilogue, c_dtype, atomic, splits, s);
+  return big ? gemm::dispatch_layout<256, 256>(p, ak, bk, epilogue, c_dtype, atomic, splits, s)
+             : gemm::dispatch_layout<128, 128>(p, ak, bk, epilogue, c_dtype, atomic, splits, s);
 }
