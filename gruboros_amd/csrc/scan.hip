@@ -275,6 +275,48 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
 
 // ------------------------------------------------------------------ backward
 
+// Four channels of one row kept as loaded (bf16 stays packed, two per
+// register) until each value is needed, to keep the backward's register
+// footprint small enough for six waves per SIMD.
+template <typename T> struct Raw4;
+template <> struct Raw4<bf16_t> {
+  uint2 r;
+  __device__ __forceinline__ static Raw4 load(const bf16_t* p) { return Raw4{*reinterpret_cast<const uint2*>(p)}; }
+  __device__ __forceinline__ static Raw4 fill(float f) {
+    const uint32_t b = f32_to_bf16(f);
+    return Raw4{make_uint2(b | (b << 16), b | (b << 16))};
+  }
+  __device__ __forceinline__ float get(int j) const {
+    const uint32_t w = j < 2 ? r.x : r.y;
+    return (j & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  }
+};
+template <> struct Raw4<float> {
+  float4 r;
+  __device__ __forceinline__ static Raw4 load(const float* p) { return Raw4{*reinterpret_cast<const float4*>(p)}; }
+  __device__ __forceinline__ static Raw4 fill(float f) { return Raw4{make_float4(f, f, f, f)}; }
+  __device__ __forceinline__ float get(int j) const { return j == 0 ? r.x : j == 1 ? r.y : j == 2 ? r.z : r.w; }
+};
+
+template <typename T, int kRows>
+__device__ __forceinline__ void load_raw(const T* base, int off, int ld, bool ok, int nrows, float pad,
+                                         Raw4<T> (&v)[kRows]) {
+  if (ok && nrows >= kRows) {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) v[i] = Raw4<T>::load(base + (off + i * ld));
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+      v[i] = (ok && i < nrows) ? Raw4<T>::load(base + (off + i * ld)) : Raw4<T>::fill(pad);
+  }
+}
+
+// Two passes over each thread's 4-step run, with the inputs held raw:
+//   1. a_t and z_t from the gate (kept), the run's reverse map for mu_t =
+//      a_t lambda_t, lambda_t = dh_t + mu_{t+1}; scan across runs and tiles.
+//   2. lambda_t down the run, then up the run with h_{t-1} rebuilt in fp32
+//      from the state entering the run: g~, g' from the hidden input,
+//      dgate = lambda a z (g~ - h_{t-1}), dhidden = lambda z g'(hidden).
 template <typename Tin, typename Th>
 __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
@@ -301,10 +343,12 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   const int64_t in_tile = b * in_sb + static_cast<int64_t>(k) * kBwdTileRows * in_ld + d0;
   const int in_off = s * kRows * ild + cl * kVec;
 
-  f4 hv[kRows], gv[kRows], dv[kRows];
-  load_run<Tin, kRows>(hidden + in_tile, gate + in_tile, in_off, ild, ok, g.T - t0, hv, gv);
-  load_grad<Th, kRows>(dh + (b * g_sb + static_cast<int64_t>(k) * kBwdTileRows * g_ld + d0),
-                       s * kRows * gld + cl * kVec, gld, ok, g.T - t0, dv);
+  Raw4<Tin> hr[kRows], gr[kRows];
+  Raw4<Th> dr[kRows];
+  load_raw<Tin, kRows>(gate + in_tile, in_off, ild, ok, g.T - t0, -INFINITY, gr);
+  load_raw<Tin, kRows>(hidden + in_tile, in_off, ild, ok, g.T - t0, 0.0f, hr);
+  load_raw<Th, kRows>(dh + (b * g_sb + static_cast<int64_t>(k) * kBwdTileRows * g_ld + d0), s * kRows * gld + cl * kVec,
+                      gld, ok, g.T - t0, 0.0f, dr);
   // h_{t0-1}: the fp32 checkpoint when given, else the forward output of the
   // row before the run (exact for fp32 outputs); h0 (or 0) at t = 0.
   f4 hc = io4<float>::fill(0.0f);
@@ -315,40 +359,34 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     else if (h0)
       hc = io4<float>::load(h0 + c);
   }
+  // gradient arriving at h_last joins dh of the last row
+  f4 dl = io4<float>::fill(0.0f);
+  int il = -1;
   if (ok && dh_last && t0 <= g.T - 1 && g.T - 1 < t0 + kRows) {
-    const f4 dl = io4<float>::load(dh_last + c);
-#pragma unroll
-    for (int i = 0; i < kRows; ++i)
-      if (t0 + i == g.T - 1) {
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) dv[i].v[j] += dl.v[j];
-      }
+    dl = io4<float>::load(dh_last + c);
+    il = g.T - 1 - t0;
   }
 
-  // Per element: a, q = z g'(hidden) (dhidden's factor) and
-  // p = a z (g~ - h_{t-1}) (dgate's factor), with h_{t-1} rebuilt along the
-  // run in fp32.
-  float a[kRows][kVec], q[kRows][kVec], p[kRows][kVec];
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      float zz, vv;
-      bwd_coeffs(gv[i].v[j], hv[i].v[j], a[i][j], zz, vv, q[i][j]);
-      p[i][j] = a[i][j] * (vv - zz * hc.v[j]);
-      hc.v[j] = a[i][j] * hc.v[j] + vv;
-    }
-  }
-
-  // Reverse run map mu -> A mu + M, mu_t = a_t lambda_t, lambda_t = gh_t + mu_{t+1}.
+  float a[kRows][kVec], z[kRows][kVec];
   f4 A, M;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) { A.v[j] = 1.0f; M.v[j] = 0.0f; }
 #pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const float e = exp2_raw(fminf(gr[i].get(j) * -kLog2e, kMaxExp2));
+      z[i][j] = __builtin_amdgcn_rcpf(1.0f + e);
+      a[i][j] = e * z[i][j];
+    }
+  }
+  // Reverse run map mu -> A mu + M.
+#pragma unroll
   for (int i = kRows - 1; i >= 0; --i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      M.v[j] = a[i][j] * (dv[i].v[j] + M.v[j]);
+      const float dv = dr[i].get(j) + (i == il ? dl.v[j] : 0.0f);
+      M.v[j] = a[i][j] * (dv + M.v[j]);
       A.v[j] = A.v[j] * a[i][j];
     }
   }
@@ -380,24 +418,41 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < kVec; ++j) mu.v[j] = pa.v[j] * mu.v[j] + pm.v[j];
   }
+  float lam[kRows][kVec];
+#pragma unroll
+  for (int i = kRows - 1; i >= 0; --i) {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      lam[i][j] = dr[i].get(j) + (i == il ? dl.v[j] : 0.0f) + mu.v[j];
+      mu.v[j] = a[i][j] * lam[i][j];
+    }
+  }
+  if (dh0 && t0 == 0) io4<float>::store(dh0 + c, mu);
+
   Tin* dhb = dhidden + in_tile;
   Tin* dgb = dgate + in_tile;
 #pragma unroll
-  for (int i = kRows - 1; i >= 0; --i) {
+  for (int i = 0; i < kRows; ++i) {
     f4 og, oh;
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float lam = dv[i].v[j] + mu.v[j];
-      og.v[j] = lam * p[i][j];
-      oh.v[j] = lam * q[i][j];
-      mu.v[j] = a[i][j] * lam;
+      // g~ = g(hidden), gp = g'(hidden) (0 at hidden = 0, as autograd of relu gives)
+      const float x = hr[i].get(j);
+      const float e2 = exp2_raw(fabsf(x) * -kLog2e);
+      const float r2 = __builtin_amdgcn_rcpf(1.0f + e2);
+      const float sig = e2 * r2;  // sigmoid(x) for x < 0
+      const float gt = x >= 0.0f ? x + 0.5f : sig;
+      const float gp = x > 0.0f ? 1.0f : (x < 0.0f ? sig * r2 : 0.0f);
+      const float vv = z[i][j] * gt;
+      og.v[j] = lam[i][j] * (a[i][j] * (vv - z[i][j] * hc.v[j]));
+      oh.v[j] = lam[i][j] * (z[i][j] * gp);
+      hc.v[j] = a[i][j] * hc.v[j] + vv;
     }
     if (t0 + i < g.T) {
       io4<Tin>::store_nt(dgb + (in_off + i * ild), og);
       io4<Tin>::store_nt(dhb + (in_off + i * ild), oh);
     }
   }
-  if (dh0 && t0 == 0) io4<float>::store(dh0 + c, mu);
 }
 
 // ------------------------------------------------------------------ host
