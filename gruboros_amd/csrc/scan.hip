@@ -83,39 +83,25 @@ __device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters,
 
 // Walk from tile k + step in direction `step` (-1: earlier tiles, forward
 // scan; +1: later tiles, backward scan) until an inclusive prefix is found,
-// folding aggregates on the way. Returns the state entering tile k.
-__device__ __forceinline__ f4 look_back(const uint64_t* status, int64_t BD, int64_t c, int k, int step) {
-  float accA[kVec], accV[kVec], carry[kVec];
-  int kk[kVec];
-  unsigned done = 0;
-#pragma unroll
-  for (int j = 0; j < kVec; ++j) { accA[j] = 1.0f; accV[j] = 0.0f; carry[j] = 0.0f; kk[j] = k + step; }
-  while (done != (1u << kVec) - 1u) {
-    uint64_t w[kVec];
-#pragma unroll
-    for (int j = 0; j < kVec; ++j)
-      w[j] = (done >> j) & 1u ? 0ull : poll_word(status + static_cast<int64_t>(kk[j]) * BD + c + j);
-    bool progress = false;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      if ((done >> j) & 1u) continue;
-      const uint32_t tag = static_cast<uint32_t>(w[j]);
-      const float val = __uint_as_float(static_cast<uint32_t>(w[j] >> 32));
-      if (tag == kTagIncl) {
-        carry[j] = accA[j] * val + accV[j];
-        done |= 1u << j;
-        progress = true;
-      } else if (tag & kTagAggBit) {
-        const float Aj = __uint_as_float(tag & ~kTagAggBit);
-        accV[j] = accA[j] * val + accV[j];
-        accA[j] = accA[j] * Aj;
-        kk[j] += step;
-        progress = true;
-      }
+// folding aggregates on the way. Returns the state entering tile k of
+// channel c (one channel per lane).
+__device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step) {
+  float accA = 1.0f, accV = 0.0f;
+  const uint64_t* w = status + static_cast<int64_t>(k + step) * BD + c;
+  const int64_t dw = step * BD;
+  while (true) {
+    const uint64_t x = poll_word(w);
+    const uint32_t tag = static_cast<uint32_t>(x);
+    const float val = __uint_as_float(static_cast<uint32_t>(x >> 32));
+    if (tag == kTagIncl) return accA * val + accV;
+    if (tag & kTagAggBit) {
+      accV = accA * val + accV;
+      accA = accA * __uint_as_float(tag & ~kTagAggBit);
+      w += dw;
+    } else {
+      __builtin_amdgcn_s_sleep(2);
     }
-    if (!progress) __builtin_amdgcn_s_sleep(2);
   }
-  return f4{{carry[0], carry[1], carry[2], carry[3]}};
 }
 
 // Load one run of rows. hb/gb are tile base pointers (wave-uniform), off is
@@ -234,22 +220,21 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
   }
   const int buf = scan_runs<kSubs, false>(s_maps, s, cl, A, V);
 
-  if (s == 0 && ok) {
-    const f4 TA = s_maps.A[buf][kSubs - 1][cl], TV = s_maps.V[buf][kSubs - 1][cl];
-    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c;
-    f4 carry;
+  // Wave 0 links the tile into its chain, one channel per lane: lane
+  // (s, cl) takes channel cl * 4 + s.
+  if (tid < 64 && ok) {
+    const float TA = reinterpret_cast<const float*>(&s_maps.A[buf][kSubs - 1][cl])[s];
+    const float TV = reinterpret_cast<const float*>(&s_maps.V[buf][kSubs - 1][cl])[s];
+    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + s;
+    float carry;
     if (k == 0) {
-      carry = h0 ? io4<float>::load(h0 + c) : io4<float>::fill(0.0f);
+      carry = h0 ? h0[c + s] : 0.0f;
     } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) publish_agg(st + j, TA.v[j], TV.v[j]);
-      carry = look_back(status, g.BD, c, k, -1);
+      publish_agg(st, TA, TV);
+      carry = look_back1(status, g.BD, c + s, k, -1);
     }
-    if (k + 1 < g.ntiles) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) publish_incl(st + j, TA.v[j] * carry.v[j] + TV.v[j]);
-    }
-    s_carry[cl] = carry;
+    if (k + 1 < g.ntiles) publish_incl(st, TA * carry + TV);
+    reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
   }
   __syncthreads();
   if (!ok) return;
@@ -392,22 +377,19 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   }
   const int buf = scan_runs<kSubs, true>(s_maps, s, cl, A, M);
 
-  if (s == 0 && ok) {
-    const f4 TA = s_maps.A[buf][0][cl], TM = s_maps.V[buf][0][cl];
-    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c;
-    f4 carry;
-    if (k == g.ntiles - 1) {
-      carry = io4<float>::fill(0.0f);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) publish_agg(st + j, TA.v[j], TM.v[j]);
-      carry = look_back(status, g.BD, c, k, +1);
+  // Wave 0 links the tile into its chain, one channel per lane: lane
+  // (s, cl) takes channel cl * 4 + s.
+  if (tid < 64 && ok) {
+    const float TA = reinterpret_cast<const float*>(&s_maps.A[buf][0][cl])[s];
+    const float TM = reinterpret_cast<const float*>(&s_maps.V[buf][0][cl])[s];
+    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + s;
+    float carry = 0.0f;
+    if (k != g.ntiles - 1) {
+      publish_agg(st, TA, TM);
+      carry = look_back1(status, g.BD, c + s, k, +1);
     }
-    if (k > 0) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) publish_incl(st + j, TA.v[j] * carry.v[j] + TM.v[j]);
-    }
-    s_carry[cl] = carry;
+    if (k > 0) publish_incl(st, TA * carry + TM);
+    reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
   }
   __syncthreads();
   if (!ok) return;
