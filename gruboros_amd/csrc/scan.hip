@@ -21,9 +21,10 @@
 //     block) takes tickets from its own atomic counter, so a tile only ever
 //     waits on tiles of its chain that were started before it.
 //   * The backward walks tiles in reverse time order with the adjoint
-//     recurrence. It needs h_{t-1}: it reads the state entering each 4-step
-//     run once (the forward's fp32 checkpoint when the output is bf16, else
-//     the fp32 output itself) and rebuilds the run's states in fp32 from it.
+//     recurrence. It needs h_{t-1}: it reads the state entering each 8-step
+//     pair of runs once (the forward's fp32 checkpoint when the output is
+//     bf16, else the fp32 output itself) and rebuilds the states in fp32
+//     from it; the first run of a pair hands its final state to the second.
 //     (A bf16-rounded state would not do: at small gates dgate depends on
 //     g(hidden) - h_{t-1}, a difference of two nearly equal numbers.)
 
@@ -49,9 +50,11 @@ constexpr int kFwdSubs = 16, kFwdRows = 8;
 constexpr int kBwdSubs = MG_SCAN_BWD_SUBS, kBwdRows = MG_SCAN_BWD_ROWS;
 constexpr int kFwdTileRows = kFwdSubs * kFwdRows;
 // fp32 state checkpoints (optional forward output, backward input): the state
-// after every kCkptRows-th step, i.e. the state entering each backward run.
-constexpr int kCkptRows = 4;
-static_assert(kBwdRows == kCkptRows && kFwdRows % kCkptRows == 0, "checkpoint spacing");
+// after every kCkptRows-th step, i.e. the state entering every second
+// backward run; the run in between gets its entering state from its
+// neighbour through LDS.
+constexpr int kCkptRows = 8;
+static_assert(2 * kBwdRows == kCkptRows && kFwdRows % kCkptRows == 0, "checkpoint spacing");
 constexpr int kBwdTileRows = kBwdSubs * kBwdRows;
 
 struct Geometry {
@@ -314,10 +317,14 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   __shared__ uint32_t s_ticket;
   __shared__ RunMaps<kSubs> s_maps;
   __shared__ f4 s_carry[kChLanes];
+  __shared__ f4 s_hmid[kSubs / 2][kChLanes];
 
+  // Runs 0, 2, 4, ... (each the first of a checkpoint interval) sit in the
+  // first half of the workgroup and 1, 3, 5, ... in the second, so the extra
+  // work of the first runs fills whole waves.
   const int tid = threadIdx.x;
   const int cl = tid % kChLanes;
-  const int s = tid / kChLanes;
+  const int s = ((tid / kChLanes) % (kSubs / 2)) * 2 + tid / (kChLanes * kSubs / 2);
   int k, b, d0;
   take_tile(g, counters, &s_ticket, true, k, b, d0);
   const int d = d0 + cl * kVec;
@@ -334,10 +341,13 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   load_raw<Tin, kRows>(hidden + in_tile, in_off, ild, ok, g.T - t0, 0.0f, hr);
   load_raw<Th, kRows>(dh + (b * g_sb + static_cast<int64_t>(k) * kBwdTileRows * g_ld + d0), s * kRows * gld + cl * kVec,
                       gld, ok, g.T - t0, 0.0f, dr);
-  // h_{t0-1}: the fp32 checkpoint when given, else the forward output of the
-  // row before the run (exact for fp32 outputs); h0 (or 0) at t = 0.
+  // h_{t0-1}: from the fp32 checkpoint for runs starting a checkpoint
+  // interval (the other runs get it from their neighbour below), else the
+  // forward output of the row before the run (exact for fp32 outputs); h0
+  // (or 0) at t = 0.
+  const bool from_left = ckpt && (s & 1);
   f4 hc = io4<float>::fill(0.0f);
-  if (ok && t0 < g.T) {
+  if (ok && t0 < g.T && !from_left) {
     if (t0 > 0)
       hc = ckpt ? io4<float>::load(ckpt + static_cast<int64_t>(t0 / kCkptRows - 1) * g.BD + c)
                 : io4<Th>::load(hout + (b * out_sb + static_cast<int64_t>(t0 - 1) * out_ld + d));
@@ -365,6 +375,21 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
       a[i][j] = e * z[i][j];
     }
   }
+  // The first run of a checkpoint interval passes its final state on.
+  if (ckpt && !(s & 1)) {
+    f4 he = hc;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const float x = hr[i].get(j);
+        const float e2 = exp2_raw(fabsf(x) * -kLog2e);
+        const float gt = x >= 0.0f ? x + 0.5f : e2 * __builtin_amdgcn_rcpf(1.0f + e2);
+        he.v[j] = a[i][j] * he.v[j] + z[i][j] * gt;
+      }
+    }
+    s_hmid[s / 2][cl] = he;
+  }
   // Reverse run map mu -> A mu + M.
 #pragma unroll
   for (int i = kRows - 1; i >= 0; --i) {
@@ -378,18 +403,19 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   const int buf = scan_runs<kSubs, true>(s_maps, s, cl, A, M);
 
   // Wave 0 links the tile into its chain, one channel per lane: lane
-  // (s, cl) takes channel cl * 4 + s.
+  // (q, cl) takes channel cl * 4 + q.
   if (tid < 64 && ok) {
-    const float TA = reinterpret_cast<const float*>(&s_maps.A[buf][0][cl])[s];
-    const float TM = reinterpret_cast<const float*>(&s_maps.V[buf][0][cl])[s];
-    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + s;
+    const int q = tid / kChLanes;
+    const float TA = reinterpret_cast<const float*>(&s_maps.A[buf][0][cl])[q];
+    const float TM = reinterpret_cast<const float*>(&s_maps.V[buf][0][cl])[q];
+    uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + q;
     float carry = 0.0f;
     if (k != g.ntiles - 1) {
       publish_agg(st, TA, TM);
-      carry = look_back1(status, g.BD, c + s, k, +1);
+      carry = look_back1(status, g.BD, c + q, k, +1);
     }
     if (k > 0) publish_incl(st, TA * carry + TM);
-    reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
+    reinterpret_cast<float*>(&s_carry[cl])[q] = carry;
   }
   __syncthreads();
   if (!ok) return;
@@ -400,6 +426,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < kVec; ++j) mu.v[j] = pa.v[j] * mu.v[j] + pm.v[j];
   }
+  if (from_left) hc = s_hmid[s / 2][cl];
   float lam[kRows][kVec];
 #pragma unroll
   for (int i = kRows - 1; i >= 0; --i) {

@@ -24,7 +24,7 @@ def _prep_h0(h0, B, Di, device):
 
 
 def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt=False):
-    """Runs mg_scan_fwd; returns (h, h_last, ckpt). ckpt (fp32 states every 4
+    """Runs mg_scan_fwd; returns (h, h_last, ckpt). ckpt (fp32 states every 8
     steps) is produced when asked for and h is not fp32: the backward needs
     fp32 states."""
     B, T, Di = hidden.shape

@@ -64,8 +64,8 @@ const char* mg_last_error(void);
  * Requirements: Di % 4 == 0, strides % 4 == 0, pointers 8-byte aligned
  *   (bf16) or 16-byte aligned (fp32), 128 * row stride < 2^31.
  * h_last (nullable): fp32 [B, Di], receives h_{T-1}.
- * ckpt (nullable): fp32 [ceil(T/4), B, Di]; ckpt[j] receives h_{4j+3}, the
- *   state entering step 4j+4. mg_scan_bwd reads it instead of h when h is
+ * ckpt (nullable): fp32 [ceil(T/8), B, Di]; ckpt[j] receives h_{8j+7}, the
+ *   state entering step 8j+8. mg_scan_bwd reads it instead of h when h is
  *   bf16 (required there for fp32-accurate gradients).
  * Supported (in_dtype, out_dtype): (BF16, BF16), (F32, F32), (BF16, F32).
  * ---------------------------------------------------------------------- */
@@ -87,8 +87,8 @@ int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
  *   dhidden_t = lambda_t z_t g'(hidden_t)   (g'(0) = 0, as relu'(0) = 0),
  *   dh0       = a_0 lambda_0.
  * h: the forward's output (same layout, dtype out_dtype). h_{t-1} is read
- * once per 4-step run, from ckpt when given (the forward's fp32 checkpoints)
- * else from h, and rebuilt in fp32 inside the run.
+ * once per 8 steps from ckpt when given (the forward's fp32 checkpoints),
+ * else once per 4 steps from h, and rebuilt in fp32 in between.
  * dh: gradient of h, dtype out_dtype, element (b,t,d) at b*g_sb + t*g_ld + d.
  * dh_last (nullable): fp32 [B, Di], gradient of h_last, added to dh_{T-1}.
  * dhidden/dgate: same layout and dtype as hidden/gate (in_sb, in_ld).
