@@ -46,7 +46,10 @@ constexpr int kTileCh = kChLanes * kVec;  // 64 channels per tile
 #define MG_SCAN_BWD_SUBS 16
 #define MG_SCAN_BWD_ROWS 4
 #endif
-constexpr int kFwdSubs = 16, kFwdRows = 8;
+#ifndef MG_SCAN_FWD_SUBS
+#define MG_SCAN_FWD_SUBS 16
+#endif
+constexpr int kFwdSubs = MG_SCAN_FWD_SUBS, kFwdRows = 8;
 constexpr int kBwdSubs = MG_SCAN_BWD_SUBS, kBwdRows = MG_SCAN_BWD_ROWS;
 constexpr int kFwdTileRows = kFwdSubs * kFwdRows;
 // fp32 state checkpoints (optional forward output, backward input): the state
