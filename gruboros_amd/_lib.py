@@ -37,6 +37,9 @@ SIGNATURES = {
                                           _vp]),
     "mg_sf_adamw_chunk_elems": (_c_i64, []),
     "mg_sf_adamw_step": (_c_int, [_vp, _c_int, _c_i64] + [ctypes.c_float] * 8 + [_vp]),
+    "mg_logits_cross_entropy_partials": (_c_int, [_c_i64]),
+    "mg_logits_cross_entropy": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _fp, _vp, _c_int, _c_int, _c_int,
+                                         ctypes.c_float, _vp]),
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp]),
 }

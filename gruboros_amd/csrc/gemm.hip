@@ -11,16 +11,14 @@
 //   MN-contiguous: element (row, k) at p + k * ld + row    (dY^T, X^T for dW)
 // The weight of Y = X W^T is the K-contiguous B (rows = output features).
 //
-// Workgroup tile BM x BN x 64 (BM, BN in {128, 256}), four waves in a 2 x 2
-// grid, each owning (BM/2) x (BN/2) as 32 x 32 MFMA blocks. Operand tiles are
-// staged through LDS as [row][64 k] bf16, 128 bytes a row, with the 16-byte
-// chunk c of row r stored at chunk c ^ ((r ^ (r >> 3)) & 7): the fragment
-// reads (32 consecutive rows, one chunk) and both kinds of tile writes hit
-// 8 distinct chunks per 8 lanes. MN-contiguous operands are loaded as 8 x 8
-// blocks (8 k-rows of 16 bytes) and transposed in registers before the LDS
-// write, so every fragment read is one 16-byte LDS load. Two LDS stages: the
-// global loads of tile k+1 are in flight while tile k is multiplied, and
-// one barrier per k-tile orders the stages.
+// Workgroup tile BM x BN x 64 (BM, BN in {128, 256}), waves in a WM x WN
+// grid, each owning (BM/WM) x (BN/WN) as 32 x 32 MFMA blocks. Operand tiles
+// go from memory straight into LDS (buffer_load ... lds), two stages: the
+// loads of tile k+1 are in flight while tile k is multiplied, one barrier
+// per k-tile. K-contiguous tiles sit in LDS as [row][64 k] (128-byte rows,
+// 16-byte chunk c of row r at chunk c ^ ((r ^ (r >> 3)) & 7)) and a fragment
+// is one 16-byte LDS read; MN-contiguous tiles stay [64 k][rows] and their
+// fragments come through the LDS transpose read (two 8-byte reads).
 //
 // The MFMA is fed the B fragment as its first operand and the A fragment as
 // its second, so a lane's accumulator holds C[m][n..n+3] (4 consecutive
@@ -59,6 +57,7 @@ struct Params {
   int tiles_m, tiles_n;
   int kt_per_split;  // k-tiles per split (gridDim.y splits)
   uint32_t a_span, b_span;  // bytes from A / B to one past their last element
+  uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
 };
 
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 3)) & 7); }
@@ -118,58 +117,83 @@ struct Loader<R, true, T> {
   static constexpr int kWrites = 0;
 };
 
-// MN-contiguous rows: thread t loads KG consecutive k-rows of 8 consecutive
-// tile rows (16 bytes each), transposes the KG x 8 block in registers and
-// writes KG k-values (2 KG bytes) into each of its 8 LDS rows.
+// MN-contiguous operands also go straight into LDS, kept as stored: a tile
+// is [64 k-rows][R] bf16, the 32-byte segment s of k-row r placed at
+// segment s ^ (r & 3). The MFMA fragments (8 consecutive k of one tile row)
+// come back through the LDS transpose read (ds_read_b64_tr_b16): in each
+// group of 16 lanes, lane 4 j + q addresses k-row j, columns 4 q .. 4 q + 3,
+// and lane i receives column i of the 4 k-rows. The swizzle puts the 4
+// k-rows of one read on distinct banks.
 template <int R, int T>
 struct Loader<R, false, T> {
-  static constexpr int kRG = R / 8;          // row groups
-  static constexpr int KG = 8 * R / T;       // k-rows per thread
-  static_assert(KG == 2 || KG == 4 || KG == 8, "tile rows vs threads");
-  uint4 v[KG];
+  static constexpr int kChunksRow = R / 8;                    // 16-byte chunks per k-row
+  static constexpr int kPerWave = 64 * kChunksRow / 64 / (T / 64);
+  static_assert(kPerWave >= 1 && kChunksRow * 64 % T == 0, "tile rows vs threads");
 
-  static constexpr int kWrites = 8;  // LDS write instructions per store
-
-  __device__ __forceinline__ void load(const Operand& o, uint4*, int r0, int rmax, int k0, int) {
-    const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
-    const int r = r0 + rb * 8;
-    const uint32_t base = static_cast<uint32_t>(k0 + kb * KG) * o.ld2 + static_cast<uint32_t>(r) * 2u;
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < KG; ++i) v[i] = load16(o, base + static_cast<uint32_t>(i) * o.ld2, r < rmax);
-  }
-  __device__ __forceinline__ void store(uint4* __restrict__ s) {
-    const int rb = threadIdx.x % kRG, kb = threadIdx.x / kRG;
-    const int c = kb * KG / 8, off = (kb * KG % 8) * 2;  // chunk and byte offset of this thread's k-range
-    // Pin the transposes here: without this the compiler moves them up to
-    // the loads, which makes the wave wait for the loads before its MFMAs.
-#pragma unroll
-    for (int i = 0; i < KG; ++i) asm volatile("" : "+v"(v[i].x), "+v"(v[i].y), "+v"(v[i].z), "+v"(v[i].w));
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(v);  // w[4 i + d]: k-row i, dword d
-    unsigned char* sb = reinterpret_cast<unsigned char*>(s);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // row rb*8+j gets element j of each of the KG k-rows
-      uint32_t od[KG / 2];
-#pragma unroll
-      for (int q = 0; q < KG / 2; ++q) {
-        const uint32_t lo = w[4 * (2 * q) + j / 2], hi = w[4 * (2 * q + 1) + j / 2];
-        od[q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-      }
-      const int r = rb * 8 + j;
-      unsigned char* dst = sb + (r * 8 + swz(r, c)) * 16 + off;
-      if constexpr (KG == 8) *reinterpret_cast<uint4*>(dst) = make_uint4(od[0], od[1], od[2], od[3]);
-      else if constexpr (KG == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(od[0], od[1]);
-      else *reinterpret_cast<uint32_t*>(dst) = od[0];
+    for (int i = 0; i < kPerWave; ++i) {
+      const int b = wave * kPerWave + i;
+      const int chunk = b * 64 + lane;
+      const int kr = chunk / kChunksRow, cpos = chunk % kChunksRow;
+      const int m = (((cpos >> 1) ^ (kr & 3)) << 4) + ((cpos & 1) << 3);  // tile column stored at this chunk
+      const uint32_t off = static_cast<uint32_t>(k0 + kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
+                                               16, r0 + m < rmax ? off : kOutOfRange, 0, 0, 0);
     }
   }
+  __device__ __forceinline__ void store(uint4*) {}
+  static constexpr int kWrites = 0;
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// The lane's MFMA fragment of tile row `row` (K-contiguous) or of the 32-row
+// block starting at `row` (MN-contiguous), k-step s (16 k).
+template <int R, bool KMAJ>
+__device__ __forceinline__ bf16x8 read_frag(const uint4* tile, int row, int s, int lane) {
+  if constexpr (KMAJ) {
+    const int r = row + (lane & 31);
+    return __builtin_bit_cast(bf16x8, tile[r * 8 + swz(r, 2 * s + (lane >> 5))]);
+  } else {
+    const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+    const int kr = 16 * s + 8 * (g >> 1) + j;              // first k-row; the second read is 4 rows on
+    const int mc = row + 16 * (g & 1) + 4 * q;
+    const int pos = (((mc >> 4) ^ (kr & 3)) << 5) + ((mc & 15) << 1);
+    const char* base = reinterpret_cast<const char*>(tile) + kr * (R * 2) + pos;
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 4 * R * 2));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
 
 enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_GELU_GRAD = 3 };
 
-__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+// erf(u) for u >= 0 by Abramowitz & Stegun, Handbook of Mathematical
+// Functions (1964), formula 7.1.26: 1 - t (a1 + t (a2 + ... + t a5)) e^{-u^2},
+// t = 1 / (1 + p u), absolute error <= 1.5e-7 -- far below the bf16 rounding
+// these epilogues end in. Branch-free, one exp and one reciprocal; e^{-u^2}
+// is returned too (GELU's derivative needs it).
+__device__ __forceinline__ float erf_pos(float u, float& eu2) {
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * u);
+  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  eu2 = exp2_raw(-u * u * kLog2e);
+  return 1.0f - poly * eu2;
+}
+
+// gelu(x) = x/2 (1 + erf(x / sqrt 2)); gelu'(x) = (1 + erf(x / sqrt 2))/2 + x phi(x)
+__device__ __forceinline__ float gelu(float x) {
+  float eu2;
+  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
+  return 0.5f * x * (1.0f + copysignf(e, x));
+}
 
 __device__ __forceinline__ float gelu_grad(float x) {
-  return 0.5f * (1.0f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-0.5f * x * x);
+  float eu2;  // e^{-x^2/2}
+  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
+  return 0.5f * (1.0f + copysignf(e, x)) + x * 0.39894228040143268f * eu2;
 }
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
@@ -191,25 +215,17 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
   tn = in_group / gsize;
 }
 
-// Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
-template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
+// The MFMA main loop of one workgroup tile BM x BN over k-tiles [kt0, kt1):
+// WM x WN waves each accumulate (BM/WM) x (BN/WN) as 32 x 32 blocks.
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
+__device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, int n0, int kt0, int kt1,
+                                         f32x16 (&acc)[BM / WM / 32][BN / WN / 32]) {
   constexpr int T = 64 * WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
-  __shared__ uint4 smem[2 * kStage];
-
-  int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int nkt = (p.K + BK - 1) / BK;
-  const int kt0 = blockIdx.y * p.kt_per_split;
-  const int kt1 = min(nkt, kt0 + p.kt_per_split);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-
   const int L = lane & 31, half = lane >> 5;
-  f32x16 acc[MB][NB];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -229,13 +245,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-
-  // LDS row of this lane's fragment for block i / j
+  // first tile row of this wave's block i / j
   int arow[MB], brow[NB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) arow[i] = wm * (BM / WM) + i * 32 + L;
+  for (int i = 0; i < MB; ++i) arow[i] = wm * (BM / WM) + i * 32;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32 + L;
+  for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32;
 
   // One basic block per k-tile, so the scheduler can interleave: the global
   // loads of tile k+1 are issued first (unconditionally: past the end of K
@@ -251,18 +266,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     lb.load(ob, nxt + BM * 8, n0, p.N, (kt + 1) * BK, p.K);
     bf16x8 af[2][MB], bfr[2][NB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) af[0][i] = __builtin_bit_cast(bf16x8, As[arow[i] * 8 + swz(arow[i], half)]);
+    for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(As, arow[i], 0, lane);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) bfr[0][j] = __builtin_bit_cast(bf16x8, Bs[brow[j] * 8 + swz(brow[j], half)]);
+    for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(Bs, brow[j], 0, lane);
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       const int cur = s & 1;
       if (s + 1 < BK / 16) {
-        const int c = 2 * (s + 1) + half;
 #pragma unroll
-        for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = __builtin_bit_cast(bf16x8, As[arow[i] * 8 + swz(arow[i], c)]);
+        for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(As, arow[i], s + 1, lane);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = __builtin_bit_cast(bf16x8, Bs[brow[j] * 8 + swz(brow[j], c)]);
+        for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bs, brow[j], s + 1, lane);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -289,6 +303,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     __syncthreads();
   }
 
+}
+
+// Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
+  constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
+  constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
+  __shared__ uint4 smem[2 * kStage];
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nkt = (p.K + BK - 1) / BK;
+  const int kt0 = blockIdx.y * p.kt_per_split;
+  const int kt1 = min(nkt, kt0 + p.kt_per_split);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int L = lane & 31, half = lane >> 5;
+  f32x16 acc[MB][NB];
+  mainloop<BM, BN, WM, WN, AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);
+
   // Epilogue, one 32-row block of the wave's (BM/2) x (BN/2) region at a
   // time: the accumulators go to a wave-private LDS block and come back as
   // whole 16-byte chunks of rows, so each global store instruction writes
@@ -304,6 +339,34 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   static_assert(32 * RB * WM * WN <= int(sizeof(smem)), "staging fits in the operand stages");
   unsigned char* stage = reinterpret_cast<unsigned char*>(smem) + wave * 32 * RB;
   const int row0 = m0 + wm * (BM / WM), col0 = n0 + wn * NW;
+  // A lane reads back the same columns for every row: col0 + (lane % CQ) * EPC.
+  const int qc = lane % CQ;
+  const int ncol = col0 + qc * EPC;
+  float4 bq = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) {
+    if (ncol < p.N) bq = *reinterpret_cast<const float4*>(p.bias + ncol);
+  }
+  // The GELU gradient's pre-activations (bf16) of block i+1 stream straight
+  // into LDS (unswizzled [32 rows][NW]) while block i is written out.
+  constexpr int PB = 32 * NW * 2;  // bytes per pre-activation block and wave
+  static_assert(EPI != EPI_GELU_GRAD || 32 * RB * WM * WN + 2 * PB * WM * WN <= int(sizeof(smem)), "aux staging");
+  unsigned char* pstage = reinterpret_cast<unsigned char*>(smem) + 32 * RB * WM * WN + wave * 2 * PB;
+  Operand oaux;
+  if constexpr (EPI == EPI_GELU_GRAD) oaux = make_operand(p.aux, p.ldaux, p.aux_span);
+  auto fetch_pre = [&](int i) {
+    if constexpr (EPI == EPI_GELU_GRAD) {
+      constexpr int kChunksRow = NW * 2 / 16;  // 16-byte chunks per row
+#pragma unroll
+      for (int u = 0; u < PB / 1024; ++u) {
+        const int chunk = u * 64 + lane;
+        const int r = chunk / kChunksRow, q = chunk % kChunksRow;
+        const uint32_t off = static_cast<uint32_t>(row0 + i * 32 + r) * oaux.ld2 + static_cast<uint32_t>(col0 + q * 8) * 2u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            oaux.rsrc, (__attribute__((address_space(3))) void*)(pstage + (i & 1) * PB + u * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  fetch_pre(0);
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -323,10 +386,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
         }
       }
     }
+    if constexpr (EPI == EPI_GELU_GRAD) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (i + 1 < MB) fetch_pre(i + 1);
     if (ATOMIC) {
       // one float per lane, 64 consecutive columns of a row per instruction
-#pragma unroll 4
+#pragma unroll 1
       for (int t = 0; t < 32 * NW / 64; ++t) {
         const int r = t / (NW / 64), c = (t % (NW / 64)) * 64 + lane;
         const int m = row0 + i * 32 + r, n = col0 + c;
@@ -335,11 +400,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
         if (m < p.M && n < p.N) unsafeAtomicAdd(static_cast<float*>(p.C) + static_cast<int64_t>(m) * p.ldc + n, v);
       }
     } else {
-#pragma unroll
+      // The GELU epilogues stay runtime loops (unrolled they are more code
+      // than the instruction cache holds); the others are unrolled.
+#pragma unroll (EPI == EPI_BIAS_GELU || EPI == EPI_GELU_GRAD) ? 2 : 32
       for (int t = 0; t < 32 / RPI; ++t) {
-        const int r = t * RPI + lane / CQ, q = lane % CQ;
-        const int m = row0 + i * 32 + r, n = col0 + q * EPC;
-        const uint4 raw = *reinterpret_cast<const uint4*>(stage + r * RB + ((q ^ (r % CQ)) * 16));
+        const int r = t * RPI + lane / CQ;
+        const int m = row0 + i * 32 + r, n = ncol;
+        const uint4 raw = *reinterpret_cast<const uint4*>(stage + r * RB + ((qc ^ (r % CQ)) * 16));
         if (m >= p.M || n >= p.N) continue;
         TC* cp = static_cast<TC*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
         if constexpr (sizeof(S) == 4) {
@@ -347,8 +414,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
           x.v[0] = __uint_as_float(raw.x); x.v[1] = __uint_as_float(raw.y);
           x.v[2] = __uint_as_float(raw.z); x.v[3] = __uint_as_float(raw.w);
           if (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU) {
-            const float4 b = *reinterpret_cast<const float4*>(p.bias + n);
-            x.v[0] += b.x; x.v[1] += b.y; x.v[2] += b.z; x.v[3] += b.w;
+            x.v[0] += bq.x; x.v[1] += bq.y; x.v[2] += bq.z; x.v[3] += bq.w;
           }
           if (EPI == EPI_BIAS_GELU) {
             // aux = bf16(acc + bias), the pre-activation; C = gelu of it
@@ -356,10 +422,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x.v[e] = gelu(round_bf16(x.v[e]));
           }
-          if (EPI == EPI_GELU_GRAD) {
-            const f4 pre = io4<bf16_t>::load(p.aux + static_cast<int64_t>(m) * p.ldaux + n);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x.v[e] *= gelu_grad(pre.v[e]);
+          if constexpr (EPI == EPI_GELU_GRAD) {
+            const uint2 w = *reinterpret_cast<const uint2*>(pstage + (i & 1) * PB + r * (NW * 2) + qc * 8);
+            x.v[0] *= gelu_grad(__uint_as_float(w.x << 16));
+            x.v[1] *= gelu_grad(__uint_as_float(w.x & 0xffff0000u));
+            x.v[2] *= gelu_grad(__uint_as_float(w.y << 16));
+            x.v[3] *= gelu_grad(__uint_as_float(w.y & 0xffff0000u));
           }
           io4<TC>::store(cp, x);
         } else {
@@ -369,6 +437,104 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------- loss head
+//
+// Streaming cross-entropy head: logits = E W^T for 64 rows at a time with
+// all V (<= 256) classes in one workgroup tile, then, from LDS, per row
+//   lse = max + log(sum exp(l - max)),  loss = lse - l[label],
+//   dlogits = (softmax - onehot(label)) * scale   (bf16),
+// so the fp32 logits never reach HBM. Reference mingru/minLM.py:138,146-149
+// (to_logits, F.cross_entropy with mean reduction); loss_part[b] = sum of
+// the row losses of workgroup b.
+constexpr int kCeRows = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t* __restrict__ labels,
+                                                        bf16_t* __restrict__ dlogits, int64_t ldd,
+                                                        float* __restrict__ loss_part, int* __restrict__ bad_label,
+                                                        float scale) {
+  constexpr int BM = kCeRows, BN = 256, WM = 1, WN = 4;
+  constexpr int MB = BM / WM / 32, NB = BN / WN / 32;
+  constexpr int kStage = (BM + BN) * 8;
+  __shared__ uint4 smem[2 * kStage];
+  __shared__ float s_loss[4];
+  static_assert(BM * BN * 4 <= int(sizeof(smem)), "logits tile fits");
+
+  const int m0 = blockIdx.x * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int L = lane & 31, half = lane >> 5;
+  f32x16 acc[MB][NB];
+  mainloop<BM, BN, WM, WN, true, true>(p, smem, m0, 0, 0, (p.K + BK - 1) / BK, acc);
+
+  // logits tile [64][256] fp32 in LDS, 16-byte chunk c of row r at c ^ (r & 63)
+  float* tile = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = i * 32 + L;
+        const int c = wave * (BN / WN / 4) + j * 8 + 2 * g + half;
+        f4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x.v[e] = acc[i][j][4 * g + e];
+        io4<float>::store(tile + r * BN + ((c ^ (r & 63)) * 4), x);
+      }
+  __syncthreads();
+
+  float lsum = 0.0f;
+  const int V = p.N;
+  const int col = 4 * lane;
+  for (int rr = 0; rr < BM / 4; ++rr) {
+    const int r = wave * (BM / 4) + rr;
+    const int64_t row = static_cast<int64_t>(m0) + r;
+    if (row >= p.M) break;
+    const int64_t lab = labels[row];
+    f4 x = io4<float>::load(tile + r * BN + ((lane ^ (r & 63)) * 4));
+    float m = -INFINITY, picked = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (col + e >= V) x.v[e] = -INFINITY;
+      m = fmaxf(m, x.v[e]);
+      if (col + e == lab) picked = x.v[e];
+    }
+    m = wave_max(m);
+    picked = wave_sum(picked);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x.v[e] = expf(x.v[e] - m);
+      sum += x.v[e];
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      lsum += logf(sum) + m - picked;
+      if ((lab < 0 || lab >= V) && bad_label) atomicOr(bad_label, 1);
+    }
+    const float inv = 1.0f / sum;
+    if (col < V) {
+      f4 d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d.v[e] = (x.v[e] * inv - (col + e == lab ? 1.0f : 0.0f)) * scale;
+      io4<bf16_t>::store(dlogits + row * ldd + col, d);
+    }
+  }
+  if (lane == 0) s_loss[wave] = lsum;
+  __syncthreads();
+  if (threadIdx.x == 0) loss_part[blockIdx.x] = s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3];
 }
 
 __global__ void zero_f32_kernel(float* __restrict__ p, int64_t rows, int cols, int64_t ld) {
@@ -410,17 +576,15 @@ int dispatch_epi(const Params& p, int epi, int c_dtype, bool atomic, int splits,
   return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
 }
 
-// 256 x 256 tiles: 8 waves (two per SIMD) when both operands stream straight
-// into LDS; 4 waves (one per SIMD, 512 registers each) when an operand is
-// transposed through registers.
+// 256 x 256 tiles run 8 waves (two per SIMD), 128 x 128 tiles 4.
 template <int BM, int BN>
 int dispatch_layout(const Params& p, bool ak, bool bk, int epi, int c_dtype, bool atomic, int splits,
                     hipStream_t s) {
-  constexpr bool kBig = BM * BN >= 256 * 256;
-  if (ak && bk) return dispatch_epi<BM, BN, 2, kBig ? 4 : 2, true, true>(p, epi, c_dtype, atomic, splits, s);
-  if (ak && !bk) return dispatch_epi<BM, BN, 2, 2, true, false>(p, epi, c_dtype, atomic, splits, s);
-  if (!ak && !bk) return dispatch_epi<BM, BN, 2, 2, false, false>(p, epi, c_dtype, atomic, splits, s);
-  return dispatch_epi<BM, BN, 2, 2, false, true>(p, epi, c_dtype, atomic, splits, s);
+  constexpr int WN = BM * BN >= 256 * 256 ? 4 : 2;
+  if (ak && bk) return dispatch_epi<BM, BN, 2, WN, true, true>(p, epi, c_dtype, atomic, splits, s);
+  if (ak && !bk) return dispatch_epi<BM, BN, 2, WN, true, false>(p, epi, c_dtype, atomic, splits, s);
+  if (!ak && !bk) return dispatch_epi<BM, BN, 2, WN, false, false>(p, epi, c_dtype, atomic, splits, s);
+  return dispatch_epi<BM, BN, 2, WN, false, true>(p, epi, c_dtype, atomic, splits, s);
 }
 
 }  // namespace gemm
@@ -473,6 +637,11 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     return fail(MG_ERR_ARG, "%s: operands must span less than 2 GiB", fn);
   p.a_span = static_cast<uint32_t>(a_span);
   p.b_span = static_cast<uint32_t>(b_span);
+  if (aux) {
+    const int64_t aux_span = (int64_t(M - 1) * ldaux + N) * 2;
+    if (aux_span + 256 * ldaux * 2 >= (int64_t(1) << 31)) return fail(MG_ERR_ARG, "%s: aux must span less than 2 GiB", fn);
+    p.aux_span = static_cast<uint32_t>(aux_span);
+  }
 
   // Tile choice: 256 x 256 when that still gives every CU a workgroup,
   // else 128 x 128. fp32 outputs with few tiles and a long K split K.
@@ -492,4 +661,34 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
   }
   return big ? gemm::dispatch_layout<256, 256>(p, ak, bk, epilogue, c_dtype, atomic, splits, s)
              : gemm::dispatch_layout<128, 128>(p, ak, bk, epilogue, c_dtype, atomic, splits, s);
+}
+
+extern "C" int mg_logits_cross_entropy_partials(int64_t N) {
+  return N < 1 ? 0 : static_cast<int>((N + gemm::kCeRows - 1) / gemm::kCeRows);
+}
+
+extern "C" int mg_logits_cross_entropy(const void* embed, int64_t lde, const void* w, int64_t ldw,
+                                       const int64_t* labels, void* dlogits, int64_t ldd, float* loss_part,
+                                       int* bad_label, int N, int D, int V, float scale, void* stream) {
+  const char* fn = "mg_logits_cross_entropy";
+  if (!embed || !w || !labels || !dlogits || !loss_part) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (N < 1 || D < 8 || D % 8 || V < 8 || V > 256 || V % 8)
+    return fail(MG_ERR_ARG, "%s: bad shape N=%d D=%d V=%d (D %% 8 == 0, 8 <= V <= 256, V %% 8 == 0)", fn, N, D, V);
+  if (lde < D || lde % 8 || ldw < D || ldw % 8 || ldd < V || ldd % 4)
+    return fail(MG_ERR_ARG, "%s: bad leading dimensions", fn);
+  if (!aligned(embed, 16) || !aligned(w, 16) || !aligned(dlogits, 8) || !aligned(labels, 8))
+    return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  const int64_t a_span = (int64_t(N - 1) * lde + D) * 2, b_span = (int64_t(V - 1) * ldw + D) * 2;
+  if (a_span + 256 * lde * 2 >= (int64_t(1) << 31)) return fail(MG_ERR_ARG, "%s: embed spans 2 GiB or more", fn);
+  gemm::Params p{};
+  p.A = static_cast<const bf16_t*>(embed);
+  p.B = static_cast<const bf16_t*>(w);
+  p.lda = lde; p.ldb = ldw;
+  p.M = N; p.N = V; p.K = D;
+  p.a_span = static_cast<uint32_t>(a_span);
+  p.b_span = static_cast<uint32_t>(b_span);
+  hipLaunchKernelGGL(gemm::logits_ce_kernel, dim3((N + gemm::kCeRows - 1) / gemm::kCeRows), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, labels, static_cast<bf16_t*>(dlogits), ldd, loss_part,
+                     bad_label, scale);
+  return check_launch(fn);
 }

@@ -15,6 +15,8 @@ With fp32 activations this is plain F.linear.
 import torch
 import torch.nn.functional as F
 
+from . import gemm
+
 _MM_OUT_DTYPE = None  # whether torch.mm(..., out_dtype=float32) works for bf16 on this build
 
 
@@ -73,3 +75,58 @@ def linear(x, layer):
     if x.dtype != torch.bfloat16 or w.dtype != torch.float32:
         raise TypeError(f"unsupported linear: activations {x.dtype}, weight {w.dtype}")
     return BF16Linear.apply(x, w, b, bf16_copy(w))
+
+
+class BF16FeedForward(torch.autograd.Function):
+    """Linear -> GELU -> Linear (reference mingru/minLM.py:17-23) in bf16 with
+    the GELU fused into the MFMA products: the first product's epilogue adds
+    the bias, keeps the pre-activation and applies GELU; in the backward the
+    product dY W2 is multiplied by GELU'(pre-activation) in its epilogue."""
+
+    @staticmethod
+    def forward(ctx, x, w1, b1, w2, b2, w1b, w2b):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        pre = torch.empty(x2.shape[0], w1b.shape[0], device=x.device, dtype=torch.bfloat16)
+        h = gemm.linear_fwd(x2, w1b, b1.detach().contiguous(), gelu_pre=pre)
+        y = F.linear(h, w2b, b2.detach().to(torch.bfloat16))
+        ctx.save_for_backward(x2, pre, h, w1b, w2b)
+        return y.view(*shape[:-1], w2b.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, pre, h, w1b, w2b = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        if dy2.dtype != torch.bfloat16:
+            dy2 = dy2.to(torch.bfloat16)
+        if not dy2.is_contiguous():
+            dy2 = dy2.contiguous()
+        dpre = gemm.linear_dx(dy2, w2b, gelu_pre=pre)
+        dw2 = _mm_f32(dy2.t(), h)
+        db2 = dy2.sum(0, dtype=torch.float32)
+        dx = torch.mm(dpre, w1b).view(*dy.shape[:-1], w1b.shape[1])
+        dw1 = _mm_f32(dpre.t(), x2)
+        db1 = dpre.sum(0, dtype=torch.float32)
+        return dx, dw1, db1, dw2, db2, None, None
+
+
+# The fused path is exact and tested, but on MI355X it is not yet faster:
+# the GELU epilogues run after the MFMA main loop of each tile with nothing
+# to overlap them (one 128 KiB-LDS workgroup per CU), and the hand-written
+# main loop trails hipBLASLt on these shapes. Off by default until it wins.
+FUSED_FEED_FORWARD = False
+
+
+def feed_forward(x, ff):
+    """ff = nn.Sequential(Linear, GELU, Linear) applied to x in x's dtype."""
+    l1, l2 = ff[0], ff[2]
+    if x.dtype == l1.weight.dtype:
+        return l2(F.gelu(l1(x)))
+    if not FUSED_FEED_FORWARD:
+        return linear(F.gelu(linear(x, l1)), l2)
+    if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32 or l1.bias is None or l2.bias is None:
+        raise TypeError(f"unsupported feed-forward: activations {x.dtype}, weight {l1.weight.dtype}")
+    return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
+                                 bf16_copy(l2.weight))

@@ -1,9 +1,13 @@
 """Loss head: logits projection + mean cross-entropy (reference
-mingru/minLM.py:138, :146-149), with the log-softmax, the loss and the
-logits gradient computed in one pass by mg_cross_entropy_fwd_bwd.
+mingru/minLM.py:138, :146-149). For bf16 embeddings and V <= 256 classes the
+logits product, log-softmax, loss and logits gradient are one kernel
+(mg_logits_cross_entropy) and the fp32 logits never reach memory; otherwise
+the logits are formed first and mg_cross_entropy_fwd_bwd does the rest in one
+pass.
 """
 import torch
 
+from . import gemm
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 from .linear import _mm_f32, bf16_copy
 
@@ -25,8 +29,19 @@ class LogitsCrossEntropy(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, embed, w, wb, labels):
-        logits = _mm_f32(embed, wb.t())               # [N, V] fp32
-        loss, dl = _ce(logits, labels, torch.bfloat16)
+        N, D = embed.shape
+        V = wb.shape[0]
+        if V <= 256 and V % 8 == 0 and D % 8 == 0:
+            L = lib()
+            dl = torch.empty(N, V, dtype=torch.bfloat16, device=embed.device)
+            part = torch.empty(L.mg_logits_cross_entropy_partials(N), dtype=torch.float32, device=embed.device)
+            rc = L.mg_logits_cross_entropy(ptr(embed), embed.stride(0), ptr(wb), wb.stride(0), ptr(labels), ptr(dl),
+                                           V, ptr(part), None, N, D, V, 1.0 / N, stream_of(embed))
+            check(rc, "mg_logits_cross_entropy")
+            loss = part.sum() / N
+        else:
+            logits = _mm_f32(embed, wb.t())               # [N, V] fp32
+            loss, dl = _ce(logits, labels, torch.bfloat16)
         ctx.save_for_backward(embed, wb, dl)
         return loss
 
@@ -35,7 +50,7 @@ class LogitsCrossEntropy(torch.autograd.Function):
         embed, wb, dl = ctx.saved_tensors
         dl = dl * g  # upstream gradient (1/grad_accum in the reference loop); stays bf16
         de = torch.mm(dl, wb) if ctx.needs_input_grad[0] else None
-        dw = _mm_f32(dl.t(), embed) if ctx.needs_input_grad[1] else None
+        dw = gemm.linear_dw(dl, embed) if ctx.needs_input_grad[1] else None
         return de, dw, None, None
 
 

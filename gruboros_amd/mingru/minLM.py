@@ -17,6 +17,7 @@ import torch.nn.functional as F
 from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
+from ..linear import feed_forward
 from ..linear import linear as _linear
 from ..loss import logits_cross_entropy
 from ..norm import add_rms_norm, rms_norm
@@ -60,8 +61,7 @@ class CausalDepthWiseConv1d(Module):
 
 
 def _ff(x, ff):
-    h = F.gelu(_linear(x, ff[0]))
-    return _linear(h, ff[2])
+    return feed_forward(x, ff)
 
 
 class minLM(Module):

@@ -230,6 +230,27 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
             int epilogue, const float* bias, void* aux, int64_t ldaux,
             int c_dtype, void* C, int64_t ldc, int accumulate, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Streaming loss head: logits GEMM + log-softmax + cross-entropy + gradient.
+ *
+ * Replaces reference mingru/minLM.py:138 (to_logits) and :146-149
+ * (F.cross_entropy over the transposed logits, mean reduction) with its
+ * backward through the logits, without writing the logits:
+ *   logits = E W^T          E: bf16 [N, D] (lde), W: bf16 [V, D] (ldw)
+ *   loss_part[b]  = sum over the rows of block b of (lse_n - logits[n, label_n])
+ *   dlogits[n, j] = (softmax(logits_n)_j - [j == label_n]) * scale   (bf16, ldd)
+ * Mean loss = sum(loss_part) / N with scale = 1/N; loss_part holds
+ * mg_logits_cross_entropy_partials(N) values (one per 64 rows).
+ * bad_label (nullable, zeroed by the caller) is set to 1 for a label outside
+ * [0, V). Requirements: D % 8 == 0, 8 <= V <= 256, V % 8 == 0, lde, ldw % 8
+ * == 0, ldd % 4 == 0, E and W 16-byte aligned, labels int64.
+ * ---------------------------------------------------------------------- */
+int mg_logits_cross_entropy_partials(int64_t N);
+int mg_logits_cross_entropy(const void* embed, int64_t lde, const void* w, int64_t ldw,
+                            const int64_t* labels, void* dlogits, int64_t ldd,
+                            float* loss_part, int* bad_label, int N, int D, int V,
+                            float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

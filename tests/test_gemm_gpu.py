@@ -137,3 +137,33 @@ def test_gemm_model_sizes(which):
         ref = dy.float().t() @ x.float()
     tol = 1e-5 if got.dtype == torch.float32 and not which.endswith("dx") else 4e-3
     assert _rel(got, ref) < tol
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_feed_forward_bf16_matches_fp64(fused, monkeypatch):
+    """bf16 FeedForward, fused (GELU in the MFMA epilogues) and unfused, vs the
+    fp64 reference Linear -> GELU -> Linear (reference mingru/minLM.py:17-23)."""
+    from gruboros_amd import linear as lin
+    from gruboros_amd.linear import feed_forward
+
+    monkeypatch.setattr(lin, "FUSED_FEED_FORWARD", fused)
+    torch.manual_seed(4)
+    D, F_ = 256, 1024
+    ff = torch.nn.Sequential(torch.nn.Linear(D, F_), torch.nn.GELU(), torch.nn.Linear(F_, D)).to(DEV)
+    with torch.no_grad():
+        ff[2].weight.normal_(0, 0.05)
+        ff[2].bias.normal_(0, 0.1)
+    x = torch.randn(3, 333, D, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    y = feed_forward(x, ff)
+    assert y.dtype == torch.bfloat16 and y.shape == (3, 333, D)
+    dy = torch.randn(y.shape, device=DEV)
+    (y.float() * dy).sum().backward()
+    ref = [t.detach().double().cpu().requires_grad_(True) for t in (x, ff[0].weight, ff[0].bias, ff[2].weight, ff[2].bias)]
+    x64, w1, b1, w2, b2 = ref
+    y64 = torch.nn.functional.linear(torch.nn.functional.gelu(torch.nn.functional.linear(x64, w1, b1)), w2, b2)
+    (y64 * dy.double().cpu()).sum().backward()
+    assert _rel(y, y64) < 2e-2
+    for got, want in ((x.grad, x64.grad), (ff[0].weight.grad, w1.grad), (ff[0].bias.grad, b1.grad),
+                      (ff[2].weight.grad, w2.grad), (ff[2].bias.grad, b2.grad)):
+        assert got.dtype == (torch.bfloat16 if got is x.grad else torch.float32)
+        assert _rel(got, want) < 2e-2

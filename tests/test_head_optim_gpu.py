@@ -144,3 +144,32 @@ def test_bf16_weight_copy_follows_the_master():
     assert _rel(xg.grad, x64.grad) < 2e-2
     assert _rel(layer.weight.grad, w64.grad) < 2e-2
     assert _rel(layer.bias.grad, b64.grad) < 2e-2
+
+
+@pytest.mark.parametrize("N,D,V", [(777, 256, 256), (64, 128, 64), (1000, 1024, 256), (130, 64, 200)])
+def test_streaming_loss_head_matches_fp64(N, D, V):
+    """mg_logits_cross_entropy (logits product + CE + gradient, no logits in memory)
+    vs the fp64 reference head F.cross_entropy(F.linear(e, W)), incl. partial row blocks."""
+    from gruboros_amd import _lib
+
+    gen = torch.Generator().manual_seed(N + V)
+    e = (torch.randn(N, D, generator=gen, dtype=torch.float64)).to(torch.bfloat16)
+    w = (torch.randn(V, D, generator=gen, dtype=torch.float64) * 0.1).to(torch.bfloat16)
+    lab = torch.randint(0, V, (N,), generator=gen)
+    lab[:2] = torch.tensor([0, V - 1])
+    L = _lib.lib()
+    dl = torch.full((N, V + 8), 3.0, device=DEV, dtype=torch.bfloat16)
+    part = torch.empty(L.mg_logits_cross_entropy_partials(N), device=DEV)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ed, wd, ld = e.to(DEV), w.to(DEV), lab.to(DEV)
+    rc = L.mg_logits_cross_entropy(_lib.ptr(ed), D, _lib.ptr(wd), D, _lib.ptr(ld), _lib.ptr(dl), V + 8, _lib.ptr(part),
+                                   _lib.ptr(bad), N, D, V, 1.0 / N, _lib.stream_of(ed))
+    assert rc == 0
+    torch.cuda.synchronize()
+    logits = (e.double() @ w.double().t()).requires_grad_(True)
+    ref = F.cross_entropy(logits, lab)
+    ref.backward()
+    assert abs(float(part.sum()) / N - float(ref)) / float(ref) < 1e-5
+    assert _rel(dl[:, :V].float(), logits.grad) < 4e-3
+    assert bool((dl[:, V:] == 3.0).all())  # padding columns untouched
+    assert int(bad) == 0
