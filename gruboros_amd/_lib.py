@@ -40,6 +40,9 @@ SIGNATURES = {
     "mg_logits_cross_entropy_partials": (_c_int, [_c_i64]),
     "mg_logits_cross_entropy": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _fp, _vp, _c_int, _c_int, _c_int,
                                          ctypes.c_float, _vp]),
+    "mg_column_sum_workspace_bytes": (_c_size, [_c_i64, _c_int]),
+    "mg_column_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_int, _fp, _vp, _c_size, _vp]),
+    "mg_gelu_bwd": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp]),
 }

@@ -1,0 +1,184 @@
+// Column sums over the token rows: the bias gradients of the FeedForward
+// linears (reference mingru/minLM.py:17-23, autograd of nn.Linear's bias),
+// one of them fused with GELU's backward, and the reduction of per-workgroup
+// partial rows that the RMSNorm weight gradient also uses.
+//
+//   mg_column_sum:   out[c] = sum_n x[n, c]                        (x bf16 / fp32)
+//   mg_gelu_bwd:     dpre[n, c] = bf16(dh[n, c] gelu'(pre[n, c]))
+//                    dbias[c]   = sum_n dpre[n, c]   (of the rounded values,
+//                                 as summing the bf16 tensor gives)
+// Both make one pass over the rows: workgroup (cb, rg) owns 2048 columns
+// (8 per thread, one 16-byte bf16 vector) of the rows rg, rg + RG, ...,
+// and writes one partial row; launch_reduce_partials sums the RG partial
+// rows in a fixed order (the results do not depend on scheduling).
+
+#include <algorithm>
+
+#include "mg_common.h"
+
+namespace mg {
+namespace colsum {
+
+constexpr int kThreads = 256;
+constexpr int kVecC = 8;                          // columns per thread
+constexpr int kCols = kThreads * kVecC;           // columns per workgroup
+
+// Row groups (= partial rows): about 512 workgroups in all.
+inline int row_groups(int64_t N, int C) {
+  const int64_t col_blocks = std::max<int64_t>(1, (C + kCols - 1) / kCols);
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(N, 512 / col_blocks)));
+}
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float (&v)[8]) {
+  const uint4 x = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = __uint_as_float(w[q] << 16);
+    v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ x, int64_t ld, int64_t N, int C,
+                                                          float* __restrict__ part) {
+  const int c = blockIdx.x * kCols + threadIdx.x * kVecC;
+  if (c >= C) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 4
+  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {
+    float v[8];
+    load8<T>(x + n * ld + c, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+  }
+  float* o = part + static_cast<int64_t>(blockIdx.y) * C + c;
+  reinterpret_cast<float4*>(o)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  reinterpret_cast<float4*>(o)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+__global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const bf16_t* __restrict__ dh, int64_t ld_dh,
+                                                            const bf16_t* __restrict__ pre, int64_t ld_pre,
+                                                            bf16_t* __restrict__ dpre, int64_t ld_out, int64_t N,
+                                                            int C, float* __restrict__ part) {
+  const int c = blockIdx.x * kCols + threadIdx.x * kVecC;
+  if (c >= C) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 2
+  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {
+    float g[8], x[8];
+    load8<bf16_t>(dh + n * ld_dh + c, g);
+    load8<bf16_t>(pre + n * ld_pre + c, x);
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      w[q] = pack_bf16x2(g[2 * q] * gelu_grad(x[2 * q]), g[2 * q + 1] * gelu_grad(x[2 * q + 1]));
+      acc[2 * q] += __uint_as_float(w[q] << 16);
+      acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
+    }
+    *reinterpret_cast<uint4*>(dpre + n * ld_out + c) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (part) {
+    float* o = part + static_cast<int64_t>(blockIdx.y) * C + c;
+    reinterpret_cast<float4*>(o)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    reinterpret_cast<float4*>(o)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+// out[c] = sum_p part[p][c]: 16 columns (4 lanes x 4) by 64 row lanes per
+// workgroup; each row lane sums every 64th partial row, then a fixed-order
+// tree over the row lanes in LDS.
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ part, int P, int C,
+                                                              float* __restrict__ out) {
+  __shared__ float4 s[64][4];
+  const int cl = threadIdx.x % 4, rl = threadIdx.x / 4;
+  const int c = blockIdx.x * 16 + cl * 4;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (c < C) {
+#pragma unroll 4
+    for (int p = rl; p < P; p += 64) {
+      const float4 v = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(p) * C + c);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+  }
+  s[rl][cl] = acc;
+  __syncthreads();
+#pragma unroll
+  for (int h = 32; h > 0; h >>= 1) {
+    if (rl < h) {
+      const float4 o = s[rl + h][cl];
+      float4& m = s[rl][cl];
+      m.x += o.x; m.y += o.y; m.z += o.z; m.w += o.w;
+    }
+    __syncthreads();
+  }
+  if (rl == 0 && c < C) *reinterpret_cast<float4*>(out + c) = s[0][cl];
+}
+
+}  // namespace colsum
+
+int launch_reduce_partials(const float* part, int P, int C, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(colsum::reduce_partials_kernel, dim3((C + 15) / 16), dim3(256), 0, st, part, P, C, out);
+  return MG_OK;
+}
+
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" size_t mg_column_sum_workspace_bytes(int64_t N, int C) {
+  if (N < 1 || C < 1) return 16;
+  return static_cast<size_t>(colsum::row_groups(N, C)) * static_cast<size_t>(std::max(C, 0)) * sizeof(float);
+}
+
+extern "C" int mg_column_sum(int dtype, const void* x, int64_t ld, int64_t N, int C, float* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  const char* fn = "mg_column_sum";
+  if (!x || !out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (N < 1 || C < 8 || C % 8 || ld < C || ld % 8) return fail(MG_ERR_ARG, "%s: bad shape N=%lld C=%d ld=%lld", fn,
+                                                               (long long)N, C, (long long)ld);
+  if (dtype != MG_F32 && dtype != MG_BF16) return fail(MG_ERR_DTYPE, "%s: dtype %d unsupported", fn, dtype);
+  if (!aligned(x, 16) || !aligned(out, 16)) return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  const int RG = colsum::row_groups(N, C);
+  if (!workspace || workspace_bytes < mg_column_sum_workspace_bytes(N, C) || !aligned(workspace, 16))
+    return fail(MG_ERR_WORKSPACE, "%s: workspace too small or misaligned", fn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const dim3 grid((C + colsum::kCols - 1) / colsum::kCols, RG);
+  if (dtype == MG_BF16)
+    hipLaunchKernelGGL(colsum::colsum_kernel<bf16_t>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const bf16_t*>(x), ld, N, C, part);
+  else
+    hipLaunchKernelGGL(colsum::colsum_kernel<float>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const float*>(x), ld, N, C, part);
+  launch_reduce_partials(part, RG, C, out, st);
+  return check_launch(fn);
+}
+
+extern "C" int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre, void* dpre, int64_t ld_out,
+                           float* dbias, int64_t N, int C, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "mg_gelu_bwd";
+  if (!dh || !pre || !dpre) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (N < 1 || C < 8 || C % 8 || ld_dh < C || ld_pre < C || ld_out < C || ld_dh % 8 || ld_pre % 8 || ld_out % 8)
+    return fail(MG_ERR_ARG, "%s: bad shape N=%lld C=%d", fn, (long long)N, C);
+  if (!aligned(dh, 16) || !aligned(pre, 16) || !aligned(dpre, 16) || (dbias && !aligned(dbias, 16)))
+    return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  const int RG = colsum::row_groups(N, C);
+  if (dbias && (!workspace || workspace_bytes < mg_column_sum_workspace_bytes(N, C) || !aligned(workspace, 16)))
+    return fail(MG_ERR_WORKSPACE, "%s: workspace too small or misaligned", fn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = dbias ? static_cast<float*>(workspace) : nullptr;
+  const dim3 grid((C + colsum::kCols - 1) / colsum::kCols, RG);
+  hipLaunchKernelGGL(colsum::gelu_bwd_kernel, grid, dim3(colsum::kThreads), 0, st, static_cast<const bf16_t*>(dh),
+                     ld_dh, static_cast<const bf16_t*>(pre), ld_pre, static_cast<bf16_t*>(dpre), ld_out, N, C, part);
+  if (dbias) launch_reduce_partials(part, RG, C, dbias, st);
+  return check_launch(fn);
+}

@@ -119,11 +119,13 @@ struct Loader<R, true, T> {
 
 // MN-contiguous operands also go straight into LDS, kept as stored: a tile
 // is [64 k-rows][R] bf16, the 32-byte segment s of k-row r placed at
-// segment s ^ (r & 3). The MFMA fragments (8 consecutive k of one tile row)
-// come back through the LDS transpose read (ds_read_b64_tr_b16): in each
-// group of 16 lanes, lane 4 j + q addresses k-row j, columns 4 q .. 4 q + 3,
-// and lane i receives column i of the 4 k-rows. The swizzle puts the 4
-// k-rows of one read on distinct banks.
+// segment s ^ h(r), h(r) = {0, 2, 5, 7}[r & 3]. The MFMA fragments (8
+// consecutive k of one tile row) come back through the LDS transpose read
+// (ds_read_b64_tr_b16): in each group of 16 lanes, lane 4 j + q addresses
+// k-row j, columns 4 q .. 4 q + 3, and lane i receives column i of the 4
+// k-rows. With this h the 16 lanes of a group hit distinct banks, and so do
+// the 32 lanes of two neighbouring groups (4 k-rows x 2 segments).
+__device__ __forceinline__ int tr_swz(int kr) { return ((kr & 3) << 1) | ((kr >> 1) & 1); }
 template <int R, int T>
 struct Loader<R, false, T> {
   static constexpr int kChunksRow = R / 8;                    // 16-byte chunks per k-row
@@ -137,7 +139,7 @@ struct Loader<R, false, T> {
       const int b = wave * kPerWave + i;
       const int chunk = b * 64 + lane;
       const int kr = chunk / kChunksRow, cpos = chunk % kChunksRow;
-      const int m = (((cpos >> 1) ^ (kr & 3)) << 4) + ((cpos & 1) << 3);  // tile column stored at this chunk
+      const int m = (((cpos >> 1) ^ tr_swz(kr)) << 4) + ((cpos & 1) << 3);  // tile column stored at this chunk
       const uint32_t off = static_cast<uint32_t>(k0 + kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
                                                16, r0 + m < rmax ? off : kOutOfRange, 0, 0, 0);
@@ -160,7 +162,7 @@ __device__ __forceinline__ bf16x8 read_frag(const uint4* tile, int row, int s, i
     const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
     const int kr = 16 * s + 8 * (g >> 1) + j;              // first k-row; the second read is 4 rows on
     const int mc = row + 16 * (g & 1) + 4 * q;
-    const int pos = (((mc >> 4) ^ (kr & 3)) << 5) + ((mc & 15) << 1);
+    const int pos = (((mc >> 4) ^ tr_swz(kr)) << 5) + ((mc & 15) << 1);
     const char* base = reinterpret_cast<const char*>(tile) + kr * (R * 2) + pos;
     typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base));
@@ -170,31 +172,6 @@ __device__ __forceinline__ bf16x8 read_frag(const uint4* tile, int row, int s, i
 }
 
 enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_GELU_GRAD = 3 };
-
-// erf(u) for u >= 0 by Abramowitz & Stegun, Handbook of Mathematical
-// Functions (1964), formula 7.1.26: 1 - t (a1 + t (a2 + ... + t a5)) e^{-u^2},
-// t = 1 / (1 + p u), absolute error <= 1.5e-7 -- far below the bf16 rounding
-// these epilogues end in. Branch-free, one exp and one reciprocal; e^{-u^2}
-// is returned too (GELU's derivative needs it).
-__device__ __forceinline__ float erf_pos(float u, float& eu2) {
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * u);
-  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
-  eu2 = exp2_raw(-u * u * kLog2e);
-  return 1.0f - poly * eu2;
-}
-
-// gelu(x) = x/2 (1 + erf(x / sqrt 2)); gelu'(x) = (1 + erf(x / sqrt 2))/2 + x phi(x)
-__device__ __forceinline__ float gelu(float x) {
-  float eu2;
-  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
-  return 0.5f * x * (1.0f + copysignf(e, x));
-}
-
-__device__ __forceinline__ float gelu_grad(float x) {
-  float eu2;  // e^{-x^2/2}
-  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
-  return 0.5f * (1.0f + copysignf(e, x)) + x * 0.39894228040143268f * eu2;
-}
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
@@ -643,16 +620,20 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     p.aux_span = static_cast<uint32_t>(aux_span);
   }
 
-  // Tile choice: 256 x 256 when that still gives every CU a workgroup,
-  // else 128 x 128. fp32 outputs with few tiles and a long K split K.
+  // Tile choice (measured on MI355X): weight gradients (both operands
+  // MN-contiguous, long K) run 128 x 128 tiles split along K into about
+  // two workgroups per CU; the other layouts run 256 x 256 when that still
+  // gives every CU a workgroup, else 128 x 128 (fp32 outputs then split K).
   const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  const bool big = t256 >= gemm::kCUs;
+  const bool wgrad = !ak && !bk;
+  const bool big = !wgrad && t256 >= gemm::kCUs;
   const int64_t tiles = big ? t256 : t128;
   const int nkt = (K + gemm::BK - 1) / gemm::BK;
+  const int64_t want_wgs = wgrad ? 2 * gemm::kCUs : gemm::kCUs;
   int splits = 1;
-  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < gemm::kCUs)
-    splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(gemm::kCUs / tiles, 1), std::max(nkt / 4, 1)));
+  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs)
+    splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
   if (K == 0 && accumulate) return MG_OK;
   const bool atomic = accumulate || splits > 1;
   if (atomic && !accumulate) {

@@ -181,6 +181,37 @@ __device__ __forceinline__ void bwd_coeffs(float gate, float hid, float& a, floa
   q = hid > 0.0f ? z : (hid < 0.0f ? qneg : 0.0f);
 }
 
+// ---------------------------------------------------------------- GELU
+
+// erf(u) for u >= 0 by Abramowitz & Stegun, Handbook of Mathematical
+// Functions (1964), formula 7.1.26: 1 - t (a1 + t (a2 + ... + t a5)) e^{-u^2},
+// t = 1 / (1 + p u), absolute error <= 1.5e-7 -- far below the bf16 rounding
+// these epilogues end in. Branch-free, one exp and one reciprocal; e^{-u^2}
+// is returned too (GELU's derivative needs it).
+__device__ __forceinline__ float erf_pos(float u, float& eu2) {
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * u);
+  const float poly = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  eu2 = exp2_raw(-u * u * kLog2e);
+  return 1.0f - poly * eu2;
+}
+
+// gelu(x) = x/2 (1 + erf(x / sqrt 2)); gelu'(x) = (1 + erf(x / sqrt 2))/2 + x phi(x)
+__device__ __forceinline__ float gelu(float x) {
+  float eu2;
+  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
+  return 0.5f * x * (1.0f + copysignf(e, x));
+}
+
+__device__ __forceinline__ float gelu_grad(float x) {
+  float eu2;  // e^{-x^2/2}
+  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
+  return 0.5f * (1.0f + copysignf(e, x)) + x * 0.39894228040143268f * eu2;
+}
+
+// Partial column sums -> column sums: out[c] = sum_p part[p * C + c]
+// (colsum.hip). Fixed summation order, so results are reproducible.
+int launch_reduce_partials(const float* part, int P, int C, float* out, hipStream_t st);
+
 // ---------------------------------------------------------------- look-back words
 //
 // One 64-bit word per (time tile, channel) carries a tile's scan state

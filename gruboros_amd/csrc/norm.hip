@@ -157,33 +157,6 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_kernel(
   }
 }
 
-// dw[c] = sum_p dw_part[p][c]. A workgroup owns 64 columns: 16 column lanes
-// (4 columns each) x 16 row lanes that stride over the partial rows; the row
-// lanes are summed in LDS.
-__global__ __launch_bounds__(256) void reduce_rows_kernel(const float* __restrict__ part, int P, int D,
-                                                          float* __restrict__ out) {
-  __shared__ f4 s_acc[16][16];
-  const int cl = threadIdx.x % 16, rl = threadIdx.x / 16;
-  const int col = blockIdx.x * 64 + 4 * cl;
-  f4 acc = io4<float>::fill(0.0f);
-  if (col < D) {
-    for (int p = rl; p < P; p += 16) {
-      const f4 v = io4<float>::load(part + static_cast<int64_t>(p) * D + col);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc.v[j] += v.v[j];
-    }
-  }
-  s_acc[rl][cl] = acc;
-  __syncthreads();
-  if (rl == 0 && col < D) {
-#pragma unroll
-    for (int q = 1; q < 16; ++q)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc.v[j] += s_acc[q][cl].v[j];
-    io4<float>::store(out + col, acc);
-  }
-}
-
 // Register steps per lane: ceil(D / 256) rounded up to a power of two (the
 // extra columns are masked).
 inline int steps_for(int D) {
@@ -237,7 +210,7 @@ int launch_bwd(const float* xn, const float* w, const float* rstd, const void* d
     default:
       return fail(MG_ERR_ARG, "mg_add_rmsnorm_bwd: D=%d unsupported (D <= 4096)", D);
   }
-  hipLaunchKernelGGL(reduce_rows_kernel, dim3((D + 63) / 64), dim3(256), 0, st, dw_part, grid, D, dw);
+  launch_reduce_partials(dw_part, grid, D, dw, st);
   return check_launch("mg_add_rmsnorm_bwd");
 }
 

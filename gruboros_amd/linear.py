@@ -16,6 +16,7 @@ import torch
 import torch.nn.functional as F
 
 from . import gemm
+from ._lib import check, dtype_code, lib, ptr, stream_of
 
 _MM_OUT_DTYPE = None  # whether torch.mm(..., out_dtype=float32) works for bf16 on this build
 
@@ -34,6 +35,39 @@ def _mm_f32(a, b):
     return torch.mm(a, b).float()
 
 
+def _dw_ok(dy2, x2):
+    """Shapes the MFMA weight-gradient product takes (mg_gemm, both operands MN-contiguous)."""
+    return (dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and dy2.stride(1) == 1 and x2.stride(1) == 1
+            and dy2.shape[1] % 8 == 0 and x2.shape[1] % 8 == 0 and dy2.stride(0) % 8 == 0 and x2.stride(0) % 8 == 0
+            and dy2.data_ptr() % 16 == 0 and x2.data_ptr() % 16 == 0)
+
+
+def column_sum(x2):
+    """fp32 column sums of a 2-D fp32/bf16 tensor with unit inner stride (mg_column_sum)."""
+    N, C = x2.shape
+    if C % 8 or x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        return x2.sum(0, dtype=torch.float32)
+    L = lib()
+    out = torch.empty(C, dtype=torch.float32, device=x2.device)
+    ws = torch.empty(L.mg_column_sum_workspace_bytes(N, C), dtype=torch.uint8, device=x2.device)
+    check(L.mg_column_sum(dtype_code(x2.dtype), ptr(x2), x2.stride(0), N, C, ptr(out), ptr(ws), ws.numel(),
+                          stream_of(x2)), "mg_column_sum")
+    return out
+
+
+def gelu_backward(dh, pre, want_bias_grad=True):
+    """(bf16(dh * gelu'(pre)), its fp32 column sums) for bf16 [N, C] inputs (mg_gelu_bwd)."""
+    N, C = pre.shape
+    L = lib()
+    dpre = torch.empty_like(pre)
+    db = torch.empty(C, dtype=torch.float32, device=pre.device) if want_bias_grad else None
+    ws = torch.empty(L.mg_column_sum_workspace_bytes(N, C) if want_bias_grad else 16, dtype=torch.uint8,
+                     device=pre.device)
+    check(L.mg_gelu_bwd(ptr(dh), dh.stride(0), ptr(pre), pre.stride(0), ptr(dpre), dpre.stride(0), ptr(db), N, C,
+                        ptr(ws), ws.numel(), stream_of(pre)), "mg_gelu_bwd")
+    return dpre, db
+
+
 def bf16_copy(w):
     """The bf16 copy of fp32 parameter w, re-made if w changed in place."""
     cache = getattr(w, "_mg_bf16", None)
@@ -46,7 +80,7 @@ def bf16_copy(w):
 class BF16Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, b, wb):
-        bb = b.to(torch.bfloat16) if b is not None else None
+        bb = bf16_copy(b) if b is not None else None
         y = F.linear(x, wb, bb)
         ctx.save_for_backward(x, wb)
         ctx.has_bias = b is not None
@@ -61,9 +95,10 @@ class BF16Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = torch.mm(dy2, wb).reshape(*dy.shape[:-1], in_f)
         if ctx.needs_input_grad[1]:
-            dw = _mm_f32(dy2.t(), x.reshape(-1, in_f))
+            x2 = x.reshape(-1, in_f)
+            dw = gemm.linear_dw(dy2, x2) if _dw_ok(dy2, x2) else _mm_f32(dy2.t(), x2)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = dy2.sum(0, dtype=torch.float32)
+            db = column_sum(dy2)
         return dx, dw, db, None
 
 
@@ -119,14 +154,49 @@ class BF16FeedForward(torch.autograd.Function):
 FUSED_FEED_FORWARD = False
 
 
+class BF16FeedForwardLib(torch.autograd.Function):
+    """Linear -> GELU -> Linear in bf16 with library GEMMs (hipBLASLt via
+    torch) and this library's GELU backward fused with the first bias
+    gradient, plus its column sums for the second."""
+
+    @staticmethod
+    def forward(ctx, x, w1, b1, w2, b2, w1b, w2b, b1b, b2b):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        pre = F.linear(x2, w1b, b1b)
+        h = F.gelu(pre)
+        y = F.linear(h, w2b, b2b)
+        ctx.save_for_backward(x2, pre, h, w1b, w2b)
+        return y.view(*shape[:-1], w2b.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, pre, h, w1b, w2b = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        if dy2.dtype != torch.bfloat16:
+            dy2 = dy2.to(torch.bfloat16)
+        if not dy2.is_contiguous():
+            dy2 = dy2.contiguous()
+        dh = torch.mm(dy2, w2b)
+        dpre, db1 = gelu_backward(dh, pre)
+        dw2 = gemm.linear_dw(dy2, h) if _dw_ok(dy2, h) else _mm_f32(dy2.t(), h)
+        db2 = column_sum(dy2)
+        dx = torch.mm(dpre, w1b).view(*dy.shape[:-1], w1b.shape[1])
+        dw1 = gemm.linear_dw(dpre, x2) if _dw_ok(dpre, x2) else _mm_f32(dpre.t(), x2)
+        return dx, dw1, db1, dw2, db2, None, None, None, None
+
+
 def feed_forward(x, ff):
     """ff = nn.Sequential(Linear, GELU, Linear) applied to x in x's dtype."""
     l1, l2 = ff[0], ff[2]
     if x.dtype == l1.weight.dtype:
         return l2(F.gelu(l1(x)))
-    if not FUSED_FEED_FORWARD:
-        return linear(F.gelu(linear(x, l1)), l2)
     if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32 or l1.bias is None or l2.bias is None:
         raise TypeError(f"unsupported feed-forward: activations {x.dtype}, weight {l1.weight.dtype}")
-    return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
-                                 bf16_copy(l2.weight))
+    if FUSED_FEED_FORWARD:
+        return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
+                                     bf16_copy(l2.weight))
+    return BF16FeedForwardLib.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
+                                    bf16_copy(l2.weight), bf16_copy(l1.bias), bf16_copy(l2.bias))

@@ -251,6 +251,26 @@ int mg_logits_cross_entropy(const void* embed, int64_t lde, const void* w, int64
                             float* loss_part, int* bad_label, int N, int D, int V,
                             float scale, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Bias gradients of the FeedForward linears (reference mingru/minLM.py:17-23:
+ * autograd of nn.Linear's bias and of nn.GELU), over N token rows.
+ *
+ * mg_column_sum: out[c] = sum_n x[n, c]  (x fp32 or bf16, row stride ld;
+ *   out fp32 [C], written).
+ * mg_gelu_bwd:   dpre[n, c] = bf16(dh[n, c] * gelu'(pre[n, c])) (bf16 in and
+ *   out, gelu(x) = x/2 (1 + erf(x/sqrt 2))), and when dbias is given,
+ *   dbias[c] = sum_n dpre[n, c] (of the bf16 values; fp32 [C], written).
+ * Both sum in a fixed order (reproducible) through a workspace of
+ * mg_column_sum_workspace_bytes(N, C) bytes. C % 8 == 0, strides % 8 == 0,
+ * 16-byte aligned pointers.
+ * ---------------------------------------------------------------------- */
+size_t mg_column_sum_workspace_bytes(int64_t N, int C);
+int mg_column_sum(int dtype, const void* x, int64_t ld, int64_t N, int C, float* out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
+                void* dpre, int64_t ld_out, float* dbias, int64_t N, int C,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -173,3 +173,24 @@ def test_streaming_loss_head_matches_fp64(N, D, V):
     assert _rel(dl[:, :V].float(), logits.grad) < 4e-3
     assert bool((dl[:, V:] == 3.0).all())  # padding columns untouched
     assert int(bad) == 0
+
+
+@pytest.mark.parametrize("N,C", [(1, 8), (777, 1024), (16376, 4096), (300, 264)])
+def test_column_sum_and_gelu_backward(N, C):
+    """mg_column_sum and mg_gelu_bwd vs fp64 torch (column sums; GELU's exact backward)."""
+    from gruboros_amd.linear import column_sum, gelu_backward
+
+    g = torch.Generator(device=DEV).manual_seed(N + C)
+    x = torch.randn(N, C, device=DEV, generator=g).to(torch.bfloat16)
+    pre = (torch.randn(N, C, device=DEV, generator=g) * 2).to(torch.bfloat16)
+    s = column_sum(x)
+    ref = x.double().sum(0)
+    assert (s.double() - ref).abs().max() <= 1e-5 * (x.double().abs().sum(0).max() + 1)
+    xf = x.float()
+    assert _rel(column_sum(xf), ref) < 1e-6
+    dpre, db = gelu_backward(x, pre)
+    p64 = pre.double().cpu().requires_grad_(True)
+    F.gelu(p64).backward(x.double().cpu())
+    assert _rel(dpre, p64.grad) < 4e-3
+    # the bias gradient sums the rounded dpre values
+    assert (db.double() - dpre.double().sum(0)).abs().max() <= 1e-5 * (dpre.double().abs().sum(0).max() + 1)
