@@ -132,6 +132,86 @@ def bench_scan(reps=20, B=16, T=8192, Di=2048):
     }
 
 
+def _event_time(fn, reps):
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps  # ms
+
+
+def bench_kernels(reps=20, N=8 * 2047, D=1024, F=4096, V=256):
+    """Per-kernel figures at the cfg3 shapes (16,376 token rows): HBM GB/s of
+    the fused norm (algorithmic bytes: fwd 12, bwd 16 per element) and the
+    streaming loss head, TFLOP/s of the hand-written MFMA products."""
+    import torch
+
+    from gruboros_amd import _lib, gemm
+    from gruboros_amd.norm import FP32_EPS
+
+    L = _lib.lib()
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+    x = torch.randn(N, D, device=dev, generator=g)
+    delta = torch.randn(N, D, device=dev, generator=g).to(torch.bfloat16)
+    w = torch.rand(D, device=dev, generator=g) + 0.5
+    x_out = torch.empty_like(x)
+    y = torch.empty(N, D, device=dev, dtype=torch.bfloat16)
+    rstd = torch.empty(N, device=dev)
+    st = _lib.stream_of(x)
+    P = _lib.ptr
+
+    def nf():
+        _lib.check(L.mg_add_rmsnorm_fwd(P(x), 1, P(delta), P(w), P(x_out), 1, P(y), P(rstd), N, D, FP32_EPS, st))
+    ms = _event_time(nf, reps)
+    out["add_rmsnorm_fwd"] = {"us": ms * 1e3, "GBs": 12 * N * D / (ms * 1e-3) / 1e9}
+    dy = torch.randn(N, D, device=dev, generator=g).to(torch.bfloat16)
+    dres = torch.randn(N, D, device=dev, generator=g)
+    dx = torch.empty_like(x)
+    dd = torch.empty_like(delta)
+    dw = torch.empty(D, device=dev)
+    ws = torch.empty(L.mg_add_rmsnorm_bwd_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+
+    def nb():
+        _lib.check(L.mg_add_rmsnorm_bwd(P(x_out), P(w), P(rstd), 1, P(dy), P(dres), P(dx), 1, P(dd), P(dw), N, D,
+                                        P(ws), ws.numel(), st))
+    ms = _event_time(nb, reps)
+    out["add_rmsnorm_bwd"] = {"us": ms * 1e3, "GBs": 16 * N * D / (ms * 1e-3) / 1e9}
+
+    e = torch.randn(N, D, device=dev, generator=g).to(torch.bfloat16)
+    wl = (torch.randn(V, D, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    lab = torch.randint(0, V, (N,), device=dev, generator=g)
+    dl = torch.empty(N, V, device=dev, dtype=torch.bfloat16)
+    part = torch.empty(L.mg_logits_cross_entropy_partials(N), device=dev)
+
+    def ce():
+        _lib.check(L.mg_logits_cross_entropy(P(e), D, P(wl), D, P(lab), P(dl), V, P(part), None, N, D, V, 1.0 / N, st))
+    ms = _event_time(ce, reps)
+    out["logits_cross_entropy"] = {"us": ms * 1e3, "GBs": (2 * N * D + 2 * V * D + 8 * N + 2 * N * V) / (ms * 1e-3) / 1e9,
+                                   "TFLOPs": 2.0 * N * D * V / (ms * 1e-3) / 1e12}
+    gemms = {}
+    for name, fin, fout in (("to_hidden_and_gate", D, 2 * D), ("ff_in", D, F), ("ff_out", F, D)):
+        xa = torch.randn(N, fin, device=dev, generator=g).to(torch.bfloat16)
+        wa = (torch.randn(fout, fin, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        da = torch.randn(N, fout, device=dev, generator=g).to(torch.bfloat16)
+        fl = 2.0 * N * fin * fout
+        for kind, fn in (("fwd", lambda: gemm.linear_fwd(xa, wa)), ("dx", lambda: gemm.linear_dx(da, wa)),
+                         ("dw", lambda: gemm.linear_dw(da, xa))):
+            ms = _event_time(fn, reps)
+            gemms[f"{name}_{kind}"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                                       "frac_bf16_peak": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+    out["mfma_gemm"] = gemms
+    return out
+
+
 def cpu_baseline(seconds_budget=20.0, B=1, S=512, dim=1024, depth=8):
     """The oracle's fp32 restatement of the reference step (mingru/minLM.py:86-155
     forward + autograd backward) on the host's cores, on a bounded sample of cfg3:
@@ -182,7 +262,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["train", "scan"], default=None)
+    ap.add_argument("--only", choices=["train", "scan", "kernels"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy (torch copy kernel): the known-size "
                          "reference for FETCH_SIZE/WRITE_SIZE counter scaling")
@@ -210,10 +290,13 @@ def main():
         print("[bench] copy calibration: 3 x 1 GiB device copies (1073741824 B read + written each)",
               file=sys.stderr, flush=True)
 
-    train = scan = None
+    train = scan = kern = None
     if args.only in (None, "scan"):
         scan = bench_scan(args.scan_reps)
         print(f"[bench] scan {json.dumps(scan)}", file=sys.stderr, flush=True)
+    if args.only in (None, "kernels"):
+        kern = bench_kernels()
+        print(f"[bench] kernels {json.dumps(kern)}", file=sys.stderr, flush=True)
     if args.only in (None, "train"):
         train = bench_train(args.steps, args.warmup)
         print(f"[bench] train {json.dumps(train)}", file=sys.stderr, flush=True)
@@ -254,6 +337,8 @@ def main():
                                 "unit": "TFLOP/s", "frac": train["tflops"] / BF16_PEAK_TFLOPS,
                                 "flops_per_step": train["flops_per_step"]}
         out["tokens_per_s_predicted"] = 8 * 2047 / (train["ms_per_step"] * 1e-3)
+    if kern:
+        out["kernels"] = kern
     if cpu:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
