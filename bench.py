@@ -47,7 +47,9 @@ def cfg3_matmul_params(dim=1024, depth=8, ff_mult=4, vocab=256, expansion=1.0):
     return depth * per_layer + vocab * dim
 
 
-def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8):
+def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8, accum=1):
+    """One optimizer step = `accum` forward+backward micro-steps on [B, S] ids (the loss
+    scaled by 1/accum as in train.py:798-800), then the Schedule-Free AdamW step."""
     import torch
 
     from gruboros_amd.mingru.minLM import minLM
@@ -59,11 +61,12 @@ def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8):
     opt = AdamWScheduleFree(model.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
     opt.train()
     gen = torch.Generator(device="cuda").manual_seed(0)
-    ids = torch.randint(0, 256, (B, S), device="cuda", generator=gen)
+    ids = [torch.randint(0, 256, (B, S), device="cuda", generator=gen) for _ in range(accum)]
 
     def step():
-        loss = model(ids, return_loss=True)
-        loss.backward()
+        for i in range(accum):
+            loss = model(ids[i], return_loss=True)
+            (loss / accum if accum > 1 else loss).backward()
         opt.step()
         opt.zero_grad(set_to_none=True)
         return loss
@@ -80,9 +83,10 @@ def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / steps
-    flops = 6.0 * cfg3_matmul_params(dim, depth) * B * (S - 1)
-    return {"ms_per_step": ms, "wall_s": wall, "tokens_per_step": B * S, "loss": float(loss.detach()),
-            "tflops": flops / (ms * 1e-3) / 1e12, "flops_per_step": flops}
+    flops = 6.0 * cfg3_matmul_params(dim, depth) * B * (S - 1) * accum
+    return {"ms_per_step": ms, "wall_s": wall, "tokens_per_step": B * S * accum, "loss": float(loss.detach()),
+            "tflops": flops / (ms * 1e-3) / 1e12, "flops_per_step": flops,
+            "params": sum(p.numel() for p in model.parameters())}
 
 
 def bench_scan(reps=20, B=16, T=8192, Di=2048):
@@ -263,6 +267,9 @@ def main():
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["train", "scan", "kernels"], default=None)
+    ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
+                    help="training workload for `value`: cfg3 (the BASELINE metric, default) or cfg5 "
+                         "(~1B params: d2048 L24, batch 4 x seq 4096, gradient accumulation 4)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy (torch copy kernel): the known-size "
                          "reference for FETCH_SIZE/WRITE_SIZE counter scaling")
@@ -298,7 +305,10 @@ def main():
         kern = bench_kernels()
         print(f"[bench] kernels {json.dumps(kern)}", file=sys.stderr, flush=True)
     if args.only in (None, "train"):
-        train = bench_train(args.steps, args.warmup)
+        if args.workload == "cfg5":
+            train = bench_train(args.steps, args.warmup, B=4, S=4096, dim=2048, depth=24, accum=4)
+        else:
+            train = bench_train(args.steps, args.warmup)
         print(f"[bench] train {json.dumps(train)}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
@@ -318,9 +328,13 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (uniform random byte ids; random-init weights; scan inputs N(0,1))",
-        "config": {"workload": "cfg3 minLM train step (vocab 256, d1024, L8, ff4, exp1.0, B8, seq2048, "
-                               "SF-AdamW) for value; cfg2 scan B16 T8192 H2048 bf16 for roofline",
-                   "global_batch": 8, "seq_len": 2048, "parallelism": "single GPU"},
+        "config": ({"workload": "cfg3 minLM train step (vocab 256, d1024, L8, ff4, exp1.0, B8, seq2048, "
+                                "SF-AdamW) for value; cfg2 scan B16 T8192 H2048 bf16 for roofline",
+                    "global_batch": 8, "seq_len": 2048, "parallelism": "single GPU"}
+                   if args.workload == "cfg3" else
+                   {"workload": "cfg5 minLM train step (vocab 256, d2048, L24, ff4, exp1.0, B4, seq4096, "
+                                "grad accum 4, SF-AdamW) for value; cfg2 scan for roofline",
+                    "global_batch": 16, "seq_len": 4096, "parallelism": "single GPU"}),
     }
     if scan:
         bwd_gbs = scan["bwd_GBs"]
@@ -336,7 +350,8 @@ def main():
         out["step_roofline"] = {"bound": "mfma", "achieved": train["tflops"], "peak": BF16_PEAK_TFLOPS,
                                 "unit": "TFLOP/s", "frac": train["tflops"] / BF16_PEAK_TFLOPS,
                                 "flops_per_step": train["flops_per_step"]}
-        out["tokens_per_s_predicted"] = 8 * 2047 / (train["ms_per_step"] * 1e-3)
+        out["tokens_per_s_predicted"] = train["tokens_per_step"] * (1 - 1 / (2048 if args.workload == "cfg3" else 4096)) \
+            / (train["ms_per_step"] * 1e-3)
     if kern:
         out["kernels"] = kern
     if cpu:

@@ -157,3 +157,29 @@ def test_tbptt_continuity(dtype):
 
 def _logits(m, ids, prev):
     return m.logits_and_hiddens(ids, prev)
+
+
+def test_tbptt_continuity_cfg4_full_size():
+    """cfg4 at its real size: minLM d1024 L8 bf16, batch 4, 65,536 byte
+    ids split into 32 chunks of 2048 with prev_hiddens carried and detached as in
+    train.py:783-804. Frozen weights: the chunked forward must equal one forward over
+    cat(chunk[:, :-1]) (65,504 positions), per position and in the final hiddens."""
+    m, _ = _model(1024, 8, 1.0, torch.bfloat16, seed=3)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    ids = torch.randint(0, 256, (4, 65536), device=DEV, generator=g)
+    chunks = ids.split(2048, dim=1)
+    h = None
+    errs, norms = [], []
+    with torch.no_grad():
+        full, hf = _logits(m, torch.cat([c[:, :-1] for c in chunks], 1), None)
+        for i, c in enumerate(chunks):
+            logits, h = _logits(m, c[:, :-1], h)
+            h = [t.detach() for t in h]
+            ref = full[:, i * 2047:(i + 1) * 2047]
+            errs.append(float((logits.float() - ref.float()).norm()))
+            norms.append(float(ref.float().norm()))
+    rel = (sum(e * e for e in errs) ** 0.5) / (sum(n * n for n in norms) ** 0.5)
+    assert rel <= 2e-2, rel
+    assert max(e / n for e, n in zip(errs, norms)) <= 2e-2  # no drift along the 32 chunks
+    for a, b in zip(h, hf):
+        assert _rel(a, b) <= 2e-2
