@@ -14,11 +14,17 @@
 // Workgroup tile BM x BN x 64 (BM, BN in {128, 256}), waves in a WM x WN
 // grid, each owning (BM/WM) x (BN/WN) as 32 x 32 MFMA blocks. Operand tiles
 // go from memory straight into LDS (buffer_load ... lds), two stages: the
-// loads of tile k+1 are in flight while tile k is multiplied, one barrier
-// per k-tile. K-contiguous tiles sit in LDS as [row][64 k] (128-byte rows,
-// 16-byte chunk c of row r at chunk c ^ ((r ^ (r >> 3)) & 7)) and a fragment
-// is one 16-byte LDS read; MN-contiguous tiles stay [64 k][rows] and their
-// fragments come through the LDS transpose read (two 8-byte reads).
+// loads of tile k+1 are in flight while tile k is multiplied. K-contiguous
+// tiles sit in LDS as [row][64 k] (128-byte rows, 16-byte chunk c of row r
+// at chunk c ^ ((r ^ (r >> 3)) & 7)) and a fragment is one 16-byte LDS
+// read; MN-contiguous tiles stay [64 k][rows] and their fragments come
+// through the LDS transpose read (two 8-byte reads).
+// Two main loops (measured on MI355X, the faster one per layout):
+//   mainloop     one barrier per k-tile, the fragments of the next k-step
+//                (also across tiles) read under the MFMAs of the current one;
+//   mainloop_pp  256 x 256 with an MN-contiguous B (the input gradient):
+//                two wave groups alternate between reading a whole k-tile of
+//                fragments and multiplying it, a barrier between phases.
 //
 // The MFMA is fed the B fragment as its first operand and the A fragment as
 // its second, so a lane's accumulator holds C[m][n..n+3] (4 consecutive
@@ -100,21 +106,22 @@ struct Loader<R, true, T> {
   static constexpr int kPerWave = R * 8 / 64 / (T / 64);  // wave instructions per tile and wave
   static_assert(kPerWave >= 1 && R * 8 % T == 0, "tile rows vs threads");
 
-  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int, int k0, int K) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // all of this wave's load instructions for the tile at (r0, k0); k >= kmax reads zero
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax) {
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int b = wave * kPerWave + i;
-      const int r = b * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);  // global chunk stored at LDS chunk lane & 7
-      const int kk = k0 + c * 8;
-      const uint32_t off = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
-                                               16, kk < K ? off : kOutOfRange, 0, 0, 0);
-    }
+    for (int i = 0; i < kPerWave; ++i) one(o, stage, r0, rmax, k0, kmax, i);
   }
-  __device__ __forceinline__ void store(uint4*) {}
-  static constexpr int kWrites = 0;
+  // load instruction i of this wave
+  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int, int k0, int kmax, int i) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = wave * kPerWave + i;
+    const int r = b * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);  // global chunk stored at LDS chunk lane & 7
+    const int kk = k0 + c * 8;
+    const uint32_t off = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
+                                             16, kk < kmax ? off : kOutOfRange, 0, 0, 0);
+  }
 };
 
 // MN-contiguous operands also go straight into LDS, kept as stored: a tile
@@ -132,21 +139,20 @@ struct Loader<R, false, T> {
   static constexpr int kPerWave = 64 * kChunksRow / 64 / (T / 64);
   static_assert(kPerWave >= 1 && kChunksRow * 64 % T == 0, "tile rows vs threads");
 
-  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax) {
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int b = wave * kPerWave + i;
-      const int chunk = b * 64 + lane;
-      const int kr = chunk / kChunksRow, cpos = chunk % kChunksRow;
-      const int m = (((cpos >> 1) ^ tr_swz(kr)) << 4) + ((cpos & 1) << 3);  // tile column stored at this chunk
-      const uint32_t off = static_cast<uint32_t>(k0 + kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
-                                               16, r0 + m < rmax ? off : kOutOfRange, 0, 0, 0);
-    }
+    for (int i = 0; i < kPerWave; ++i) one(o, stage, r0, rmax, k0, kmax, i);
   }
-  __device__ __forceinline__ void store(uint4*) {}
-  static constexpr int kWrites = 0;
+  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax, int i) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = wave * kPerWave + i;
+    const int chunk = b * 64 + lane;
+    const int kr = chunk / kChunksRow, cpos = chunk % kChunksRow;
+    const int m = (((cpos >> 1) ^ tr_swz(kr)) << 4) + ((cpos & 1) << 3);  // tile column stored at this chunk
+    const uint32_t off = static_cast<uint32_t>(k0 + kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
+                                             16, (r0 + m < rmax && k0 + kr < kmax) ? off : kOutOfRange, 0, 0, 0);
+  }
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -193,16 +199,25 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 }
 
 // The MFMA main loop of one workgroup tile BM x BN over k-tiles [kt0, kt1):
-// WM x WN waves each accumulate (BM/WM) x (BN/WN) as 32 x 32 blocks.
-template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
+// WM x WN waves each accumulate (BM/WM) x (BN/WN) as 32 x 32 blocks. The
+// loads of tile t+1 are issued at the start of tile t, the fragments of
+// k-step s+1 are read under the MFMAs of step s, one barrier per k-tile.
+// EARLY: the barrier comes before the MFMAs of the tile's last k-step; after
+//   it tile t+1 is visible to every wave, so its first fragments are read
+//   under those MFMAs (faster for 256 x 256 tiles).
+// otherwise: the barrier ends the tile, which leaves the loads the whole tile
+//   to land (faster for the 128 x 128 weight-gradient tiles, two per CU).
+// Either way every wave is done reading stage t & 1 at the barrier, and the
+// next iteration's loads refill it.
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, bool EARLY>
 __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, int n0, int kt0, int kt1,
                                          f32x16 (&acc)[BM / WM / 32][BN / WN / 32]) {
   constexpr int T = 64 * WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
+  constexpr int S = BK / 16;                            // k-steps per tile
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int L = lane & 31, half = lane >> 5;
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -214,46 +229,61 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
   const Operand ob = make_operand(p.B, p.ldb, p.b_span);
   Loader<BM, AK, T> la;
   Loader<BN, BKM, T> lb;
-  if (kt0 < kt1) {
-    la.load(oa, smem, m0, p.M, kt0 * BK, p.K);
-    lb.load(ob, smem + BM * 8, n0, p.N, kt0 * BK, p.K);
-    la.store(smem);
-    lb.store(smem + BM * 8);
-  }
+  const int kmax = min(p.K, kt1 * BK);
+  // Loads of k-tile t (relative to kt0) into stage t & 1. Past kt1 they are
+  // still issued (every wave waits on the same counts) but read as zero.
+  auto issue = [&](int t) {
+    uint4* st = smem + ((t & 1) * kStage);
+    la.load(oa, st, m0, p.M, (kt0 + t) * BK, kmax);
+    lb.load(ob, st + BM * 8, n0, p.N, (kt0 + t) * BK, kmax);
+  };
+  const int n = kt1 - kt0;
+  issue(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  // first tile row of this wave's block i / j
+
   int arow[MB], brow[NB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) arow[i] = wm * (BM / WM) + i * 32;
 #pragma unroll
   for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32;
 
-  // One basic block per k-tile, so the scheduler can interleave: the global
-  // loads of tile k+1 are issued first (unconditionally: past the end of K
-  // they read as zero, and the stage they fill is never read), the LDS
-  // fragment reads of step s+1 go ahead of the MFMAs of step s, and the LDS
-  // writes of tile k+1 are spread between the MFMAs of the last step.
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int st = (kt - kt0) & 1;
-    const uint4* As = smem + st * kStage;
+  bf16x8 af[2][MB], bfr[2][NB];
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(smem, arow[i], 0, lane);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(smem + BM * 8, brow[j], 0, lane);
+  }
+  for (int t = 0; t < n; ++t) {
+    issue(t + 1);
+    const uint4* As = smem + (t & 1) * kStage;
     const uint4* Bs = As + BM * 8;
-    uint4* nxt = smem + (st ^ 1) * kStage;
-    la.load(oa, nxt, m0, p.M, (kt + 1) * BK, p.K);
-    lb.load(ob, nxt + BM * 8, n0, p.N, (kt + 1) * BK, p.K);
-    bf16x8 af[2][MB], bfr[2][NB];
+    if constexpr (!EARLY) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(As, arow[i], 0, lane);
+      for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(As, arow[i], 0, lane);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(Bs, brow[j], 0, lane);
+      for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(Bs, brow[j], 0, lane);
+    }
 #pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
+    for (int s = 0; s < S; ++s) {
       const int cur = s & 1;
-      if (s + 1 < BK / 16) {
+      if (s + 1 < S) {
 #pragma unroll
         for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(As, arow[i], s + 1, lane);
 #pragma unroll
         for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bs, brow[j], s + 1, lane);
+      } else if constexpr (EARLY) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < n) {
+          const uint4* An = smem + ((t + 1) & 1) * kStage;
+          const uint4* Bn = An + BM * 8;
+#pragma unroll
+          for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(An, arow[i], 0, lane);
+#pragma unroll
+          for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bn, brow[j], 0, lane);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -261,25 +291,140 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
 #pragma unroll
         for (int j = 0; j < NB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
-      if (s == BK / 16 - 1) {
-        la.store(nxt);
-        lb.store(nxt + BM * 8);
-        // spread the LDS writes of register-staged operands between the MFMAs
-        constexpr int kW = decltype(la)::kWrites + decltype(lb)::kWrites;
-        if constexpr (kW > 0) {
-#pragma unroll
-          for (int q = 0; q < MB * NB; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x200, (kW + MB * NB - 1) / (MB * NB), 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          }
-        }
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    if constexpr (!EARLY) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
   }
+  // the zero-reading loads issued for tile n may still be landing in LDS,
+  // which the epilogue reuses
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
 
+// Ping-pong main loop, 256 x 256 tiles, 8 waves in two groups of four (one
+// wave of each group per SIMD; group g owns tile rows 128 g .. 128 g + 127,
+// each wave 128 x 64). The groups alternate, a workgroup barrier between
+// phases: while one group multiplies a whole k-tile from registers, the
+// other reads its fragments of that k-tile from LDS.
+//   phase 2t:   group 0 reads tile t        group 1 multiplies tile t-1
+//   phase 2t+1: group 0 multiplies tile t   group 1 reads tile t
+// Every wave issues its share of tile t+1's loads at the start of phase 2t
+// (stage t+1 & 1 was last read in phase 2t-1) and waits for them at the end
+// of phase 2t+1. (Spreading the loads between the reads and MFMAs measured
+// slower for this operand layout.)
+template <bool AK, bool BKM>
+__device__ __forceinline__ void mainloop_pp(const Params& p, uint4* smem, int m0, int n0, int kt0, int kt1,
+                                            f32x16 (&acc)[4][2]) {
+  constexpr int BM = 256, BN = 256, T = 512, MB = 4, NB = 2, S = BK / 16;
+  constexpr int kStage = (BM + BN) * 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / 4, wn = wave % 4;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  Loader<BM, AK, T> la;
+  Loader<BN, BKM, T> lb;
+  constexpr int LA = decltype(la)::kPerWave, LB = decltype(lb)::kPerWave;
+  static_assert(LA + LB == 2 * S, "two load instructions per k-step");
+  const int kmax = min(p.K, kt1 * BK);
+  auto dma = [&](int t, int q) {  // load instruction q of k-tile t
+    uint4* st = smem + ((t & 1) * kStage);
+    if (q < LA) la.one(oa, st, m0, p.M, (kt0 + t) * BK, kmax, q);
+    else lb.one(ob, st + BM * 8, n0, p.N, (kt0 + t) * BK, kmax, q - LA);
+  };
+
+  // K-contiguous fragment (tile row r = r0 + 32 i + lane % 32, k-step s) at
+  // byte r * 128 + (((2 s + half) ^ f(r)) * 16), f(r) = (r ^ (r >> 3)) & 7.
+  // f(r0 + 32 i + l) = f(r0 + l) ^ (4 if i is odd), so with
+  // P_par = (r0 + l) * 128 + ((half ^ f(r0 + l) ^ 4 par) * 16) the address
+  // is (P_{i&1} ^ 32 s) + 4096 i. The xor is redone at each read (volatile)
+  // instead of keeping 16 addresses live next to 224 registers of
+  // fragments and accumulators.
+  const int L = lane & 31, half = lane >> 5;
+  auto kbase = [&](int r0, int par) -> uint32_t {
+    const int r = r0 + L;
+    return static_cast<uint32_t>(r * 128 + (((half ^ ((r ^ (r >> 3)) & 7)) ^ (4 * par)) << 4));
+  };
+  const uint32_t pa0 = kbase(wm * 128, 0), pa1 = kbase(wm * 128, 1);
+  const uint32_t pb0 = kbase(wn * 64, 0), pb1 = kbase(wn * 64, 1);
+  auto kread = [&](const uint4* tile, uint32_t P, int s, int i) -> bf16x8 {
+    uint32_t x;
+    asm volatile("v_xor_b32 %0, %1, %2" : "=v"(x) : "n"(32 * s), "v"(P));
+    return __builtin_bit_cast(bf16x8,
+                              *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tile) + x + 4096 * i));
+  };
+  bf16x8 fa[S][MB], fb[S][NB];
+  auto frag_a = [&](const uint4* As, int s, int i) -> bf16x8 {
+    if constexpr (AK) return kread(As, (i & 1) ? pa1 : pa0, s, i);
+    else return read_frag<BM, AK>(As, wm * 128 + i * 32, s, lane);
+  };
+  auto frag_b = [&](const uint4* Bs, int s, int j) -> bf16x8 {
+    if constexpr (BKM) return kread(Bs, (j & 1) ? pb1 : pb0, s, j);
+    else return read_frag<BN, BKM>(Bs, wn * 64 + j * 32, s, lane);
+  };
+  auto issue = [&](int t) {
+#pragma unroll
+    for (int q = 0; q < LA + LB; ++q) dma(t, q);
+  };
+  // all fragments of tile t
+  auto read_all = [&](int t) {
+    const uint4* As = smem + (t & 1) * kStage;
+    const uint4* Bs = As + BM * 8;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) fa[s][i] = frag_a(As, s, i);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) fb[s][j] = frag_b(Bs, s, j);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  // the MFMAs of the fragments in registers
+  auto multiply = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s][j], fa[s][i], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int n = kt1 - kt0;
+  issue(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (wm == 0) {
+    for (int t = 0; t < n; ++t) {
+      issue(t + 1);
+      read_all(t);
+      __syncthreads();
+      multiply();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+  } else {
+    for (int t = 0; t < n; ++t) {
+      issue(t + 1);
+      if (t > 0) multiply();
+      __syncthreads();
+      read_all(t);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+    multiply();
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 }
 
 // Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
@@ -299,7 +444,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   const int wm = wave / WN, wn = wave % WN;
   const int L = lane & 31, half = lane >> 5;
   f32x16 acc[MB][NB];
-  mainloop<BM, BN, WM, WN, AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);
+  if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
+    mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);
+  else
+    mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256)>(p, smem, m0, n0, kt0, kt1, acc);
 
   // Epilogue, one 32-row block of the wave's (BM/2) x (BN/2) region at a
   // time: the accumulators go to a wave-private LDS block and come back as
@@ -379,7 +527,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     } else {
       // The GELU epilogues stay runtime loops (unrolled they are more code
       // than the instruction cache holds); the others are unrolled.
-#pragma unroll (EPI == EPI_BIAS_GELU || EPI == EPI_GELU_GRAD) ? 2 : 32
+      constexpr int kStoreUnroll = (EPI == EPI_BIAS_GELU || EPI == EPI_GELU_GRAD) ? 2 : 32;
+#pragma unroll kStoreUnroll
       for (int t = 0; t < 32 / RPI; ++t) {
         const int r = t * RPI + lane / CQ;
         const int m = row0 + i * 32 + r, n = ncol;
@@ -453,7 +602,7 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int L = lane & 31, half = lane >> 5;
   f32x16 acc[MB][NB];
-  mainloop<BM, BN, WM, WN, true, true>(p, smem, m0, 0, 0, (p.K + BK - 1) / BK, acc);
+  mainloop<BM, BN, WM, WN, true, true, false>(p, smem, m0, 0, 0, (p.K + BK - 1) / BK, acc);
 
   // logits tile [64][256] fp32 in LDS, 16-byte chunk c of row r at c ^ (r & 63)
   float* tile = reinterpret_cast<float*>(smem);

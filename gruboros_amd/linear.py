@@ -119,14 +119,14 @@ class BF16FeedForward(torch.autograd.Function):
     product dY W2 is multiplied by GELU'(pre-activation) in its epilogue."""
 
     @staticmethod
-    def forward(ctx, x, w1, b1, w2, b2, w1b, w2b):
+    def forward(ctx, x, w1, b1, w2, b2, w1b, w2b, b2b):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         if not x2.is_contiguous():
             x2 = x2.contiguous()
         pre = torch.empty(x2.shape[0], w1b.shape[0], device=x.device, dtype=torch.bfloat16)
         h = gemm.linear_fwd(x2, w1b, b1.detach().contiguous(), gelu_pre=pre)
-        y = F.linear(h, w2b, b2.detach().to(torch.bfloat16))
+        y = F.linear(h, w2b, b2b)
         ctx.save_for_backward(x2, pre, h, w1b, w2b)
         return y.view(*shape[:-1], w2b.shape[0])
 
@@ -139,12 +139,12 @@ class BF16FeedForward(torch.autograd.Function):
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
         dpre = gemm.linear_dx(dy2, w2b, gelu_pre=pre)
-        dw2 = _mm_f32(dy2.t(), h)
-        db2 = dy2.sum(0, dtype=torch.float32)
+        dw2 = gemm.linear_dw(dy2, h) if _dw_ok(dy2, h) else _mm_f32(dy2.t(), h)
+        db2 = column_sum(dy2)
         dx = torch.mm(dpre, w1b).view(*dy.shape[:-1], w1b.shape[1])
-        dw1 = _mm_f32(dpre.t(), x2)
-        db1 = dpre.sum(0, dtype=torch.float32)
-        return dx, dw1, db1, dw2, db2, None, None
+        dw1 = gemm.linear_dw(dpre, x2) if _dw_ok(dpre, x2) else _mm_f32(dpre.t(), x2)
+        db1 = column_sum(dpre)
+        return dx, dw1, db1, dw2, db2, None, None, None
 
 
 # The fused path is exact and tested, but on MI355X it is not yet faster:
@@ -197,6 +197,6 @@ def feed_forward(x, ff):
         raise TypeError(f"unsupported feed-forward: activations {x.dtype}, weight {l1.weight.dtype}")
     if FUSED_FEED_FORWARD:
         return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
-                                     bf16_copy(l2.weight))
+                                     bf16_copy(l2.weight), bf16_copy(l2.bias))
     return BF16FeedForwardLib.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
                                     bf16_copy(l2.weight), bf16_copy(l1.bias), bf16_copy(l2.bias))
