@@ -720,8 +720,11 @@ using namespace mg;
 
 extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, const void* B, int64_t ldb, int M,
                        int N, int K, int epilogue, const float* bias, void* aux, int64_t ldaux, int c_dtype, void* C,
-                       int64_t ldc, int accumulate, void* stream) {
+                       int64_t ldc, int flags, void* stream) {
   const char* fn = "mg_gemm";
+  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC)) return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
+  const bool accumulate = flags & MG_GEMM_ACCUMULATE;
+  const bool deterministic = flags & MG_GEMM_DETERMINISTIC;
   if (!A || !B || !C) return fail(MG_ERR_ARG, "%s: null operand", fn);
   if (M < 0 || N < 0 || K < 0) return fail(MG_ERR_ARG, "%s: negative size", fn);
   if ((a_layout != MG_KCONTIG && a_layout != MG_MNCONTIG) || (b_layout != MG_KCONTIG && b_layout != MG_MNCONTIG))
@@ -781,7 +784,7 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
   const int nkt = (K + gemm::BK - 1) / gemm::BK;
   const int64_t want_wgs = wgrad ? 2 * gemm::kCUs : gemm::kCUs;
   int splits = 1;
-  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs)
+  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
     splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
   if (K == 0 && accumulate) return MG_OK;
   const bool atomic = accumulate || splits > 1;

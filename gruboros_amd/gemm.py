@@ -12,6 +12,7 @@ from . import _lib
 
 KCONTIG, MNCONTIG = 0, 1
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD = 0, 1, 2, 3
+FLAG_ACCUMULATE, FLAG_DETERMINISTIC = 1, 2
 
 
 def _rows(t, name):
@@ -21,8 +22,14 @@ def _rows(t, name):
     return t.stride(0)
 
 
-def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False):
-    """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm)."""
+def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False,
+         deterministic=None):
+    """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm).
+    deterministic (default: torch.are_deterministic_algorithms_enabled()): no split along K,
+    so fp32 results are the same on every run."""
+    if deterministic is None:
+        deterministic = torch.are_deterministic_algorithms_enabled()
+    flags = (FLAG_ACCUMULATE if accumulate else 0) | (FLAG_DETERMINISTIC if deterministic else 0)
     _lib.require_cuda(a, b, out)
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise _lib.MingruHipError(f"mg_gemm operands must be bfloat16 (got {a.dtype}, {b.dtype})")
@@ -33,7 +40,7 @@ def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None
     L = _lib.lib()
     rc = L.mg_gemm(a_layout, _lib.ptr(a), lda, b_layout, _lib.ptr(b), ldb, M, N, K, epilogue,
                    _lib.ptr(bias) if bias is not None else None, _lib.ptr(aux) if aux is not None else None, ldaux,
-                   _lib.dtype_code(out.dtype), _lib.ptr(out), ldc, int(accumulate), _lib.stream_of(out))
+                   _lib.dtype_code(out.dtype), _lib.ptr(out), ldc, flags, _lib.stream_of(out))
     _lib.check(rc, "mg_gemm")
     return out
 
@@ -60,10 +67,10 @@ def linear_dx(dy, w, *, gelu_pre=None):
                 epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre)
 
 
-def linear_dw(dy, x, out=None, accumulate=False):
+def linear_dw(dy, x, out=None, accumulate=False, deterministic=None):
     """dy [N, out] bf16, x [N, in] bf16 -> dy^T x [out, in] fp32 (written, or added when accumulate)."""
     n, o = dy.shape
     k = x.shape[1]
     if out is None:
         out = torch.empty(o, k, device=dy.device, dtype=torch.float32)
-    return gemm(dy, MNCONTIG, x, MNCONTIG, o, k, n, out, accumulate=accumulate)
+    return gemm(dy, MNCONTIG, x, MNCONTIG, o, k, n, out, accumulate=accumulate, deterministic=deterministic)

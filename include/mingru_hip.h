@@ -209,9 +209,14 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  *   MG_EPI_BIAS_GELU  aux = bf16(acc + bias[n]); C = gelu(aux)   (bf16 C, aux [M, N] bf16, ldaux)
  *   MG_EPI_GELU_GRAD  C = acc * gelu'(aux[m][n])                  (bf16 C, aux as written above)
  *   gelu(x) = x/2 (1 + erf(x/sqrt(2))), nn.GELU()'s exact form.
- * accumulate = 1 (fp32 C, no epilogue): C += A B. fp32 outputs with few
- *   output tiles are split along K across workgroups that add with fp32
- *   atomics; the library zeroes C first unless accumulating.
+ * flags (bit set):
+ *   MG_GEMM_ACCUMULATE (fp32 C, no epilogue): C += A B.
+ *   MG_GEMM_DETERMINISTIC: no split along K. Without it, fp32 outputs with
+ *     few output tiles are split along K across workgroups that add with
+ *     fp32 atomics (the library zeroes C first unless accumulating), so the
+ *     summation order, and the last bit of the result, can vary run to run.
+ *     With it every element is summed by one workgroup in a fixed order and
+ *     the result is the same on every run.
  * Requirements: N % 8 == 0; K % 8 == 0 if an operand is K-contiguous;
  *   M % 8 == 0 if A is MN-contiguous; lda, ldb, ldaux % 8 == 0; ldc % 8 == 0
  *   (bf16 C) or % 4 == 0 (fp32 C); A, B, C, bias, aux 16-byte aligned; each
@@ -223,12 +228,14 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
 #define MG_EPI_BIAS 1
 #define MG_EPI_BIAS_GELU 2
 #define MG_EPI_GELU_GRAD 3
+#define MG_GEMM_ACCUMULATE 1
+#define MG_GEMM_DETERMINISTIC 2
 
 int mg_gemm(int a_layout, const void* A, int64_t lda,
             int b_layout, const void* B, int64_t ldb,
             int M, int N, int K,
             int epilogue, const float* bias, void* aux, int64_t ldaux,
-            int c_dtype, void* C, int64_t ldc, int accumulate, void* stream);
+            int c_dtype, void* C, int64_t ldc, int flags, void* stream);
 
 /* ------------------------------------------------------------------------
  * Streaming loss head: logits GEMM + log-softmax + cross-entropy + gradient.

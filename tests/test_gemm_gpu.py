@@ -113,6 +113,24 @@ def test_gemm_accumulate_and_split():
     assert _rel(acc, ref + base.double()) < 1e-5
 
 
+def test_gemm_deterministic_flag():
+    """Weight-gradient product with and without the split along K: the
+    deterministic form repeats bit for bit and agrees with the split one."""
+    from gruboros_amd.gemm import linear_dw
+
+    g = torch.Generator(device=DEV).manual_seed(11)
+    dy = torch.randn(16376, 1024, device=DEV, generator=g).to(torch.bfloat16)
+    x = torch.randn(16376, 1024, device=DEV, generator=g).to(torch.bfloat16)
+    d1 = linear_dw(dy, x, deterministic=True)
+    d2 = linear_dw(dy, x, deterministic=True)
+    split = linear_dw(dy, x, deterministic=False)
+    assert torch.equal(d1, d2)
+    assert _rel(split, d1) < 1e-6
+    acc = d1.clone()
+    linear_dw(dy, x, out=acc, accumulate=True, deterministic=True)
+    assert _rel(acc, 2 * d1) < 1e-6
+
+
 @pytest.mark.parametrize("which", ["hg_fwd", "hg_dx", "hg_dw", "ff1_fwd", "ff2_dw", "logits_fwd"])
 def test_gemm_model_sizes(which):
     """cfg3 shapes (16376 tokens, d1024, ff 4096, vocab 256) vs torch's fp32 product on the GPU."""

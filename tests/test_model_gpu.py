@@ -183,3 +183,83 @@ def test_tbptt_continuity_cfg4_full_size():
     assert max(e / n for e, n in zip(errs, norms)) <= 2e-2  # no drift along the 32 chunks
     for a, b in zip(h, hf):
         assert _rel(a, b) <= 2e-2
+
+
+def test_checkpoint_resume_and_clonal_merge():
+    """Checkpoint format and resume path of reference train.py: the dict of
+    train.py:710-713 (model_state_dict, optimizer_state_dict, model_config
+    with the keys of train.py:612) written with torch.save, read back with a
+    code-free loader, loaded as at train.py:636-642 (load_state_dict on model
+    and optimizer, then optimizer.train()). Training resumed from it follows
+    the uninterrupted run; the gossip clonal merge
+    (gossip/evolutionary_node.py:296-304) is the same load into a live model.
+    Run with torch's deterministic switch, under which the weight-gradient
+    products do not split along K (no atomics), so both runs add in the same
+    order and the comparison can be exact."""
+    from gruboros_amd.mingru.minLM import minLM
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    config = {"num_tokens": 256, "dim": 64, "depth": 2, "ff_mult": 4, "expansion": 1.0, "enable_conv": False,
+              "dropout": 0.0}
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    batches = [torch.randint(0, 256, (2, 129), device=DEV, generator=gen) for _ in range(4)]
+
+    def make(seed):
+        torch.manual_seed(seed)
+        m = minLM(**config, compute_dtype=torch.bfloat16).to(DEV)
+        opt = AdamWScheduleFree(m.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+        opt.train()
+        return m, opt
+
+    def train(m, opt, ids):
+        loss = m(ids, return_loss=True)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return float(loss.detach())
+
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        _checkpoint_resume(config, batches, make, train)
+    finally:
+        torch.use_deterministic_algorithms(False)
+
+
+def _checkpoint_resume(config, batches, make, train):
+    import io
+
+    a, opt_a = make(0)
+    for ids in batches[:2]:
+        train(a, opt_a, ids)
+    buf = io.BytesIO()
+    torch.save({"step": 2, "model_state_dict": a.state_dict(), "optimizer_state_dict": opt_a.state_dict(),
+                "ema_fitness": 1.0, "model_config": config}, buf)
+    losses_a = [train(a, opt_a, ids) for ids in batches[2:]]
+
+    buf.seek(0)
+    ckpt = torch.load(buf, map_location=DEV, weights_only=True)
+    assert set(ckpt) == {"step", "model_state_dict", "optimizer_state_dict", "ema_fitness", "model_config"}
+    assert list(ckpt["model_config"]) == ["num_tokens", "dim", "depth", "ff_mult", "expansion", "enable_conv",
+                                          "dropout"]
+    st = ckpt["optimizer_state_dict"]["state"]
+    assert len(st) == len(list(a.parameters())) and all(set(v) == {"z", "exp_avg_sq"} for v in st.values())
+    assert ckpt["optimizer_state_dict"]["param_groups"][0]["train_mode"] is True
+
+    # resume into a fresh process-like model (different init), and a clonal
+    # merge into a model that has trained on other data. Each reads its own
+    # copy of the file: torch's Optimizer.load_state_dict keeps the loaded
+    # state tensors themselves (no copy), so two optimizers loading one dict
+    # would share, and both update, the same z and exp_avg_sq.
+    b, opt_b = make(1)
+    c, opt_c = make(2)
+    train(c, opt_c, batches[3])
+    for m, opt in ((b, opt_b), (c, opt_c)):
+        buf.seek(0)
+        ckpt = torch.load(buf, map_location=DEV, weights_only=True)
+        m.load_state_dict(ckpt["model_state_dict"])
+        opt.load_state_dict(ckpt["optimizer_state_dict"])
+        opt.train()
+        losses = [train(m, opt, ids) for ids in batches[2:]]
+        assert losses == losses_a
+        for (n, pa), pb in zip(a.named_parameters(), m.parameters()):
+            assert torch.equal(pb, pa), n
