@@ -132,7 +132,7 @@ def bench_scan(reps=20, B=16, T=8192, Di=2048):
         "fwd_ms": tf, "bwd_ms": tb, "fwd_bwd_ms": tf + tb,
         "fwd_GBs": gbs(6 * n, tf), "bwd_GBs": gbs(12 * n, tb), "fwd_bwd_GBs": gbs(18 * n, tf + tb),
         "fwd_bwd_frac": gbs(18 * n, tf + tb) / HBM_PEAK_GBS,
-        "note": "event times include the look-back workspace clear launched with each kernel",
+        "note": "event times cover the scan kernels only (the look-back workspace is initialised once)",
     }
 
 

@@ -221,17 +221,25 @@ int launch_reduce_partials(const float* part, int P, int C, float* out, hipStrea
 //   tag == 1                : inclusive prefix; value is the carry itself
 // A coefficient is a product of a_t in [0, 1], so its sign bit is free.
 
+// Look-back words: value in the high half, tag in the low half. An inclusive
+// prefix has tag kTagIncl; an aggregate (A, V) carries A's bits with the
+// sign bit set (A is in [0, 1], so its sign bit and bit 30 are free). Bit 30
+// of either tag is the call parity: a workspace alternates parity from call
+// to call, so words left by the previous call read as "not ready" and the
+// words need no clearing between calls.
 constexpr uint32_t kTagIncl = 1u;
 constexpr uint32_t kTagAggBit = 0x80000000u;
+constexpr uint32_t kTagParity = 0x40000000u;
 
-__device__ __forceinline__ void publish_agg(uint64_t* w, float A, float V) {
+__device__ __forceinline__ void publish_agg(uint64_t* w, float A, float V, uint32_t parity) {
   uint64_t x = (static_cast<uint64_t>(__float_as_uint(V)) << 32) |
-               static_cast<uint64_t>(__float_as_uint(A) | kTagAggBit);
+               static_cast<uint64_t>(__float_as_uint(A) | kTagAggBit | (parity ? kTagParity : 0u));
   __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void publish_incl(uint64_t* w, float V) {
-  uint64_t x = (static_cast<uint64_t>(__float_as_uint(V)) << 32) | static_cast<uint64_t>(kTagIncl);
+__device__ __forceinline__ void publish_incl(uint64_t* w, float V, uint32_t parity) {
+  uint64_t x = (static_cast<uint64_t>(__float_as_uint(V)) << 32) |
+               static_cast<uint64_t>(kTagIncl | (parity ? kTagParity : 0u));
   __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -20,6 +20,13 @@
 //     the workspace (decoupled look-back). Each chain of tiles (one channel
 //     block) takes tickets from its own atomic counter, so a tile only ever
 //     waits on tiles of its chain that were started before it.
+//   * The workspace is zeroed once (mg_scan_workspace_init) and then kept
+//     consistent by the kernels: the tile that draws a chain's last ticket
+//     resets the count and flips the chain's parity bit (bit 31 of the
+//     counter), and look-back words carry the parity of the call that wrote
+//     them. Every word a call reads was written by the previous call of the
+//     same direction (or is zero), so stale words never look ready and no
+//     clearing kernel runs per call.
 //   * The backward walks tiles in reverse time order with the adjoint
 //     recurrence. It needs h_{t-1}: it reads the state entering each 8-step
 //     pair of runs once (the forward's fp32 checkpoint when the output is
@@ -29,6 +36,8 @@
 //     g(hidden) - h_{t-1}, a difference of two nearly equal numbers.)
 
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 #include "mg_common.h"
 
@@ -69,19 +78,31 @@ struct Geometry {
   int64_t BD;    // B * Di
 };
 
-// Workspace: one ticket counter per chain, then one look-back word per
-// (tile, channel).
-inline size_t ws_header_bytes(int ncb) { return (static_cast<size_t>(ncb) * 4 + 255) / 256 * 256; }
+// Workspace: ticket counters (one per chain and direction), then one
+// look-back word per (tile, channel) for the forward tiles, then the same for
+// the backward tiles.
+inline size_t ws_header_bytes(int ncb) { return (static_cast<size_t>(ncb) * 2 * 4 + 255) / 256 * 256; }
 
 // Chain and tile of this workgroup. The chain comes from the block index; the
 // tile (time position) from the chain's ticket counter, in start order. The
 // results are wave-uniform, so tile base addresses live in scalar registers.
+// The counter's bit 31 is the chain's parity for this call; the draw of the
+// last ticket resets the count and flips the parity for the next call (no
+// other draw of this call follows it, and the next call starts after this
+// kernel has finished).
+constexpr uint32_t kParityBit = 0x80000000u;
 __device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters, uint32_t* s_ticket,
-                                          bool reverse, int& k, int& b, int& d0) {
+                                          bool reverse, int& k, int& b, int& d0, uint32_t& parity) {
   const int cbi = static_cast<int>(blockIdx.x % static_cast<uint32_t>(g.ncb));
-  if (threadIdx.x == 0) *s_ticket = atomicAdd(counters + cbi, 1u);
+  if (threadIdx.x == 0) {
+    const uint32_t old = atomicAdd(counters + cbi, 1u);
+    if ((old & ~kParityBit) == static_cast<uint32_t>(g.ntiles - 1)) atomicExch(counters + cbi, (old & kParityBit) ^ kParityBit);
+    *s_ticket = old;
+  }
   __syncthreads();
-  const int kk = static_cast<int>(__builtin_amdgcn_readfirstlane(*s_ticket));
+  const uint32_t t = __builtin_amdgcn_readfirstlane(*s_ticket);
+  parity = t >> 31;
+  const int kk = static_cast<int>(t & ~kParityBit);
   k = reverse ? (g.ntiles - 1 - kk) : kk;
   b = cbi / g.nblk_d;
   d0 = (cbi % g.nblk_d) * kTileCh;
@@ -91,18 +112,20 @@ __device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters,
 // scan; +1: later tiles, backward scan) until an inclusive prefix is found,
 // folding aggregates on the way. Returns the state entering tile k of
 // channel c (one channel per lane).
-__device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step) {
+__device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step,
+                                            uint32_t parity) {
   float accA = 1.0f, accV = 0.0f;
   const uint64_t* w = status + static_cast<int64_t>(k + step) * BD + c;
   const int64_t dw = step * BD;
+  const uint32_t par = parity ? kTagParity : 0u;
   while (true) {
     const uint64_t x = poll_word(w);
     const uint32_t tag = static_cast<uint32_t>(x);
     const float val = __uint_as_float(static_cast<uint32_t>(x >> 32));
-    if (tag == kTagIncl) return accA * val + accV;
-    if (tag & kTagAggBit) {
+    if (tag == (kTagIncl | par)) return accA * val + accV;
+    if ((tag & (kTagAggBit | kTagParity)) == (kTagAggBit | par)) {
       accV = accA * val + accV;
-      accA = accA * __uint_as_float(tag & ~kTagAggBit);
+      accA = accA * __uint_as_float(tag & ~(kTagAggBit | kTagParity));
       w += dw;
     } else {
       __builtin_amdgcn_s_sleep(2);
@@ -200,7 +223,8 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
   const int cl = tid % kChLanes;
   const int s = tid / kChLanes;
   int k, b, d0;
-  take_tile(g, counters, &s_ticket, false, k, b, d0);
+  uint32_t parity;
+  take_tile(g, counters, &s_ticket, false, k, b, d0, parity);
   const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
   const int t0 = k * kFwdTileRows + s * kRows;
@@ -236,10 +260,10 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
     if (k == 0) {
       carry = h0 ? h0[c + s] : 0.0f;
     } else {
-      publish_agg(st, TA, TV);
-      carry = look_back1(status, g.BD, c + s, k, -1);
+      publish_agg(st, TA, TV, parity);
+      carry = look_back1(status, g.BD, c + s, k, -1, parity);
     }
-    if (k + 1 < g.ntiles) publish_incl(st, TA * carry + TV);
+    if (k + 1 < g.ntiles) publish_incl(st, TA * carry + TV, parity);
     reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
   }
   __syncthreads();
@@ -329,7 +353,8 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   const int cl = tid % kChLanes;
   const int s = ((tid / kChLanes) % (kSubs / 2)) * 2 + tid / (kChLanes * kSubs / 2);
   int k, b, d0;
-  take_tile(g, counters, &s_ticket, true, k, b, d0);
+  uint32_t parity;
+  take_tile(g, counters, &s_ticket, true, k, b, d0, parity);
   const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
   const int t0 = k * kBwdTileRows + s * kRows;
@@ -414,10 +439,10 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + q;
     float carry = 0.0f;
     if (k != g.ntiles - 1) {
-      publish_agg(st, TA, TM);
-      carry = look_back1(status, g.BD, c + q, k, +1);
+      publish_agg(st, TA, TM, parity);
+      carry = look_back1(status, g.BD, c + q, k, +1, parity);
     }
-    if (k > 0) publish_incl(st, TA * carry + TM);
+    if (k > 0) publish_incl(st, TA * carry + TM, parity);
     reinterpret_cast<float*>(&s_carry[cl])[q] = carry;
   }
   __syncthreads();
@@ -469,7 +494,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
 
 // ------------------------------------------------------------------ host
 
-__global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {
+__global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {  // workspace initialisation
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n16;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
     p[i] = make_uint4(0, 0, 0, 0);
@@ -484,17 +509,21 @@ inline void make_geometry(int B, int T, int Di, int tile_rows, Geometry& g) {
   g.BD = static_cast<int64_t>(B) * Di;
 }
 
-inline size_t ws_bytes(const Geometry& g) {
-  return ws_header_bytes(g.ncb) + static_cast<size_t>(g.ntiles) * g.BD * sizeof(uint64_t);
-}
-
-// One workspace size serves both directions.
+// One workspace serves both directions: counters for both, then the forward
+// words, then the backward words.
 inline size_t ws_bytes_any(int B, int T, int Di) {
   Geometry f, b;
   make_geometry(B, T, Di, kFwdTileRows, f);
   make_geometry(B, T, Di, kBwdTileRows, b);
-  return std::max(ws_bytes(f), ws_bytes(b));
+  return ws_header_bytes(f.ncb) + static_cast<size_t>(f.ntiles + b.ntiles) * f.BD * sizeof(uint64_t);
 }
+
+// Host-side record of initialised workspaces (address -> shape), so that a
+// call on a workspace that was not initialised for its shape is refused
+// rather than reading stale look-back words.
+struct WsShape { int B, T, Di; size_t bytes; };
+std::mutex g_ws_mu;
+std::unordered_map<uintptr_t, WsShape> g_ws;
 
 inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, void* ws, size_t ws_size,
                         Geometry& g) {
@@ -503,10 +532,20 @@ inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, voi
   make_geometry(B, T, Di, tile_rows, g);
   const int64_t nblocks = static_cast<int64_t>(g.ncb) * g.ntiles;
   if (nblocks > 0x7fffffff) return fail(MG_ERR_ARG, "%s: problem too large (%lld tiles)", fn, (long long)nblocks);
-  const size_t need = ws_bytes(g);
+  const size_t need = ws_bytes_any(B, T, Di);
   if (!ws || ws_size < need)
     return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, ws_size, need);
   if (!aligned(ws, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
+  return MG_OK;
+}
+
+// The last check before a launch: the workspace was initialised for this shape.
+inline int check_registered(const char* fn, void* ws, int B, int T, int Di) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  const auto it = g_ws.find(reinterpret_cast<uintptr_t>(ws));
+  if (it == g_ws.end() || it->second.B != B || it->second.T != T || it->second.Di != Di)
+    return fail(MG_ERR_WORKSPACE, "%s: workspace not initialised for B=%d T=%d Di=%d (mg_scan_workspace_init)", fn, B,
+                T, Di);
   return MG_OK;
 }
 
@@ -528,25 +567,24 @@ inline int check_f32vec(const char* fn, const char* name, const void* p) {
   return MG_OK;
 }
 
-inline void zero_ws(void* ws, const Geometry& g, hipStream_t st) {
-  const int64_t n16 = static_cast<int64_t>(ws_bytes(g) / 16);
-  const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
-  hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, st, static_cast<uint4*>(ws), n16);
+// Forward or backward counters and look-back words of a workspace.
+inline uint32_t* ws_counters(void* ws, const Geometry& g, bool bwd) {
+  return static_cast<uint32_t*>(ws) + (bwd ? g.ncb : 0);
 }
-
-inline uint32_t* ws_counters(void* ws) { return static_cast<uint32_t*>(ws); }
-inline uint64_t* ws_status(void* ws, const Geometry& g) {
-  return reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + ws_header_bytes(g.ncb));
+inline uint64_t* ws_status(void* ws, const Geometry& g, bool bwd) {
+  uint64_t* w = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + ws_header_bytes(g.ncb));
+  if (bwd) w += static_cast<int64_t>((g.T + kFwdTileRows - 1) / kFwdTileRows) * g.BD;
+  return w;
 }
 
 template <typename Tin, typename Tout>
 void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0, void* h,
                 int64_t out_sb, int64_t out_ld, float* h_last, float* ckpt, const Geometry& g, void* ws,
                 hipStream_t st) {
-  zero_ws(ws, g, st);
   hipLaunchKernelGGL((scan_fwd_kernel<Tin, Tout>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kFwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
-                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_counters(ws), ws_status(ws, g));
+                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_counters(ws, g, false),
+                     ws_status(ws, g, false));
 }
 
 template <typename Tin, typename Th>
@@ -555,12 +593,11 @@ void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_
                 int64_t g_ld,
                 const float* dh_last, void* dhidden, void* dgate, float* dh0, const Geometry& g, void* ws,
                 hipStream_t st) {
-  zero_ws(ws, g, st);
   hipLaunchKernelGGL((scan_bwd_kernel<Tin, Th>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kBwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
                      static_cast<const Th*>(h), out_sb, out_ld, ckpt, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
-                     static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), dh0, g, ws_counters(ws),
-                     ws_status(ws, g));
+                     static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), dh0, g, ws_counters(ws, g, true),
+                     ws_status(ws, g, true));
 }
 
 }  // namespace scan
@@ -578,6 +615,29 @@ extern "C" size_t mg_scan_workspace_bytes(int B, int T, int Di) {
   return scan::ws_bytes_any(B, T, Di);
 }
 
+extern "C" int mg_scan_workspace_init(void* workspace, size_t workspace_bytes, int B, int T, int Di, void* stream) {
+  const char* fn = "mg_scan_workspace_init";
+  if (B < 1 || T < 1 || Di < 4 || Di % scan::kVec) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
+  const size_t need = scan::ws_bytes_any(B, T, Di);
+  if (!workspace || workspace_bytes < need)
+    return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, workspace_bytes, need);
+  if (!aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
+  const int64_t n16 = static_cast<int64_t>(need / 16);
+  const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
+  hipLaunchKernelGGL(scan::zero_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint4*>(workspace), n16);
+  if (int rc = check_launch(fn)) return rc;
+  std::lock_guard<std::mutex> lock(scan::g_ws_mu);
+  scan::g_ws[reinterpret_cast<uintptr_t>(workspace)] = scan::WsShape{B, T, Di, workspace_bytes};
+  return MG_OK;
+}
+
+extern "C" int mg_scan_workspace_release(void* workspace) {
+  std::lock_guard<std::mutex> lock(scan::g_ws_mu);
+  scan::g_ws.erase(reinterpret_cast<uintptr_t>(workspace));
+  return MG_OK;
+}
+
 extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
                            const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
                            float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
@@ -592,6 +652,9 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "h_last", h_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
+  if (!((in_dtype == MG_BF16 || in_dtype == MG_F32) && (out_dtype == MG_F32 || in_dtype == out_dtype)))
+    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
+  if ((rc = scan::check_registered(fn, workspace, B, T, Di))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
     scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
@@ -624,6 +687,9 @@ extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_f32vec(fn, "dh_last", dh_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh0", dh0))) return rc;
   if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
+  if (!((in_dtype == MG_BF16 || in_dtype == MG_F32) && (out_dtype == MG_F32 || in_dtype == out_dtype)))
+    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
+  if ((rc = scan::check_registered(fn, workspace, B, T, Di))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
     scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,

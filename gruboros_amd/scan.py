@@ -10,6 +10,34 @@ from . import _lib
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 
 
+# Look-back workspaces, one per (device, stream, B, T, Di): initialised
+# (zero-filled) once, then kept consistent by the kernels across calls, which
+# on one stream run in order. Calls on different streams get different
+# workspaces.
+_WORKSPACES = {}
+
+
+def _workspace(device, B, T, Di):
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream, B, T, Di)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        L = lib()
+        wsb = L.mg_scan_workspace_bytes(B, T, Di)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=device)
+        check(L.mg_scan_workspace_init(ptr(ws), wsb, B, T, Di, stream_of(ws)), "mg_scan_workspace_init")
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def release_workspaces():
+    """Free the cached look-back workspaces (they are re-made on demand)."""
+    L = lib()
+    for ws in _WORKSPACES.values():
+        L.mg_scan_workspace_release(ptr(ws))
+    _WORKSPACES.clear()
+
+
 def _vec_ok(t: torch.Tensor) -> bool:
     """Last dim dense and the two outer strides multiples of 4 elements."""
     return t.stride(-1) == 1 and t.stride(0) % 4 == 0 and t.stride(1) % 4 == 0
@@ -34,11 +62,10 @@ def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt=False):
     ckpt = None
     if need_ckpt and out_dtype != torch.float32:
         ckpt = torch.empty(L.mg_scan_ckpt_elems(B, T, Di), dtype=torch.float32, device=hidden.device)
-    wsb = L.mg_scan_workspace_bytes(B, T, Di)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=hidden.device)
+    ws = _workspace(hidden.device, B, T, Di)
     rc = L.mg_scan_fwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
                        ptr(h0), dtype_code(out_dtype), ptr(h), h.stride(0), h.stride(1), ptr(h_last), ptr(ckpt),
-                       B, T, Di, ptr(ws), wsb, stream_of(hidden))
+                       B, T, Di, ptr(ws), ws.numel(), stream_of(hidden))
     check(rc, "mg_scan_fwd")
     return h, h_last, ckpt
 
@@ -54,12 +81,11 @@ def _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0
     if dh_last is not None:
         dh_last = dh_last.reshape(B, Di).to(torch.float32).contiguous()
     dh0 = torch.empty(B, 1, Di, dtype=torch.float32, device=dev) if want_dh0 else None
-    wsb = L.mg_scan_workspace_bytes(B, T, Di)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ws = _workspace(dev, B, T, Di)
     rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
                        ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1), ptr(ckpt),
                        ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0),
-                       B, T, Di, ptr(ws), wsb, stream_of(hidden))
+                       B, T, Di, ptr(ws), ws.numel(), stream_of(hidden))
     check(rc, "mg_scan_bwd")
     return dh0
 

@@ -31,7 +31,7 @@ extern "C" {
 #define MG_OK 0
 #define MG_ERR_ARG 1      /* bad shape, stride, alignment or null pointer */
 #define MG_ERR_DTYPE 2    /* unsupported dtype combination */
-#define MG_ERR_WORKSPACE 3 /* workspace missing or too small */
+#define MG_ERR_WORKSPACE 3 /* workspace missing, too small or not initialised */
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -70,7 +70,18 @@ const char* mg_last_error(void);
  * Supported (in_dtype, out_dtype): (BF16, BF16), (F32, F32), (BF16, F32).
  * ---------------------------------------------------------------------- */
 size_t mg_scan_ckpt_elems(int B, int T, int Di);
-size_t mg_scan_workspace_bytes(int B, int T, int Di);  /* serves fwd and bwd */
+
+/* Look-back workspace (ticket counters and look-back words; serves both
+ * directions). It is zero-filled once by mg_scan_workspace_init, on
+ * `stream`, for one (B, T, Di); the kernels then keep it consistent from
+ * call to call, so calls do no clearing of their own. Calls of that shape on
+ * it must be ordered (one stream, or synchronised): concurrent calls need
+ * separate workspaces. mg_scan_fwd/bwd refuse (MG_ERR_WORKSPACE) a workspace
+ * not initialised for their shape. Memory that is freed and reused must be
+ * initialised again; mg_scan_workspace_release forgets an address. */
+size_t mg_scan_workspace_bytes(int B, int T, int Di);
+int mg_scan_workspace_init(void* workspace, size_t workspace_bytes, int B, int T, int Di, void* stream);
+int mg_scan_workspace_release(void* workspace);
 
 int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,

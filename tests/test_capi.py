@@ -40,10 +40,11 @@ def test_every_declared_symbol_is_exported(L):
 
 def test_version_and_queries(L):
     assert L.mg_version() >= 100
-    # per-chain ticket counters (rounded to 256 B) + one 8-byte look-back word per
-    # (tile, channel), for the direction with the shorter tiles (64 steps)
-    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + 5 * 2 * 64 * 8
-    assert L.mg_scan_workspace_bytes(16, 8192, 2048) == 2048 + 128 * 16 * 2048 * 8
+    # ticket counters per chain and direction (rounded to 256 B) + one 8-byte
+    # look-back word per (tile, channel) for the forward (128-step tiles) and
+    # the backward (64-step tiles)
+    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + (3 + 5) * 2 * 64 * 8
+    assert L.mg_scan_workspace_bytes(16, 8192, 2048) == 4096 + (64 + 128) * 16 * 2048 * 8
 
 
 def _fwd(L, **kw):
@@ -64,6 +65,12 @@ def test_argument_errors(L):
     assert _fwd(L, in_ld=66) == 1
     assert _fwd(L, hidden=18) == 1  # misaligned
     assert _fwd(L, out_dtype=1, in_dtype=0) == 2  # f32 -> bf16 not offered
+    # every argument valid, but the workspace was never initialised
+    assert _fwd(L) == 3
+    assert "not initialised" in L.mg_last_error().decode()
+    assert L.mg_scan_workspace_init(None, 1 << 20, 2, 8, 64, None) == 3
+    assert L.mg_scan_workspace_init(16, 8, 2, 8, 64, None) == 3
+    assert L.mg_scan_workspace_init(16, 1 << 20, 2, 8, 62, None) == 1
 
 
 def test_product_refuses_cpu_tensors():

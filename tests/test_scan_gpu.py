@@ -182,3 +182,26 @@ def test_scan_cfg2_full_size_bf16():
     e_last = float(np.max(np.abs(last[..., sel].double().cpu().numpy() - ref[:, -1:]) / ref[:, -1:]))
     print(f"cfg2 sample: h {e_h:.2e} h_last {e_last:.2e} dhidden {e_dh:.2e} dgate {e_dg:.2e}", flush=True)
     assert e_h <= 2e-2 and e_dh <= 2e-2 and e_dg <= 2e-2 and e_last <= 1e-4
+
+
+def test_workspace_reuse_across_calls():
+    """The look-back workspace is cleared once and then reused call after
+    call (the kernels alternate a parity bit instead of clearing it): a run of
+    forward/backward calls on one cached workspace, with other shapes and
+    length-1 steps in between, gives bit for bit the results of calls on a
+    freshly initialised workspace, and stays within tolerance of fp64."""
+    from gruboros_amd import scan as S
+
+    S.release_workspaces()
+    cases = [(3, 700, 132, torch.bfloat16, True, s) for s in range(5)]
+    cases += [(2, 1, 64, torch.float32, True, 9), (3, 700, 132, torch.float32, False, 10), (1, 129, 8, torch.bfloat16,
+                                                                                               True, 11)]
+    cases += [(3, 700, 132, torch.bfloat16, False, s) for s in range(20, 23)]
+    reused = [_run(*_make(B, T, Di, dt, h0, seed=s), packed=False) for B, T, Di, dt, h0, s in cases]
+    for (B, T, Di, dt, h0, s), got in zip(cases, reused):
+        S.release_workspaces()
+        args = _make(B, T, Di, dt, h0, seed=s)
+        fresh = _run(*args, packed=False)
+        for x, y in zip(got, fresh):
+            assert (x is None and y is None) or torch.equal(x, y), (B, T, Di, dt, s)
+        _check(got, _oracle(*args), dt, f"reuse {B}x{T}x{Di} seed {s}")
