@@ -152,6 +152,60 @@ def _event_time(fn, reps):
     return e0.elapsed_time(e1) / reps  # ms
 
 
+def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64):
+    """Generation (reference generate.py:184-212) on the cfg3 model: tokens/s of
+    the per-token step, greedy sampling on the device, no host sync per token.
+    `model_call`: the drop-in model called once per token as generate.py does;
+    `decoder_graph`: gruboros_amd.decode.Decoder (decode kernels, one HIP graph
+    replay per token). `weight_GBs`: bf16 weight bytes read per step / step time."""
+    import torch
+
+    from gruboros_amd.decode import Decoder
+    from gruboros_amd.mingru.minLM import minLM
+
+    torch.manual_seed(0)
+    model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0,
+                  compute_dtype=torch.bfloat16).cuda().eval()
+    wbytes = 2 * sum(p.numel() for n, p in model.named_parameters() if p.dim() == 2 and "token_emb" not in n)
+    res = {"model": f"minLM d{dim} L{depth} bf16", "steps": steps, "weight_bytes_per_step": wbytes}
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for B in batches:
+        ids = torch.randint(0, 256, (B, prompt), device="cuda", generator=gen)
+        row = {}
+        with torch.no_grad():
+            # the model called once per token, as reference generate.py does
+            logits, hid = model(ids, return_prev_hiddens=True)
+            tok = logits[:, -1].argmax(-1)
+            for _ in range(5):
+                logits, hid = model(tok[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+                tok = logits[:, -1].argmax(-1)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                logits, hid = model(tok[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+                tok = logits[:, -1].argmax(-1)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            row["model_call"] = {"ms_per_token_step": ms, "tokens_per_s": B / (ms * 1e-3)}
+            dec = Decoder(model, B)
+            tok = dec.prefill(ids).argmax(-1)
+            for _ in range(5):
+                tok = dec.step(tok).argmax(-1)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(steps):
+                tok = dec.step(tok).argmax(-1)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            row["decoder_graph"] = {"ms_per_token_step": ms, "tokens_per_s": B / (ms * 1e-3),
+                                    "weight_GBs": wbytes / (ms * 1e-3) / 1e9}
+        res[f"batch{B}"] = row
+    return res
+
+
 def bench_kernels(reps=20, N=8 * 2047, D=1024, F=4096, V=256):
     """Per-kernel figures at the cfg3 shapes (16,376 token rows): HBM GB/s of
     the fused norm (algorithmic bytes: fwd 12, bwd 16 per element) and the
@@ -267,7 +321,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["train", "scan", "kernels"], default=None)
+    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode"], default=None)
     ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
                     help="training workload for `value`: cfg3 (the BASELINE metric, default) or cfg5 "
                          "(~1B params: d2048 L24, batch 4 x seq 4096, gradient accumulation 4)")
@@ -298,13 +352,16 @@ def main():
         print("[bench] copy calibration: 3 x 1 GiB device copies (1073741824 B read + written each)",
               file=sys.stderr, flush=True)
 
-    train = scan = kern = None
+    train = scan = kern = dec = None
     if args.only in (None, "scan"):
         scan = bench_scan(args.scan_reps)
         print(f"[bench] scan {json.dumps(scan)}", file=sys.stderr, flush=True)
     if args.only in (None, "kernels"):
         kern = bench_kernels()
         print(f"[bench] kernels {json.dumps(kern)}", file=sys.stderr, flush=True)
+    if args.only in (None, "decode"):
+        dec = bench_decode()
+        print(f"[bench] decode {json.dumps(dec)}", file=sys.stderr, flush=True)
     if args.only in (None, "train"):
         if args.workload == "cfg5":
             train = bench_train(args.steps, args.warmup, B=4, S=4096, dim=2048, depth=24, accum=4)
@@ -355,6 +412,8 @@ def main():
             / (train["ms_per_step"] * 1e-3)
     if kern:
         out["kernels"] = kern
+    if dec:
+        out["decode"] = dec
     if cpu:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

@@ -24,6 +24,10 @@ SIGNATURES = {
     "mg_scan_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "mg_scan_workspace_init": (_c_int, [_vp, _c_size, _c_int, _c_int, _c_int, _vp]),
     "mg_scan_workspace_release": (_c_int, [_vp]),
+    "mg_decode_mingru": (_c_int, [_c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                  _vp]),
+    "mg_decode_ff": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
+    "mg_decode_head": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
     "mg_scan_ckpt_elems": (_c_size, [_c_int, _c_int, _c_int]),
     "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
                              _c_int, _c_int, _c_int, _vp, _c_size, _vp]),

@@ -1,0 +1,350 @@
+// One-token decode step of minLM for small batches (B <= 8), bf16 weights,
+// fp32 residual stream and scan state: the generation loop of reference
+// generate.py:199-212, which calls minLM.forward on one token with the
+// previous hiddens (reference mingru/minLM.py:97-138; minGRU's one-step
+// path mingru/minGRU.py:45-52).
+//
+// Per layer two launches, plus one for the head:
+//   mg_decode_mingru  x_in (+ pending) -> RMSNorm -> [hidden | gate] rows of
+//                     to_hidden_and_gate -> one recurrence step per channel
+//                     (state updated in place) -> x_out = x_in + pending + h
+//   mg_decode_ff      RMSNorm(x) -> Linear + GELU (-> act) ; act -> Linear
+//                     -> pending (the FeedForward branch, added by the next
+//                     layer's mg_decode_mingru or by the head)
+//   mg_decode_head    x + pending -> RMSNorm -> to_logits
+// Each workgroup recomputes the RMSNorm of the B input rows (a few KiB) into
+// LDS as the bf16 vector the projection reads, then each wave produces R
+// output rows for all B inputs: lanes stride the reduction dimension in
+// 16-byte weight vectors, so the weights are read once, coalesced, and every
+// weight element is used for all B rows. The step is weight-bandwidth bound
+// (about 2 bytes per parameter per token); the launches are what a HIP graph
+// captures.
+//
+// Rounding follows the bf16 training path: the norm output, the projection
+// outputs, the scan output, GELU's input and output and the FeedForward
+// output are bf16 values, the residual stream and the scan state fp32.
+
+#include <algorithm>
+
+#include "mg_common.h"
+
+namespace mg {
+namespace decode {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxB = 8;
+constexpr int kLdsBytes = 64 * 1024;
+
+enum Mode { MINGRU = 0, FF1 = 1, FF2 = 2, HEAD = 3 };
+
+struct Args {
+  int B, D, K, rows;             // batch, model dim, reduction length, output rows
+  int V;                         // embedding rows (tokens are clamped into [0, V))
+  const int64_t* tokens;         // MINGRU of layer 0: x_in rows are emb[tokens[b]]
+  const float* emb;              // [V, D]
+  const float* x_in;             // [B, D] fp32 residual stream
+  const bf16_t* pending;         // [B, D] bf16 branch output to add first (nullable)
+  float* x_out;                  // MINGRU: x_in + pending + h
+  const float* norm_w;           // [D]
+  const bf16_t* W;               // [rows, K] bf16
+  const bf16_t* bias;            // [rows] bf16 (nullable)
+  float* state;                  // MINGRU: [B, D] fp32 recurrence state, in place
+  const bf16_t* act;             // FF2: [B, K] bf16 input
+  bf16_t* out;                   // FF1: act [B, F]; FF2: pending [B, D]; HEAD: logits [B, V]
+  float eps;
+};
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Sum each of a lane's N values over the wave (N a power of two <= 64) with
+// log2(N) halving exchanges plus a butterfly: at the exchange with lane ^ o
+// a lane keeps the upper half of its n live values if its bit o is set, the
+// lower half otherwise, and adds its partner's copy of that half. Lane l ends
+// with the total of value (l >> (6 - log2 N)); 64 / N lanes hold each total.
+// (Stages are template-unrolled so every array index is a constant: a
+// runtime index would turn into compare/select chains over the registers.)
+template <int n, int o, int N>
+__device__ __forceinline__ void wave_sum_stage(float (&v)[N], int lane) {
+  if constexpr (o >= 1) {
+    if constexpr (n > 1) {
+      const bool up = lane & o;
+#pragma unroll
+      for (int i = 0; i < n / 2; ++i) {
+        const float lo = v[i], hi = v[i + n / 2];
+        v[i] = (up ? hi : lo) + __shfl_xor(up ? lo : hi, o, 64);
+      }
+      wave_sum_stage<n / 2, o / 2, N>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], o, 64);
+      wave_sum_stage<1, o / 2, N>(v, lane);
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ float wave_sum_n(float (&v)[N]) {
+  wave_sum_stage<N, 32, N>(v, threadIdx.x & 63);
+  return v[0];
+}
+
+// Where the residual-stream rows come from (a template parameter, so the
+// loads carry no branches and can all be in flight together).
+enum Src { SRC_X = 0, SRC_X_PENDING = 1, SRC_TOKENS = 2 };
+
+// Residual-stream value (b, c) before the norm: x_in (or the embedding row)
+// plus the pending branch output.
+template <int SRC>
+__device__ __forceinline__ float stream_at(const Args& a, int b, int c) {
+  float x;
+  if constexpr (SRC == SRC_TOKENS) {
+    const int64_t t = min(max(a.tokens[b], int64_t(0)), static_cast<int64_t>(a.V - 1));
+    x = a.emb[t * a.D + c];
+  } else {
+    x = a.x_in[static_cast<int64_t>(b) * a.D + c];
+  }
+  if constexpr (SRC == SRC_X_PENDING) x += bf16_to_f32(a.pending[static_cast<int64_t>(b) * a.D + c]);
+  return x;
+}
+
+// MODE: which step; BP: batch rows (padded); R: output rows per wave;
+// NC: 512-element chunks of the reduction a lane covers (K <= 512 NC); CPT:
+// columns per thread in the norm prologue (D <= 256 CPT).
+template <int MODE, int SRC, int BP, int R, int NC, int CPT>
+__global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
+  extern __shared__ uint4 lds[];
+  bf16_t* s_in = reinterpret_cast<bf16_t*>(lds);  // [BP][K]
+  __shared__ float s_part[kWaves][BP];
+  __shared__ float s_rstd[BP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = a.K;
+
+  // 0. this wave's weight rows (MINGRU: rows d and D+d, hidden and gate of
+  // channel d), requested before anything else so that their latency
+  // overlaps the norm prologue
+  const int g = blockIdx.x * kWaves + wave;  // row group
+  int rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = MODE == MINGRU ? g + r * a.D : g * R + r;
+  const bool active = rows[0] < (MODE == MINGRU ? a.D : a.rows);
+  uint4 wv[NC][R];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      // clamped, unconditional loads (nothing branches between them); rows
+      // past the end are never used, chunks past K are skipped below
+      const int k0 = min(c * 512 + lane * 8, K - 8);
+      const int row = active ? rows[r] : 0;
+      wv[c][r] = *reinterpret_cast<const uint4*>(a.W + static_cast<int64_t>(row) * K + k0);
+    }
+
+  // 1. the B input rows, as bf16, into LDS (rows B..BP-1 zero)
+  if constexpr (MODE == FF2) {
+    for (int i = tid; i < BP * (K / 8); i += kThreads) {
+      const int b = i / (K / 8), c8 = i % (K / 8);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (b < a.B) v = *reinterpret_cast<const uint4*>(a.act + static_cast<int64_t>(b) * K + c8 * 8);
+      reinterpret_cast<uint4*>(s_in)[i] = v;
+    }
+  } else {
+    // RMSNorm over D = K: the rows are read once into registers (column
+    // tid + 256 i), the sum of squares reduced over the workgroup, then
+    // y = x r w goes to LDS
+    float xr[BP][CPT];
+    float ss[BP];
+#pragma unroll
+    for (int b = 0; b < BP; ++b) {
+      ss[b] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * kThreads;
+        const float x = stream_at<SRC>(a, min(b, a.B - 1), min(c, K - 1));  // unconditional load
+        xr[b][i] = (b < a.B && c < K) ? x : 0.0f;
+        ss[b] += xr[b][i] * xr[b][i];
+      }
+    }
+    {
+      // lane l ends with the wave's total of row l / (64 / BP)
+      const float s = wave_sum_n<BP>(ss);
+      if (lane % (64 / BP) == 0) s_part[wave][lane / (64 / BP)] = s;
+    }
+    __syncthreads();
+    if (tid < BP) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) s += s_part[w][tid];
+      s_rstd[tid] = __builtin_amdgcn_rsqf(s / static_cast<float>(K) + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < K) {
+        const float w = a.norm_w[c];
+#pragma unroll
+        for (int b = 0; b < BP; ++b) s_in[b * K + c] = f32_to_bf16(xr[b][i] * s_rstd[b] * w);
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+
+  // 2. the dot products, weights from registers, inputs from LDS
+  float acc[R][BP];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < BP; ++b) acc[r][b] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k0 = c * 512 + lane * 8;
+    if (k0 >= K) break;
+#pragma unroll
+    for (int b = 0; b < BP; ++b) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(s_in + b * K + k0);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t ww[4] = {wv[c][r].x, wv[c][r].y, wv[c][r].z, wv[c][r].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)  // two bf16 products per instruction, fp32 accumulation
+          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, ww[q]),
+                                                      __builtin_bit_cast(bf16x2, xw[q]), acc[r][b], false);
+      }
+    }
+  }
+  constexpr int N = R * BP;
+  float flat[N];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < BP; ++b) flat[r * BP + b] = acc[r][b];
+  const float sum = wave_sum_n<N>(flat);
+
+  // 3. epilogue: the first lane holding value (r, b) = (idx / BP, idx % BP)
+  constexpr int kCopies = 64 / N;
+  const int idx = lane / kCopies, r = idx / BP, b = idx % BP;
+  if (MODE == MINGRU) {
+    // hidden (r = 0) and gate (r = 1) of one batch row are 32 lanes apart
+    const float other = __shfl_xor(sum, 32, 64);
+    if (lane % kCopies || r != 0 || b >= a.B) return;
+    const int d = g;
+    const float hid = round_bf16(sum), gate = round_bf16(other);
+    float coef, v;
+    fwd_coeffs(gate, hid, coef, v);
+    float* st = a.state + static_cast<int64_t>(b) * a.D + d;
+    const float h = coef * *st + v;
+    *st = h;
+    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + round_bf16(h);
+    return;
+  }
+  if (lane % kCopies || b >= a.B) return;
+  bf16_t* o = a.out + static_cast<int64_t>(b) * a.rows + rows[0] + r;
+  if constexpr (MODE == FF1) {
+    *o = f32_to_bf16(gelu(round_bf16(sum + bf16_to_f32(a.bias[rows[0] + r]))));
+  } else if constexpr (MODE == FF2) {
+    *o = f32_to_bf16(sum + bf16_to_f32(a.bias[rows[0] + r]));
+  } else {
+    *o = f32_to_bf16(sum);
+  }
+}
+
+template <int MODE, int SRC, int BP, int R>
+int launch_bp(const Args& a, dim3 grid, size_t lds, hipStream_t st) {
+  if constexpr (MODE == FF2) {
+    if (a.K <= 4096) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 8, 1>), grid, dim3(kThreads), lds, st, a);
+    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 16, 1>), grid, dim3(kThreads), lds, st, a);
+  } else {
+    if (a.K <= 1024) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 2, 4>), grid, dim3(kThreads), lds, st, a);
+    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 4, 8>), grid, dim3(kThreads), lds, st, a);
+  }
+  return check_launch("mg_decode");
+}
+
+template <int MODE, int SRC, int R>
+int launch(const Args& a, hipStream_t st) {
+  const int groups = MODE == MINGRU ? a.D : a.rows / R;
+  const dim3 grid((groups + kWaves - 1) / kWaves);
+  const int BP = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
+  const size_t lds = static_cast<size_t>(BP) * a.K * sizeof(bf16_t);
+  switch (BP) {
+    case 1: return launch_bp<MODE, SRC, 1, R>(a, grid, lds, st);
+    case 2: return launch_bp<MODE, SRC, 2, R>(a, grid, lds, st);
+    case 4: return launch_bp<MODE, SRC, 4, R>(a, grid, lds, st);
+    default: return launch_bp<MODE, SRC, 8, R>(a, grid, lds, st);
+  }
+}
+
+// kmax: 2048 for the model dimension (norm prologue), 8192 for the FeedForward width
+inline int check_shape(const char* fn, int B, int K, int kmax) {
+  if (B < 1 || B > kMaxB) return fail(MG_ERR_ARG, "%s: batch %d outside [1, %d]", fn, B, kMaxB);
+  if (K < 8 || K % 8 || K > kmax)
+    return fail(MG_ERR_ARG, "%s: length %d must be a positive multiple of 8, at most %d", fn, K, kmax);
+  const int BP = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+  if (static_cast<size_t>(BP) * K * 2 > static_cast<size_t>(kLdsBytes))
+    return fail(MG_ERR_ARG, "%s: batch %d x length %d exceeds the 64 KiB input staging", fn, B, K);
+  return MG_OK;
+}
+
+}  // namespace decode
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" int mg_decode_mingru(int B, int D, const int64_t* tokens, const float* emb, int V, const float* x_in,
+                                const void* pending, float* x_out, const float* norm_w, const void* w_hg,
+                                float* state, float eps, void* stream) {
+  const char* fn = "mg_decode_mingru";
+  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
+  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !x_out || !norm_w || !w_hg || !state)
+    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
+  if (!aligned(w_hg, 16)) return fail(MG_ERR_ARG, "%s: weight not 16-byte aligned", fn);
+  decode::Args a{};
+  a.B = B; a.D = D; a.K = D; a.rows = 2 * D; a.V = V;
+  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
+  a.x_out = x_out; a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w_hg); a.state = state; a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tokens) return decode::launch<decode::MINGRU, decode::SRC_TOKENS, 2>(a, st);
+  if (pending) return decode::launch<decode::MINGRU, decode::SRC_X_PENDING, 2>(a, st);
+  return decode::launch<decode::MINGRU, decode::SRC_X, 2>(a, st);
+}
+
+extern "C" int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
+                            const void* b1, void* act, const void* w2, const void* b2, void* pending_out, float eps,
+                            void* stream) {
+  const char* fn = "mg_decode_ff";
+  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
+  if (int rc = decode::check_shape(fn, B, F, 8192)) return rc;
+  if (!x || !norm_w || !w1 || !b1 || !act || !w2 || !b2 || !pending_out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (F % 4 || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(act, 16))
+    return fail(MG_ERR_ARG, "%s: F %% 4, 16-byte weights and act required", fn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  decode::Args a{};
+  a.B = B; a.D = D; a.K = D; a.rows = F;
+  a.x_in = x; a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w1); a.bias = static_cast<const bf16_t*>(b1);
+  a.out = static_cast<bf16_t*>(act); a.eps = eps;
+  if (int rc = decode::launch<decode::FF1, decode::SRC_X, 4>(a, st)) return rc;
+  decode::Args c{};
+  c.B = B; c.D = D; c.K = F; c.rows = D;
+  c.act = static_cast<const bf16_t*>(act); c.W = static_cast<const bf16_t*>(w2); c.bias = static_cast<const bf16_t*>(b2);
+  c.out = static_cast<bf16_t*>(pending_out);
+  return decode::launch<decode::FF2, decode::SRC_X, 1>(c, st);
+}
+
+extern "C" int mg_decode_head(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
+                              const void* w_out, void* logits, float eps, void* stream) {
+  const char* fn = "mg_decode_head";
+  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
+  if (V < 1 || !x_in || !norm_w || !w_out || !logits) return fail(MG_ERR_ARG, "%s: bad argument", fn);
+  if (!aligned(w_out, 16)) return fail(MG_ERR_ARG, "%s: weight not 16-byte aligned", fn);
+  decode::Args a{};
+  a.B = B; a.D = D; a.K = D; a.rows = V;
+  a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending); a.norm_w = norm_w;
+  a.W = static_cast<const bf16_t*>(w_out); a.out = static_cast<bf16_t*>(logits); a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (pending) return decode::launch<decode::HEAD, decode::SRC_X_PENDING, 1>(a, st);
+  return decode::launch<decode::HEAD, decode::SRC_X, 1>(a, st);
+}

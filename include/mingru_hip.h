@@ -289,6 +289,34 @@ int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
                 void* dpre, int64_t ld_out, float* dbias, int64_t N, int C,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * One-token decode step (generation), batch 1..8, bf16 weights, fp32
+ * residual stream and recurrence state; replaces the per-token call of
+ * minLM.forward in reference generate.py:199-212 (mingru/minLM.py:97-138 on
+ * one position, minGRU's one-step path mingru/minGRU.py:45-52). Expansion
+ * 1.0 (Di = D), no conv, no dropout. Per layer:
+ *   mg_decode_mingru: x = (tokens ? emb[tokens] : x_in) + pending (bf16,
+ *     nullable); n = bf16(RMSNorm(x) * norm_w); [hidden | gate] = bf16(n W_hg^T)
+ *     (W_hg bf16 [2D, D]); state = a state + z g(hidden) (fp32 [B, D], in
+ *     place); x_out = x + bf16(state). Tokens are clamped into [0, V).
+ *   mg_decode_ff: n = bf16(RMSNorm(x) * norm_w); act = bf16(gelu(bf16(n W1^T
+ *     + b1))) (W1 bf16 [F, D], b1 bf16 [F], act bf16 [B, F] scratch);
+ *     pending_out = bf16(act W2^T + b2) (W2 bf16 [D, F], b2 bf16 [D]).
+ *   mg_decode_head: logits = bf16(bf16(RMSNorm(x_in + pending) * norm_w)
+ *     W_out^T) (W_out bf16 [V, D], logits bf16 [B, V]).
+ * RMSNorm: x / sqrt(mean(x^2) + eps). D <= 2048, F <= 8192, both multiples
+ * of 8, with the batch (rounded up to 1, 2, 4 or 8) times max(D, F) bf16
+ * values within 64 KiB; weights 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int mg_decode_mingru(int B, int D, const int64_t* tokens, const float* emb, int V, const float* x_in,
+                     const void* pending, float* x_out, const float* norm_w, const void* w_hg,
+                     float* state, float eps, void* stream);
+int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
+                 const void* b1, void* act, const void* w2, const void* b2, void* pending_out,
+                 float eps, void* stream);
+int mg_decode_head(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
+                   const void* w_out, void* logits, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,18 @@ def test_argument_errors(L):
     assert L.mg_scan_workspace_init(16, 1 << 20, 2, 8, 62, None) == 1
 
 
+def test_decode_argument_errors(L):
+    import ctypes
+
+    eps = ctypes.c_float(1e-7)
+    # batch above 8, a dimension that is not a multiple of 8, a width over the LDS staging
+    assert L.mg_decode_mingru(9, 64, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru(1, 60, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_ff(8, 64, 8192, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru(1, 64, 16, None, 256, None, None, 16, 16, 16, 16, eps, None) == 1  # no embedding
+    assert L.mg_decode_head(1, 64, 0, 16, None, 16, 16, 16, eps, None) == 1
+
+
 def test_product_refuses_cpu_tensors():
     import torch
     from gruboros_amd.scan import gate_scan

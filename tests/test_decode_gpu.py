@@ -1,0 +1,100 @@
+"""GPU parity of the one-token decode path (gruboros_amd.decode.Decoder on
+mg_decode_mingru / mg_decode_ff / mg_decode_head) for the generation loop of
+reference generate.py:184-212.
+
+Checks:
+  * against the drop-in model's own one-token call (model(token,
+    prev_hiddens=...), reference mingru/minLM.py:101-102 with minGRU's
+    one-step path mingru/minGRU.py:47-52) step by step: logits and states;
+  * against one parallel forward over prompt + generated tokens (T single
+    steps equal one T-long scan);
+  * the captured HIP graph replays exactly what the launches compute, also
+    after the weights change.
+Tolerances: bf16 activations, so relative (Frobenius) 1e-2 on logits and
+states: the two paths sum the projections in different orders, and a bf16
+rounding of a projection output can land on the other side.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+def _model(dim=256, depth=2, seed=0):
+    from gruboros_amd.mingru.minLM import minLM
+
+    torch.manual_seed(seed)
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0, compute_dtype=torch.bfloat16)
+    with torch.no_grad():
+        for layer in m.layers:  # non-zero second FF weights so every block contributes
+            layer[4][2].weight.normal_(0, 0.02)
+    return m.to(DEV).eval()
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_decoder_matches_one_token_model_calls(B):
+    from gruboros_amd.decode import Decoder
+
+    m = _model()
+    gen = torch.Generator(device=DEV).manual_seed(B)
+    prompt = torch.randint(0, 256, (B, 17), device=DEV, generator=gen)
+    dec = Decoder(m, B)
+    with torch.no_grad():
+        logits, hid = m(prompt, return_prev_hiddens=True)
+        last = dec.prefill(prompt)
+        assert torch.equal(last, logits[:, -1])
+        for step in range(6):
+            tok = torch.randint(0, 256, (B,), device=DEV, generator=gen)
+            logits, hid = m(tok[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+            got = dec.step(tok)
+            e_l = _rel(got, logits[:, -1])
+            e_h = max(_rel(a, b) for a, b in zip(dec.hiddens(), hid))
+            print(f"B={B} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
+            assert e_l < 1e-2 and e_h < 1e-2
+
+
+def test_decoder_equals_parallel_forward():
+    from gruboros_amd.decode import Decoder
+
+    B, P, N = 2, 9, 12
+    m = _model(dim=512, depth=3, seed=1)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    seq = torch.randint(0, 256, (B, P + N), device=DEV, generator=gen)
+    dec = Decoder(m, B)
+    with torch.no_grad():
+        full, hid = m(seq, return_prev_hiddens=True)
+        dec.prefill(seq[:, :P])
+        for t in range(P, P + N):
+            got = dec.step(seq[:, t])
+            assert _rel(got, full[:, t]) < 1e-2, t
+        for a, b in zip(dec.hiddens(), hid):
+            assert _rel(a, b) < 1e-2
+
+
+def test_decoder_graph_replays_the_launches():
+    from gruboros_amd.decode import Decoder
+
+    B = 4
+    m = _model(seed=2)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    prompt = torch.randint(0, 256, (B, 5), device=DEV, generator=gen)
+    toks = [torch.randint(0, 256, (B,), device=DEV, generator=gen) for _ in range(5)]
+    eager, graph = Decoder(m, B, graph=False), Decoder(m, B, graph=True)
+    for d in (eager, graph):
+        d.prefill(prompt)
+    for i, t in enumerate(toks):
+        if i == 3:  # weights changed in place (as a gossip merge or a checkpoint load does)
+            with torch.no_grad():
+                m.layers[0][2].to_hidden_and_gate.weight.mul_(0.5)
+                m.to_logits.weight.add_(0.01)
+        a = eager.step(t).clone()
+        b = graph.step(t).clone()
+        assert torch.equal(a, b), i
+        for x, y in zip(eager.hiddens(), graph.hiddens()):
+            assert torch.equal(x, y), i
