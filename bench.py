@@ -400,9 +400,10 @@ def main():
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bwd_gbs / HBM_PEAK_GBS,
                            "traffic": measured_traffic("scan_bwd_kernel"),
                            "algorithmic_bytes": 12 * scan["elements"],
-                           "note": "achieved = 12 B/element x 2^28 / mean launch time (HIP events on the launch "
-                                   "stream, incl. the ~6 us look-back workspace clear); traffic = calibrated "
-                                   "FETCH_SIZE+WRITE_SIZE bytes per launch (profiles/scan_cfg2_traffic.md)"}
+                           "note": "achieved = 12 B/element x 2^28 / mean launch time of the timed launches "
+                                   "(HIP events on the launch stream, after ~30 ms of warm-up); traffic = "
+                                   "calibrated FETCH_SIZE+WRITE_SIZE bytes per launch "
+                                   "(profiles/scan_cfg2_traffic.md)"}
         out["scan"] = scan
     if train:
         out["step_roofline"] = {"bound": "mfma", "achieved": train["tflops"], "peak": BF16_PEAK_TFLOPS,
