@@ -36,11 +36,15 @@
 //   BIAS_GELU  aux = bf16(acc + bias[n]);  C = gelu(aux)      (FeedForward up)
 //   GELU_GRAD  C = acc * gelu'(aux[m][n])                     (its backward)
 // with gelu(x) = x/2 (1 + erf(x / sqrt 2)), the exact form of nn.GELU().
-// fp32 outputs may be split along K over several workgroups that add into C
-// with fp32 atomics (summation order then varies run to run, ~1 ulp).
+// fp32 outputs may be split along K over several workgroups: each writes its
+// partial tile to a workspace, and the last of a tile's workgroups to finish
+// (a per-tile counter) adds the partials in split order into C, so the
+// result does not depend on scheduling.
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "mg_common.h"
 
@@ -62,6 +66,9 @@ struct Params {
   int M, N, K;
   int tiles_m, tiles_n;
   int kt_per_split;  // k-tiles per split (gridDim.y splits)
+  float* part;       // split partials: gridDim.y dense [M, N] fp32 slices
+  uint32_t* tile_cnt;  // per-tile arrival counters (zero between calls)
+  int accumulate;    // C += (fp32 outputs)
   uint32_t a_span, b_span;  // bytes from A / B to one past their last element
   uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
 };
@@ -428,7 +435,33 @@ __device__ __forceinline__ void mainloop_pp(const Params& p, uint4* smem, int m0
 }
 
 // Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
-template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
+// Split partials cross workgroups on other XCDs, whose L2s are not coherent
+// with each other for plain accesses: they are written and read with
+// device-scope atomic stores and loads (the coherent, L2-bypassing forms),
+// 8 bytes at a time, so no L2 writeback or invalidation is needed.
+__device__ __forceinline__ void store_coherent(float* p, const f4& x) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(p);
+  __hip_atomic_store(q, (static_cast<uint64_t>(__float_as_uint(x.v[1])) << 32) | __float_as_uint(x.v[0]),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, (static_cast<uint64_t>(__float_as_uint(x.v[3])) << 32) | __float_as_uint(x.v[2]),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f4 load_coherent(const float* p) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  f4 x;
+  x.v[0] = __uint_as_float(static_cast<uint32_t>(a)); x.v[1] = __uint_as_float(static_cast<uint32_t>(a >> 32));
+  x.v[2] = __uint_as_float(static_cast<uint32_t>(b)); x.v[3] = __uint_as_float(static_cast<uint32_t>(b >> 32));
+  return x;
+}
+
+// How a workgroup's tile reaches C: written (C_STORE), added to C by its one
+// writer (C_ADD), or written as a split-K partial and summed into C by the
+// tile's last workgroup (C_SPLIT).
+enum CMode { C_STORE = 0, C_ADD = 1, C_SPLIT = 2 };
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
@@ -514,17 +547,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     if constexpr (EPI == EPI_GELU_GRAD) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (i + 1 < MB) fetch_pre(i + 1);
-    if (ATOMIC) {
-      // one float per lane, 64 consecutive columns of a row per instruction
-#pragma unroll 1
-      for (int t = 0; t < 32 * NW / 64; ++t) {
-        const int r = t / (NW / 64), c = (t % (NW / 64)) * 64 + lane;
-        const int m = row0 + i * 32 + r, n = col0 + c;
-        const int q = c / 4;
-        const float v = *reinterpret_cast<const float*>(stage + r * RB + ((q ^ (r % CQ)) * 16) + (c % 4) * 4);
-        if (m < p.M && n < p.N) unsafeAtomicAdd(static_cast<float*>(p.C) + static_cast<int64_t>(m) * p.ldc + n, v);
-      }
-    } else {
+    {
       // The GELU epilogues stay runtime loops (unrolled they are more code
       // than the instruction cache holds); the others are unrolled.
       constexpr int kStoreUnroll = (EPI == EPI_BIAS_GELU || EPI == EPI_GELU_GRAD) ? 2 : 32;
@@ -534,7 +557,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
         const int m = row0 + i * 32 + r, n = ncol;
         const uint4 raw = *reinterpret_cast<const uint4*>(stage + r * RB + ((qc ^ (r % CQ)) * 16));
         if (m >= p.M || n >= p.N) continue;
-        TC* cp = static_cast<TC*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
+        TC* cp = CMODE == C_SPLIT
+                     ? reinterpret_cast<TC*>(p.part + (static_cast<int64_t>(blockIdx.y) * p.M + m) * p.N + n)
+                     : static_cast<TC*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
         if constexpr (sizeof(S) == 4) {
           f4 x;
           x.v[0] = __uint_as_float(raw.x); x.v[1] = __uint_as_float(raw.y);
@@ -555,13 +580,55 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
             x.v[2] *= gelu_grad(__uint_as_float(w.y << 16));
             x.v[3] *= gelu_grad(__uint_as_float(w.y & 0xffff0000u));
           }
-          io4<TC>::store(cp, x);
+          if constexpr (CMODE == C_ADD) {
+            const f4 old = io4<float>::load(reinterpret_cast<const float*>(cp));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x.v[e] = old.v[e] + x.v[e];
+          }
+          if constexpr (CMODE == C_SPLIT) {
+            store_coherent(reinterpret_cast<float*>(cp), x);
+          } else {
+            io4<TC>::store(cp, x);
+          }
         } else {
           *reinterpret_cast<uint4*>(cp) = raw;
         }
       }
     }
     __syncthreads();
+  }
+  if constexpr (CMODE == C_SPLIT) {
+    // Count arrivals once the partial has been written (device-coherent
+    // stores, completed); the last workgroup of the tile sums the gridDim.y
+    // partials in split order (plus C when accumulating) and resets the
+    // counter for the next call.
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(p.tile_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      s_last = old + 1 == gridDim.y;
+      if (s_last) __hip_atomic_store(p.tile_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    constexpr int kChunks = BM * BN / 4;  // 4-float chunks of the tile
+    const int64_t slice = static_cast<int64_t>(p.M) * p.N;
+#pragma unroll 2
+    for (int q = threadIdx.x; q < kChunks; q += 64 * WM * WN) {
+      const int m = m0 + q / (BN / 4), n = n0 + (q % (BN / 4)) * 4;
+      if (m >= p.M || n >= p.N) continue;
+      float* cp = static_cast<float*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
+      f4 sum = p.accumulate ? io4<float>::load(cp) : io4<float>::fill(0.0f);
+      const float* pp = p.part + static_cast<int64_t>(m) * p.N + n;
+      for (int sp = 0; sp < static_cast<int>(gridDim.y); ++sp) {
+        const f4 v = load_coherent(pp + sp * slice);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
+      }
+      io4<float>::store(cp, sum);
+    }
   }
 }
 
@@ -663,55 +730,92 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   if (threadIdx.x == 0) loss_part[blockIdx.x] = s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3];
 }
 
-__global__ void zero_f32_kernel(float* __restrict__ p, int64_t rows, int cols, int64_t ld) {
-  const int64_t n = rows * cols;
-  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x); i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t r = i / cols, c = i - r * cols;
-    p[r * ld + c] = 0.0f;
-  }
+__global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {  // workspace initialisation
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
 }
 
 constexpr int kCUs = 256;
 
-template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, bool ATOMIC>
-int launch(const Params& p0, int splits, hipStream_t stream) {
+// Tile size and K split of a product (measured on MI355X): weight gradients
+// (both operands MN-contiguous, long K) run 128 x 128 tiles split along K
+// into about two workgroups per CU; the other layouts run 256 x 256 when
+// that still gives every CU a workgroup, else 128 x 128 (fp32 outputs then
+// split K). `ysplits` is the split count the launch uses (gridDim.y).
+struct Plan {
+  bool big;
+  int tiles, kt_per_split, ysplits;
+};
+
+inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogue, bool deterministic) {
+  Plan pl;
+  const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
+  const bool wgrad = !ak && !bk;
+  pl.big = !wgrad && t256 >= kCUs;
+  const int64_t tiles = pl.big ? t256 : t128;
+  pl.tiles = static_cast<int>(tiles);
+  const int nkt = (K + BK - 1) / BK;
+  const int64_t want_wgs = wgrad ? 2 * kCUs : kCUs;
+  int splits = 1;
+  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
+    splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
+  pl.kt_per_split = std::max((nkt + splits - 1) / splits, 1);
+  pl.ysplits = std::max((nkt + pl.kt_per_split - 1) / pl.kt_per_split, 1);
+  return pl;
+}
+
+// Workspace of a split plan: tile counters, then the partials. Only plans
+// with fewer tiles than 2 x kCUs split, so the counter area has one fixed
+// size (a workspace can then serve products of different shapes).
+constexpr size_t kCounterBytes = 2 * kCUs * 4;
+inline size_t ws_bytes(const Plan& pl, int M, int N) {
+  if (pl.ysplits <= 1) return 0;
+  return kCounterBytes + static_cast<size_t>(pl.ysplits) * M * N * sizeof(float);
+}
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
+int launch(const Params& p0, const Plan& pl, hipStream_t stream) {
   Params p = p0;
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  const int nkt = (p.K + BK - 1) / BK;
-  p.kt_per_split = std::max((nkt + splits - 1) / splits, 1);
-  const int ysplits = std::max((nkt + p.kt_per_split - 1) / p.kt_per_split, 1);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, ATOMIC>), dim3(p.tiles_m * p.tiles_n, ysplits),
+  p.kt_per_split = pl.kt_per_split;
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, CMODE>), dim3(p.tiles_m * p.tiles_n, pl.ysplits),
                      dim3(64 * WM * WN), 0, stream, p);
   return check_launch("mg_gemm");
 }
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
-int dispatch_epi(const Params& p, int epi, int c_dtype, bool atomic, int splits, hipStream_t s) {
+int dispatch_epi(const Params& p, const Plan& pl, int epi, int c_dtype, hipStream_t s) {
   if (c_dtype == MG_F32) {
-    if (atomic) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, true>(p, splits, s);
-    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, false>(p, 1, s);
-    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, float, false>(p, 1, s);
+    if (pl.ysplits > 1) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_SPLIT>(p, pl, s);
+    if (p.accumulate) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_ADD>(p, pl, s);
+    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_STORE>(p, pl, s);
+    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, float, C_STORE>(p, pl, s);
   } else {
-    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, bf16_t, false>(p, 1, s);
-    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, false>(p, 1, s);
-    if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, false>(p, 1, s);
-    if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, false>(p, 1, s);
+    if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, bf16_t, C_STORE>(p, pl, s);
+    if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, C_STORE>(p, pl, s);
+    if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, C_STORE>(p, pl, s);
+    if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, C_STORE>(p, pl, s);
   }
   return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
 }
 
 // 256 x 256 tiles run 8 waves (two per SIMD), 128 x 128 tiles 4.
 template <int BM, int BN>
-int dispatch_layout(const Params& p, bool ak, bool bk, int epi, int c_dtype, bool atomic, int splits,
-                    hipStream_t s) {
+int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, int c_dtype, hipStream_t s) {
   constexpr int WN = BM * BN >= 256 * 256 ? 4 : 2;
-  if (ak && bk) return dispatch_epi<BM, BN, 2, WN, true, true>(p, epi, c_dtype, atomic, splits, s);
-  if (ak && !bk) return dispatch_epi<BM, BN, 2, WN, true, false>(p, epi, c_dtype, atomic, splits, s);
-  if (!ak && !bk) return dispatch_epi<BM, BN, 2, WN, false, false>(p, epi, c_dtype, atomic, splits, s);
-  return dispatch_epi<BM, BN, 2, WN, false, true>(p, epi, c_dtype, atomic, splits, s);
+  if (ak && bk) return dispatch_epi<BM, BN, 2, WN, true, true>(p, pl, epi, c_dtype, s);
+  if (ak && !bk) return dispatch_epi<BM, BN, 2, WN, true, false>(p, pl, epi, c_dtype, s);
+  if (!ak && !bk) return dispatch_epi<BM, BN, 2, WN, false, false>(p, pl, epi, c_dtype, s);
+  return dispatch_epi<BM, BN, 2, WN, false, true>(p, pl, epi, c_dtype, s);
 }
+
+// Host-side record of initialised workspaces (address -> size), so that a
+// split product never runs on counters that were not zeroed.
+std::mutex g_ws_mu;
+std::unordered_map<uintptr_t, size_t> g_ws;
 
 }  // namespace gemm
 }  // namespace mg
@@ -720,7 +824,7 @@ using namespace mg;
 
 extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, const void* B, int64_t ldb, int M,
                        int N, int K, int epilogue, const float* bias, void* aux, int64_t ldaux, int c_dtype, void* C,
-                       int64_t ldc, int flags, void* stream) {
+                       int64_t ldc, int flags, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "mg_gemm";
   if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC)) return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
   const bool accumulate = flags & MG_GEMM_ACCUMULATE;
@@ -772,28 +876,55 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     p.aux_span = static_cast<uint32_t>(aux_span);
   }
 
-  // Tile choice (measured on MI355X): weight gradients (both operands
-  // MN-contiguous, long K) run 128 x 128 tiles split along K into about
-  // two workgroups per CU; the other layouts run 256 x 256 when that still
-  // gives every CU a workgroup, else 128 x 128 (fp32 outputs then split K).
-  const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  const bool wgrad = !ak && !bk;
-  const bool big = !wgrad && t256 >= gemm::kCUs;
-  const int64_t tiles = big ? t256 : t128;
-  const int nkt = (K + gemm::BK - 1) / gemm::BK;
-  const int64_t want_wgs = wgrad ? 2 * gemm::kCUs : gemm::kCUs;
-  int splits = 1;
-  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
-    splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
   if (K == 0 && accumulate) return MG_OK;
-  const bool atomic = accumulate || splits > 1;
-  if (atomic && !accumulate) {
-    hipLaunchKernelGGL(gemm::zero_f32_kernel, dim3(1024), dim3(256), 0, s, static_cast<float*>(C), int64_t(M), N, ldc);
-    if (int rc = check_launch(fn)) return rc;
+  // Without a workspace the product runs unsplit; with one, the split plan
+  // needs it initialised and large enough.
+  gemm::Plan pl = gemm::plan(M, N, K, ak, bk, c_dtype, epilogue, deterministic || !workspace);
+  if (pl.ysplits > 1) {
+    const size_t need = gemm::ws_bytes(pl, M, N);
+    if (workspace_bytes < need)
+      return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu (mg_gemm_workspace_bytes)", fn,
+                  workspace_bytes, need);
+    if (!aligned(workspace, 256)) return fail(MG_ERR_ARG, "%s: workspace not 256-byte aligned", fn);
+    {
+      std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
+      const auto it = gemm::g_ws.find(reinterpret_cast<uintptr_t>(workspace));
+      if (it == gemm::g_ws.end() || it->second < need)
+        return fail(MG_ERR_WORKSPACE, "%s: workspace not initialised (mg_gemm_workspace_init)", fn);
+    }
+    p.tile_cnt = static_cast<uint32_t*>(workspace);
+    p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + gemm::kCounterBytes);
   }
-  return big ? gemm::dispatch_layout<256, 256>(p, ak, bk, epilogue, c_dtype, atomic, splits, s)
-             : gemm::dispatch_layout<128, 128>(p, ak, bk, epilogue, c_dtype, atomic, splits, s);
+  p.accumulate = accumulate ? 1 : 0;
+  return pl.big ? gemm::dispatch_layout<256, 256>(p, pl, ak, bk, epilogue, c_dtype, s)
+                : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epilogue, c_dtype, s);
+}
+
+extern "C" size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
+                                          int c_dtype, int flags) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  const gemm::Plan pl = gemm::plan(M, N, K, a_layout == MG_KCONTIG, b_layout == MG_KCONTIG, c_dtype, epilogue,
+                                   flags & MG_GEMM_DETERMINISTIC);
+  return gemm::ws_bytes(pl, M, N);
+}
+
+extern "C" int mg_gemm_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "mg_gemm_workspace_init";
+  if (!workspace || workspace_bytes < 256 || !aligned(workspace, 256))
+    return fail(MG_ERR_ARG, "%s: need a 256-byte aligned workspace of at least 256 bytes", fn);
+  const int64_t n16 = static_cast<int64_t>(workspace_bytes / 16);
+  hipLaunchKernelGGL(gemm::zero_kernel, dim3(static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint4*>(workspace), n16);
+  if (int rc = check_launch(fn)) return rc;
+  std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
+  gemm::g_ws[reinterpret_cast<uintptr_t>(workspace)] = workspace_bytes;
+  return MG_OK;
+}
+
+extern "C" int mg_gemm_workspace_release(void* workspace) {
+  std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
+  gemm::g_ws.erase(reinterpret_cast<uintptr_t>(workspace));
+  return MG_OK;
 }
 
 extern "C" int mg_logits_cross_entropy_partials(int64_t N) {

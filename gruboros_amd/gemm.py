@@ -22,11 +22,30 @@ def _rows(t, name):
     return t.stride(0)
 
 
+# Split-K workspaces, one per (device, stream), grown on demand; each is
+# initialised (zeroed) once, after which the kernels keep its counters at zero.
+_WORKSPACES = {}
+
+
+def _workspace(device, nbytes):
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        L = _lib.lib()
+        if ws is not None:
+            L.mg_gemm_workspace_release(_lib.ptr(ws))
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _lib.check(L.mg_gemm_workspace_init(_lib.ptr(ws), ws.numel(), _lib.stream_of(ws)), "mg_gemm_workspace_init")
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False,
          deterministic=None):
     """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm).
-    deterministic (default: torch.are_deterministic_algorithms_enabled()): no split along K,
-    so fp32 results are the same on every run."""
+    Results repeat bit for bit. deterministic (default: torch.are_deterministic_algorithms_enabled())
+    also rules out the split along K, so the sum order depends only on K."""
     if deterministic is None:
         deterministic = torch.are_deterministic_algorithms_enabled()
     flags = (FLAG_ACCUMULATE if accumulate else 0) | (FLAG_DETERMINISTIC if deterministic else 0)
@@ -38,9 +57,13 @@ def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None
     if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
         raise _lib.MingruHipError("mg_gemm bias must be contiguous float32")
     L = _lib.lib()
+    cd = _lib.dtype_code(out.dtype)
+    wsb = L.mg_gemm_workspace_bytes(a_layout, b_layout, M, N, K, epilogue, cd, flags)
+    ws = _workspace(out.device, wsb) if wsb else None
     rc = L.mg_gemm(a_layout, _lib.ptr(a), lda, b_layout, _lib.ptr(b), ldb, M, N, K, epilogue,
                    _lib.ptr(bias) if bias is not None else None, _lib.ptr(aux) if aux is not None else None, ldaux,
-                   _lib.dtype_code(out.dtype), _lib.ptr(out), ldc, flags, _lib.stream_of(out))
+                   cd, _lib.ptr(out), ldc, flags, _lib.ptr(ws), ws.numel() if ws is not None else 0,
+                   _lib.stream_of(out))
     _lib.check(rc, "mg_gemm")
     return out
 

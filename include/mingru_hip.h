@@ -222,12 +222,17 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  *   gelu(x) = x/2 (1 + erf(x/sqrt(2))), nn.GELU()'s exact form.
  * flags (bit set):
  *   MG_GEMM_ACCUMULATE (fp32 C, no epilogue): C += A B.
- *   MG_GEMM_DETERMINISTIC: no split along K. Without it, fp32 outputs with
- *     few output tiles are split along K across workgroups that add with
- *     fp32 atomics (the library zeroes C first unless accumulating), so the
- *     summation order, and the last bit of the result, can vary run to run.
- *     With it every element is summed by one workgroup in a fixed order and
- *     the result is the same on every run.
+ *   MG_GEMM_DETERMINISTIC: never split along K.
+ * Split along K: fp32 outputs with few output tiles are split along K over
+ *   several workgroups when a workspace is given. Each writes its partial
+ *   tile there; the last one of a tile to finish adds the partials, in
+ *   split order, into C (plus C's old value when accumulating), so results
+ *   repeat bit for bit either way (split and unsplit sums differ in order).
+ *   workspace: mg_gemm_workspace_bytes(...) bytes (0: the product never
+ *   splits; NULL is then fine), 256-byte aligned, initialised once by
+ *   mg_gemm_workspace_init (its counters must start at zero; the kernels
+ *   leave them at zero). A NULL workspace runs unsplit. Calls sharing a
+ *   workspace must be ordered on one stream.
  * Requirements: N % 8 == 0; K % 8 == 0 if an operand is K-contiguous;
  *   M % 8 == 0 if A is MN-contiguous; lda, ldb, ldaux % 8 == 0; ldc % 8 == 0
  *   (bf16 C) or % 4 == 0 (fp32 C); A, B, C, bias, aux 16-byte aligned; each
@@ -246,7 +251,12 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
             int b_layout, const void* B, int64_t ldb,
             int M, int N, int K,
             int epilogue, const float* bias, void* aux, int64_t ldaux,
-            int c_dtype, void* C, int64_t ldc, int flags, void* stream);
+            int c_dtype, void* C, int64_t ldc, int flags,
+            void* workspace, size_t workspace_bytes, void* stream);
+size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
+                               int c_dtype, int flags);
+int mg_gemm_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+int mg_gemm_workspace_release(void* workspace);
 
 /* ------------------------------------------------------------------------
  * Streaming loss head: logits GEMM + log-softmax + cross-entropy + gradient.

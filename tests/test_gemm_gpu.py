@@ -114,18 +114,26 @@ def test_gemm_accumulate_and_split():
 
 
 def test_gemm_deterministic_flag():
-    """Weight-gradient product with and without the split along K: the
-    deterministic form repeats bit for bit and agrees with the split one."""
+    """Weight-gradient product with and without the split along K (partials
+    summed in split order by the tile's last workgroup): both forms repeat bit
+    for bit, also with other shapes run on the same workspace in between, and
+    they agree with each other."""
     from gruboros_amd.gemm import linear_dw
 
     g = torch.Generator(device=DEV).manual_seed(11)
     dy = torch.randn(16376, 1024, device=DEV, generator=g).to(torch.bfloat16)
     x = torch.randn(16376, 1024, device=DEV, generator=g).to(torch.bfloat16)
+    dy4 = torch.randn(16376, 4096, device=DEV, generator=g).to(torch.bfloat16)
     d1 = linear_dw(dy, x, deterministic=True)
     d2 = linear_dw(dy, x, deterministic=True)
     split = linear_dw(dy, x, deterministic=False)
+    w4 = linear_dw(dy4, x, deterministic=False)   # another split plan on the same workspace
+    split2 = linear_dw(dy, x, deterministic=False)
+    w4b = linear_dw(dy4, x, deterministic=False)
     assert torch.equal(d1, d2)
+    assert torch.equal(split, split2) and torch.equal(w4, w4b)
     assert _rel(split, d1) < 1e-6
+    assert _rel(w4, dy4.float().t() @ x.float()) < 1e-5
     acc = d1.clone()
     linear_dw(dy, x, out=acc, accumulate=True, deterministic=True)
     assert _rel(acc, 2 * d1) < 1e-6
