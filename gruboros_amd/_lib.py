@@ -52,8 +52,6 @@ SIGNATURES = {
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
-    "mg_gemm_workspace_init": (_c_int, [_vp, _c_size, _vp]),
-    "mg_gemm_workspace_release": (_c_int, [_vp]),
 }
 
 _LIB = None

@@ -37,14 +37,11 @@
 //   GELU_GRAD  C = acc * gelu'(aux[m][n])                     (its backward)
 // with gelu(x) = x/2 (1 + erf(x / sqrt 2)), the exact form of nn.GELU().
 // fp32 outputs may be split along K over several workgroups: each writes its
-// partial tile to a workspace, and the last of a tile's workgroups to finish
-// (a per-tile counter) adds the partials in split order into C, so the
-// result does not depend on scheduling.
+// partial tile to a workspace, and a second kernel adds the partials in split
+// order into C, so the result does not depend on scheduling.
 
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
-#include <unordered_map>
 
 #include "mg_common.h"
 
@@ -67,7 +64,6 @@ struct Params {
   int tiles_m, tiles_n;
   int kt_per_split;  // k-tiles per split (gridDim.y splits)
   float* part;       // split partials: gridDim.y dense [M, N] fp32 slices
-  uint32_t* tile_cnt;  // per-tile arrival counters (zero between calls)
   int accumulate;    // C += (fp32 outputs)
   uint32_t a_span, b_span;  // bytes from A / B to one past their last element
   uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
@@ -435,30 +431,9 @@ __device__ __forceinline__ void mainloop_pp(const Params& p, uint4* smem, int m0
 }
 
 // Workgroup tile BM x BN, WM x WN waves each owning (BM/WM) x (BN/WN).
-// Split partials cross workgroups on other XCDs, whose L2s are not coherent
-// with each other for plain accesses: they are written and read with
-// device-scope atomic stores and loads (the coherent, L2-bypassing forms),
-// 8 bytes at a time, so no L2 writeback or invalidation is needed.
-__device__ __forceinline__ void store_coherent(float* p, const f4& x) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(p);
-  __hip_atomic_store(q, (static_cast<uint64_t>(__float_as_uint(x.v[1])) << 32) | __float_as_uint(x.v[0]),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, (static_cast<uint64_t>(__float_as_uint(x.v[3])) << 32) | __float_as_uint(x.v[2]),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f4 load_coherent(const float* p) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
-  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  f4 x;
-  x.v[0] = __uint_as_float(static_cast<uint32_t>(a)); x.v[1] = __uint_as_float(static_cast<uint32_t>(a >> 32));
-  x.v[2] = __uint_as_float(static_cast<uint32_t>(b)); x.v[3] = __uint_as_float(static_cast<uint32_t>(b >> 32));
-  return x;
-}
-
 // How a workgroup's tile reaches C: written (C_STORE), added to C by its one
-// writer (C_ADD), or written as a split-K partial and summed into C by the
-// tile's last workgroup (C_SPLIT).
+// writer (C_ADD), or written as a split-K partial (C_SPLIT; split_reduce_kernel
+// then sums the partials into C).
 enum CMode { C_STORE = 0, C_ADD = 1, C_SPLIT = 2 };
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
@@ -585,50 +560,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x.v[e] = old.v[e] + x.v[e];
           }
-          if constexpr (CMODE == C_SPLIT) {
-            store_coherent(reinterpret_cast<float*>(cp), x);
-          } else {
-            io4<TC>::store(cp, x);
-          }
+          io4<TC>::store(cp, x);
         } else {
           *reinterpret_cast<uint4*>(cp) = raw;
         }
       }
     }
     __syncthreads();
-  }
-  if constexpr (CMODE == C_SPLIT) {
-    // Count arrivals once the partial has been written (device-coherent
-    // stores, completed); the last workgroup of the tile sums the gridDim.y
-    // partials in split order (plus C when accumulating) and resets the
-    // counter for the next call.
-    __shared__ int s_last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(p.tile_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      s_last = old + 1 == gridDim.y;
-      if (s_last) __hip_atomic_store(p.tile_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    constexpr int kChunks = BM * BN / 4;  // 4-float chunks of the tile
-    const int64_t slice = static_cast<int64_t>(p.M) * p.N;
-#pragma unroll 2
-    for (int q = threadIdx.x; q < kChunks; q += 64 * WM * WN) {
-      const int m = m0 + q / (BN / 4), n = n0 + (q % (BN / 4)) * 4;
-      if (m >= p.M || n >= p.N) continue;
-      float* cp = static_cast<float*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
-      f4 sum = p.accumulate ? io4<float>::load(cp) : io4<float>::fill(0.0f);
-      const float* pp = p.part + static_cast<int64_t>(m) * p.N + n;
-      for (int sp = 0; sp < static_cast<int>(gridDim.y); ++sp) {
-        const f4 v = load_coherent(pp + sp * slice);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
-      }
-      io4<float>::store(cp, sum);
-    }
   }
 }
 
@@ -730,10 +668,24 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   if (threadIdx.x == 0) loss_part[blockIdx.x] = s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3];
 }
 
-__global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {  // workspace initialisation
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n16;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    p[i] = make_uint4(0, 0, 0, 0);
+// C[m, n] (+)= sum over the S split partials, added in split order.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                           float* __restrict__ C, int64_t ldc, int accumulate) {
+  const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
+  const int64_t slice = static_cast<int64_t>(M) * N;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n4;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t m = i / (N / 4), n = (i % (N / 4)) * 4;
+    float* cp = C + m * ldc + n;
+    f4 sum = accumulate ? io4<float>::load(cp) : io4<float>::fill(0.0f);
+    const float* pp = part + m * N + n;
+    for (int s = 0; s < S; ++s) {
+      const f4 v = io4<float>::load(pp + s * slice);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
+    }
+    io4<float>::store(cp, sum);
+  }
 }
 
 constexpr int kCUs = 256;
@@ -766,13 +718,10 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   return pl;
 }
 
-// Workspace of a split plan: tile counters, then the partials. Only plans
-// with fewer tiles than 2 x kCUs split, so the counter area has one fixed
-// size (a workspace can then serve products of different shapes).
-constexpr size_t kCounterBytes = 2 * kCUs * 4;
+// Workspace of a split plan: the partials.
 inline size_t ws_bytes(const Plan& pl, int M, int N) {
   if (pl.ysplits <= 1) return 0;
-  return kCounterBytes + static_cast<size_t>(pl.ysplits) * M * N * sizeof(float);
+  return static_cast<size_t>(pl.ysplits) * M * N * sizeof(float);
 }
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
@@ -812,10 +761,6 @@ int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, 
   return dispatch_epi<BM, BN, 2, WN, false, true>(p, pl, epi, c_dtype, s);
 }
 
-// Host-side record of initialised workspaces (address -> size), so that a
-// split product never runs on counters that were not zeroed.
-std::mutex g_ws_mu;
-std::unordered_map<uintptr_t, size_t> g_ws;
 
 }  // namespace gemm
 }  // namespace mg
@@ -877,27 +822,24 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
   }
 
   if (K == 0 && accumulate) return MG_OK;
-  // Without a workspace the product runs unsplit; with one, the split plan
-  // needs it initialised and large enough.
+  // Without a workspace the product runs unsplit.
   gemm::Plan pl = gemm::plan(M, N, K, ak, bk, c_dtype, epilogue, deterministic || !workspace);
   if (pl.ysplits > 1) {
     const size_t need = gemm::ws_bytes(pl, M, N);
     if (workspace_bytes < need)
       return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu (mg_gemm_workspace_bytes)", fn,
                   workspace_bytes, need);
-    if (!aligned(workspace, 256)) return fail(MG_ERR_ARG, "%s: workspace not 256-byte aligned", fn);
-    {
-      std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
-      const auto it = gemm::g_ws.find(reinterpret_cast<uintptr_t>(workspace));
-      if (it == gemm::g_ws.end() || it->second < need)
-        return fail(MG_ERR_WORKSPACE, "%s: workspace not initialised (mg_gemm_workspace_init)", fn);
-    }
-    p.tile_cnt = static_cast<uint32_t*>(workspace);
-    p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + gemm::kCounterBytes);
+    if (!aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
+    p.part = static_cast<float*>(workspace);
   }
   p.accumulate = accumulate ? 1 : 0;
-  return pl.big ? gemm::dispatch_layout<256, 256>(p, pl, ak, bk, epilogue, c_dtype, s)
-                : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epilogue, c_dtype, s);
+  const int rc = pl.big ? gemm::dispatch_layout<256, 256>(p, pl, ak, bk, epilogue, c_dtype, s)
+                        : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epilogue, c_dtype, s);
+  if (rc || pl.ysplits <= 1) return rc;
+  const int64_t n4 = int64_t(M) * (N / 4);
+  hipLaunchKernelGGL(gemm::split_reduce_kernel, dim3(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048))),
+                     dim3(256), 0, s, p.part, pl.ysplits, M, N, static_cast<float*>(C), ldc, p.accumulate);
+  return check_launch(fn);
 }
 
 extern "C" size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
@@ -906,25 +848,6 @@ extern "C" size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int
   const gemm::Plan pl = gemm::plan(M, N, K, a_layout == MG_KCONTIG, b_layout == MG_KCONTIG, c_dtype, epilogue,
                                    flags & MG_GEMM_DETERMINISTIC);
   return gemm::ws_bytes(pl, M, N);
-}
-
-extern "C" int mg_gemm_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "mg_gemm_workspace_init";
-  if (!workspace || workspace_bytes < 256 || !aligned(workspace, 256))
-    return fail(MG_ERR_ARG, "%s: need a 256-byte aligned workspace of at least 256 bytes", fn);
-  const int64_t n16 = static_cast<int64_t>(workspace_bytes / 16);
-  hipLaunchKernelGGL(gemm::zero_kernel, dim3(static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<uint4*>(workspace), n16);
-  if (int rc = check_launch(fn)) return rc;
-  std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
-  gemm::g_ws[reinterpret_cast<uintptr_t>(workspace)] = workspace_bytes;
-  return MG_OK;
-}
-
-extern "C" int mg_gemm_workspace_release(void* workspace) {
-  std::lock_guard<std::mutex> lock(gemm::g_ws_mu);
-  gemm::g_ws.erase(reinterpret_cast<uintptr_t>(workspace));
-  return MG_OK;
 }
 
 extern "C" int mg_logits_cross_entropy_partials(int64_t N) {

@@ -22,8 +22,7 @@ def _rows(t, name):
     return t.stride(0)
 
 
-# Split-K workspaces, one per (device, stream), grown on demand; each is
-# initialised (zeroed) once, after which the kernels keep its counters at zero.
+# Split-K partial buffers, one per (device, stream), grown on demand.
 _WORKSPACES = {}
 
 
@@ -32,11 +31,7 @@ def _workspace(device, nbytes):
     key = (device.index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        L = _lib.lib()
-        if ws is not None:
-            L.mg_gemm_workspace_release(_lib.ptr(ws))
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _lib.check(L.mg_gemm_workspace_init(_lib.ptr(ws), ws.numel(), _lib.stream_of(ws)), "mg_gemm_workspace_init")
         _WORKSPACES[key] = ws
     return ws
 

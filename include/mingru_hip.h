@@ -225,14 +225,12 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  *   MG_GEMM_DETERMINISTIC: never split along K.
  * Split along K: fp32 outputs with few output tiles are split along K over
  *   several workgroups when a workspace is given. Each writes its partial
- *   tile there; the last one of a tile to finish adds the partials, in
- *   split order, into C (plus C's old value when accumulating), so results
- *   repeat bit for bit either way (split and unsplit sums differ in order).
+ *   tile there and a second kernel adds the partials, in split order, into C
+ *   (plus C's old value when accumulating), so results repeat bit for bit
+ *   either way (split and unsplit sums differ in order).
  *   workspace: mg_gemm_workspace_bytes(...) bytes (0: the product never
- *   splits; NULL is then fine), 256-byte aligned, initialised once by
- *   mg_gemm_workspace_init (its counters must start at zero; the kernels
- *   leave them at zero). A NULL workspace runs unsplit. Calls sharing a
- *   workspace must be ordered on one stream.
+ *   splits), 16-byte aligned; NULL runs unsplit. Calls sharing a workspace
+ *   must be ordered on one stream.
  * Requirements: N % 8 == 0; K % 8 == 0 if an operand is K-contiguous;
  *   M % 8 == 0 if A is MN-contiguous; lda, ldb, ldaux % 8 == 0; ldc % 8 == 0
  *   (bf16 C) or % 4 == 0 (fp32 C); A, B, C, bias, aux 16-byte aligned; each
@@ -255,8 +253,6 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
             void* workspace, size_t workspace_bytes, void* stream);
 size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
                                int c_dtype, int flags);
-int mg_gemm_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
-int mg_gemm_workspace_release(void* workspace);
 
 /* ------------------------------------------------------------------------
  * Streaming loss head: logits GEMM + log-softmax + cross-entropy + gradient.
