@@ -22,6 +22,23 @@ def _rows(t, name):
     return t.stride(0)
 
 
+def spans_ok(rows, ld):
+    """Whether a bf16 operand of `rows` rows at row stride `ld` fits mg_gemm's
+    buffer ranges (under 2 GiB, with 256 rows of slack)."""
+    return (rows + 256) * ld * 2 < (1 << 31)
+
+
+def fits(a, w):
+    """Whether linear_fwd(a, w) and linear_dx(a, w) (with a GELU pre-activation
+    of a's rows) meet mg_gemm's rules: bf16 2-D tensors with unit inner
+    stride, a's and both of w's dimensions and the row strides multiples of
+    8, 16-byte aligned, every operand under 2 GiB."""
+    return all(t.dtype == torch.bfloat16 and t.dim() == 2 and t.stride(1) == 1 and t.stride(0) % 8 == 0
+               and t.data_ptr() % 16 == 0 for t in (a, w)) and a.shape[1] % 8 == 0 and \
+        w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0 and spans_ok(a.shape[0], max(a.stride(0), *w.shape)) and \
+        spans_ok(w.shape[0], w.stride(0))
+
+
 # Split-K partial buffers, one per (device, stream), grown on demand.
 _WORKSPACES = {}
 

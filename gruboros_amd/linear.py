@@ -39,7 +39,8 @@ def _dw_ok(dy2, x2):
     """Shapes the MFMA weight-gradient product takes (mg_gemm, both operands MN-contiguous)."""
     return (dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and dy2.stride(1) == 1 and x2.stride(1) == 1
             and dy2.shape[1] % 8 == 0 and x2.shape[1] % 8 == 0 and dy2.stride(0) % 8 == 0 and x2.stride(0) % 8 == 0
-            and dy2.data_ptr() % 16 == 0 and x2.data_ptr() % 16 == 0)
+            and dy2.data_ptr() % 16 == 0 and x2.data_ptr() % 16 == 0
+            and gemm.spans_ok(dy2.shape[0], dy2.stride(0)) and gemm.spans_ok(x2.shape[0], x2.stride(0)))
 
 
 def column_sum(x2):
@@ -112,52 +113,26 @@ def linear(x, layer):
     return BF16Linear.apply(x, w, b, bf16_copy(w))
 
 
+# Where the GELU of the FeedForward runs (measured on MI355X in the cfg3
+# training step, 16376 rows):
+#   forward: hipBLASLt's x W1^T + b1 (94 us) and a GELU pass (43 us), against
+#     187 us for mg_gemm with the bias + GELU epilogue;
+#   backward: hipBLASLt's dY W2 and mg_gelu_bwd (fused with the first bias
+#     gradient), 208 us against 244 us for mg_gemm's GELU-gradient epilogue
+#     plus a column sum (that epilogue's VALU work runs after the tile's MFMA
+#     loop with nothing to overlap it).
+# Both fused forms are exact and tested; they stay off while slower.
+FUSED_GELU_FORWARD = False
+FUSED_GELU_BACKWARD = False
+
+
 class BF16FeedForward(torch.autograd.Function):
     """Linear -> GELU -> Linear (reference mingru/minLM.py:17-23) in bf16 with
-    the GELU fused into the MFMA products: the first product's epilogue adds
-    the bias, keeps the pre-activation and applies GELU; in the backward the
-    product dY W2 is multiplied by GELU'(pre-activation) in its epilogue."""
-
-    @staticmethod
-    def forward(ctx, x, w1, b1, w2, b2, w1b, w2b, b2b):
-        shape = x.shape
-        x2 = x.reshape(-1, shape[-1])
-        if not x2.is_contiguous():
-            x2 = x2.contiguous()
-        pre = torch.empty(x2.shape[0], w1b.shape[0], device=x.device, dtype=torch.bfloat16)
-        h = gemm.linear_fwd(x2, w1b, b1.detach().contiguous(), gelu_pre=pre)
-        y = F.linear(h, w2b, b2b)
-        ctx.save_for_backward(x2, pre, h, w1b, w2b)
-        return y.view(*shape[:-1], w2b.shape[0])
-
-    @staticmethod
-    def backward(ctx, dy):
-        x2, pre, h, w1b, w2b = ctx.saved_tensors
-        dy2 = dy.reshape(-1, dy.shape[-1])
-        if dy2.dtype != torch.bfloat16:
-            dy2 = dy2.to(torch.bfloat16)
-        if not dy2.is_contiguous():
-            dy2 = dy2.contiguous()
-        dpre = gemm.linear_dx(dy2, w2b, gelu_pre=pre)
-        dw2 = gemm.linear_dw(dy2, h) if _dw_ok(dy2, h) else _mm_f32(dy2.t(), h)
-        db2 = column_sum(dy2)
-        dx = torch.mm(dpre, w1b).view(*dy.shape[:-1], w1b.shape[1])
-        dw1 = gemm.linear_dw(dpre, x2) if _dw_ok(dpre, x2) else _mm_f32(dpre.t(), x2)
-        db1 = column_sum(dpre)
-        return dx, dw1, db1, dw2, db2, None, None, None
-
-
-# The fused path is exact and tested, but on MI355X it is not yet faster:
-# the GELU epilogues run after the MFMA main loop of each tile with nothing
-# to overlap them (one 128 KiB-LDS workgroup per CU), and the hand-written
-# main loop trails hipBLASLt on these shapes. Off by default until it wins.
-FUSED_FEED_FORWARD = False
-
-
-class BF16FeedForwardLib(torch.autograd.Function):
-    """Linear -> GELU -> Linear in bf16 with library GEMMs (hipBLASLt via
-    torch) and this library's GELU backward fused with the first bias
-    gradient, plus its column sums for the second."""
+    fp32 weight gradients. Forward: either mg_gemm with the bias + GELU
+    epilogue (keeping bf16(x W1^T + b1) for the backward) or hipBLASLt (via
+    torch) and a GELU pass. Backward: either mg_gemm's GELU-gradient
+    epilogue on dY W2 or hipBLASLt's dY W2 and mg_gelu_bwd; weight gradients
+    on mg_gemm, bias gradients on mg_column_sum / mg_gelu_bwd."""
 
     @staticmethod
     def forward(ctx, x, w1, b1, w2, b2, w1b, w2b, b1b, b2b):
@@ -165,8 +140,12 @@ class BF16FeedForwardLib(torch.autograd.Function):
         x2 = x.reshape(-1, shape[-1])
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        pre = F.linear(x2, w1b, b1b)
-        h = F.gelu(pre)
+        if FUSED_GELU_FORWARD and gemm.fits(x2, w1b):
+            pre = torch.empty(x2.shape[0], w1b.shape[0], device=x.device, dtype=torch.bfloat16)
+            h = gemm.linear_fwd(x2, w1b, b1.detach().contiguous(), gelu_pre=pre)
+        else:
+            pre = F.linear(x2, w1b, b1b)
+            h = F.gelu(pre)
         y = F.linear(h, w2b, b2b)
         ctx.save_for_backward(x2, pre, h, w1b, w2b)
         return y.view(*shape[:-1], w2b.shape[0])
@@ -179,8 +158,11 @@ class BF16FeedForwardLib(torch.autograd.Function):
             dy2 = dy2.to(torch.bfloat16)
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
-        dh = torch.mm(dy2, w2b)
-        dpre, db1 = gelu_backward(dh, pre)
+        if FUSED_GELU_BACKWARD and gemm.fits(dy2, w2b):
+            dpre = gemm.linear_dx(dy2, w2b, gelu_pre=pre)
+            db1 = column_sum(dpre)
+        else:
+            dpre, db1 = gelu_backward(torch.mm(dy2, w2b), pre)
         dw2 = gemm.linear_dw(dy2, h) if _dw_ok(dy2, h) else _mm_f32(dy2.t(), h)
         db2 = column_sum(dy2)
         dx = torch.mm(dpre, w1b).view(*dy.shape[:-1], w1b.shape[1])
@@ -195,8 +177,5 @@ def feed_forward(x, ff):
         return l2(F.gelu(l1(x)))
     if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32 or l1.bias is None or l2.bias is None:
         raise TypeError(f"unsupported feed-forward: activations {x.dtype}, weight {l1.weight.dtype}")
-    if FUSED_FEED_FORWARD:
-        return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
-                                     bf16_copy(l2.weight), bf16_copy(l2.bias))
-    return BF16FeedForwardLib.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
-                                    bf16_copy(l2.weight), bf16_copy(l1.bias), bf16_copy(l2.bias))
+    return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
+                                 bf16_copy(l2.weight), bf16_copy(l1.bias), bf16_copy(l2.bias))

@@ -165,14 +165,17 @@ def test_gemm_model_sizes(which):
     assert _rel(got, ref) < tol
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_feed_forward_bf16_matches_fp64(fused, monkeypatch):
-    """bf16 FeedForward, fused (GELU in the MFMA epilogues) and unfused, vs the
-    fp64 reference Linear -> GELU -> Linear (reference mingru/minLM.py:17-23)."""
+@pytest.mark.parametrize("fused_fwd", [True, False])
+@pytest.mark.parametrize("fused_bwd", [True, False])
+def test_feed_forward_bf16_matches_fp64(fused_fwd, fused_bwd, monkeypatch):
+    """bf16 FeedForward with the GELU in the MFMA epilogues or in separate
+    passes (forward and backward independently) vs the fp64 reference
+    Linear -> GELU -> Linear (reference mingru/minLM.py:17-23)."""
     from gruboros_amd import linear as lin
     from gruboros_amd.linear import feed_forward
 
-    monkeypatch.setattr(lin, "FUSED_FEED_FORWARD", fused)
+    monkeypatch.setattr(lin, "FUSED_GELU_FORWARD", fused_fwd)
+    monkeypatch.setattr(lin, "FUSED_GELU_BACKWARD", fused_bwd)
     torch.manual_seed(4)
     D, F_ = 256, 1024
     ff = torch.nn.Sequential(torch.nn.Linear(D, F_), torch.nn.GELU(), torch.nn.Linear(F_, D)).to(DEV)
