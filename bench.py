@@ -152,6 +152,29 @@ def _event_time(fn, reps):
     return e0.elapsed_time(e1) / reps  # ms
 
 
+def bench_ceilings(n=1 << 28, reps=10):
+    """Achievable HBM bandwidth of plain streaming kernels on the same box, as a
+    yardstick for the scan's fraction of the datasheet peak: torch's copy
+    (1 read, 1 write), add (2 reads, 1 write) and addcmul (3 reads, 1 write)
+    over n bf16 elements per tensor (512 MiB each at the default n)."""
+    import torch
+
+    t = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(4)]
+    a, b, c, o = t
+    ops = {"copy_1r1w": (lambda: o.copy_(a), 2), "add_2r1w": (lambda: torch.add(a, b, out=o), 3),
+           "addcmul_3r1w": (lambda: torch.addcmul(a, b, c, out=o), 4)}
+    for _ in range(100):  # ~20 ms of copies first: the GPU clocks ramp up under sustained load
+        o.copy_(a)
+    res = {}
+    for name, (fn, tensors) in ops.items():
+        ms = _event_time(fn, reps)
+        res[name + "_GBs"] = tensors * 2 * n / (ms * 1e-3) / 1e9
+    res["peak_GBs"] = HBM_PEAK_GBS
+    del t, a, b, c, o
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64):
     """Generation (reference generate.py:184-212) on the cfg3 model: tokens/s of
     the per-token step, greedy sampling on the device, no host sync per token.
@@ -321,7 +344,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode"], default=None)
+    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode", "ceilings"], default=None)
     ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
                     help="training workload for `value`: cfg3 (the BASELINE metric, default) or cfg5 "
                          "(~1B params: d2048 L24, batch 4 x seq 4096, gradient accumulation 4)")
@@ -352,7 +375,10 @@ def main():
         print("[bench] copy calibration: 3 x 1 GiB device copies (1073741824 B read + written each)",
               file=sys.stderr, flush=True)
 
-    train = scan = kern = dec = None
+    train = scan = kern = dec = ceil = None
+    if args.only in (None, "ceilings"):
+        ceil = bench_ceilings()
+        print(f"[bench] ceilings {json.dumps(ceil)}", file=sys.stderr, flush=True)
     if args.only in (None, "scan"):
         scan = bench_scan(args.scan_reps)
         print(f"[bench] scan {json.dumps(scan)}", file=sys.stderr, flush=True)
@@ -411,6 +437,8 @@ def main():
                                 "flops_per_step": train["flops_per_step"]}
         out["tokens_per_s_predicted"] = train["tokens_per_step"] * (1 - 1 / (2048 if args.workload == "cfg3" else 4096)) \
             / (train["ms_per_step"] * 1e-3)
+    if ceil:
+        out["hbm_ceilings"] = ceil
     if kern:
         out["kernels"] = kern
     if dec:

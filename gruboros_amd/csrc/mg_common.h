@@ -215,18 +215,14 @@ int launch_reduce_partials(const float* part, int P, int C, float* out, hipStrea
 // ---------------------------------------------------------------- look-back words
 //
 // One 64-bit word per (time tile, channel) carries a tile's scan state
-// between workgroups. Low half = tag, high half = value (fp32 bits).
-//   tag == 0                : not yet published (workspace is zeroed per call)
-//   tag & 0x80000000        : aggregate; coefficient = bits(tag & 0x7fffffff)
-//   tag == 1                : inclusive prefix; value is the carry itself
-// A coefficient is a product of a_t in [0, 1], so its sign bit is free.
-
-// Look-back words: value in the high half, tag in the low half. An inclusive
-// prefix has tag kTagIncl; an aggregate (A, V) carries A's bits with the
-// sign bit set (A is in [0, 1], so its sign bit and bit 30 are free). Bit 30
-// of either tag is the call parity: a workspace alternates parity from call
-// to call, so words left by the previous call read as "not ready" and the
-// words need no clearing between calls.
+// between workgroups: value (fp32 bits) in the high half, tag in the low
+// half. An inclusive prefix has tag kTagIncl and its value is the carry
+// itself; an aggregate (A, V) carries A's bits with the sign bit set (A is a
+// product of a_t in [0, 1], so its sign bit and bit 30 are free). Bit 30 of
+// either tag is the call parity: a workspace alternates parity from call to
+// call, so words left by the previous call (or the zeros of a fresh
+// workspace) read as "not ready" and the words need no clearing between
+// calls.
 constexpr uint32_t kTagIncl = 1u;
 constexpr uint32_t kTagAggBit = 0x80000000u;
 constexpr uint32_t kTagParity = 0x40000000u;

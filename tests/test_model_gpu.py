@@ -193,9 +193,9 @@ def test_checkpoint_resume_and_clonal_merge():
     and optimizer, then optimizer.train()). Training resumed from it follows
     the uninterrupted run; the gossip clonal merge
     (gossip/evolutionary_node.py:296-304) is the same load into a live model.
-    Run with torch's deterministic switch, under which the weight-gradient
-    products do not split along K (no atomics), so both runs add in the same
-    order and the comparison can be exact."""
+    Run with torch's deterministic switch, so that the library products
+    called through torch pick fixed-order algorithms and the comparison can
+    be exact."""
     from gruboros_amd.mingru.minLM import minLM
     from gruboros_amd.optim import AdamWScheduleFree
 
