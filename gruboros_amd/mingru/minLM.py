@@ -20,7 +20,7 @@ from torch.nn import Module, ModuleList, RMSNorm
 from ..linear import feed_forward
 from ..linear import linear as _linear
 from ..loss import logits_cross_entropy
-from ..norm import add_rms_norm, rms_norm
+from ..norm import add_rms_norm, rms_norm, rms_norm_residual
 from .minGRU import minGRU
 
 
@@ -150,7 +150,7 @@ class minLM(Module):
                     x, pending = x + pending.float(), None
                 x = conv(x) + x
             if pending is None:
-                n = rms_norm(x, norm.weight, cd)
+                x, n = rms_norm_residual(x, norm.weight, cd)
             else:
                 x, n = add_rms_norm(x, pending, norm.weight, cd)
 

@@ -52,6 +52,27 @@ def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta):
     return dx, ddelta, dw
 
 
+class RMSNormResidualFn(torch.autograd.Function):
+    """(x, rmsnorm(x) * w) for an fp32 x that also continues as the residual
+    stream: the gradient reaching x through the residual joins the norm's
+    gradient inside the backward kernel instead of in a separate add."""
+
+    @staticmethod
+    def forward(ctx, x, w, out_dtype):
+        _, y, rstd = _fwd(x, None, w, out_dtype)
+        ctx.save_for_backward(x, w, rstd)
+        ctx.set_materialize_grads(False)
+        return x.view_as(x), y
+
+    @staticmethod
+    def backward(ctx, dx_res, dy):
+        x, w, rstd = ctx.saved_tensors
+        if dx_res is None and dy is None:
+            return None, None, None
+        dx, _, dw = _bwd(x, w, rstd, dy, dx_res, ctx.needs_input_grad[0], None, False)
+        return dx, (dw if ctx.needs_input_grad[1] else None), None
+
+
 class RMSNormFn(torch.autograd.Function):
     """y = x * w / sqrt(mean(x^2) + eps) over the last dim; x fp32, y in out_dtype."""
 
@@ -76,11 +97,14 @@ class AddRMSNormFn(torch.autograd.Function):
         x_out, y, rstd = _fwd(x, delta, w, out_dtype)
         ctx.save_for_backward(x_out, w, rstd)
         ctx.delta_dtype = delta.dtype
+        ctx.set_materialize_grads(False)  # an unused x_out (the final norm's) gets no zero tensor
         return x_out, y
 
     @staticmethod
     def backward(ctx, dx_out, dy):
         xn, w, rstd = ctx.saved_tensors
+        if dx_out is None and dy is None:
+            return None, None, None, None
         want_dx, want_dd = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dx, dd, dw = _bwd(xn, w, rstd, dy, dx_out, want_dx, ctx.delta_dtype, want_dd)
         return dx, dd, (dw if ctx.needs_input_grad[2] else None), None
@@ -100,6 +124,13 @@ def rms_norm(x, w, out_dtype=None):
     """RMSNorm of an fp32 tensor over its last dim with fp32 epsilon; output in out_dtype."""
     _check(x, w)
     return RMSNormFn.apply(x.contiguous(), w, out_dtype or x.dtype)
+
+
+def rms_norm_residual(x, w, out_dtype=None):
+    """Returns (x, rms_norm(x, w)) where the first output carries x on as the
+    residual stream (one backward kernel for both uses of x)."""
+    _check(x, w)
+    return RMSNormResidualFn.apply(x.contiguous(), w, out_dtype or x.dtype)
 
 
 def add_rms_norm(x, delta, w, out_dtype=None):
