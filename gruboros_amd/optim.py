@@ -19,11 +19,37 @@ exactly as the package's mode switch does.
 
 step() runs the whole update as one mg_sf_adamw_step launch (all parameter
 tensors, one pass over p, g, z, v), which also refreshes the bf16 copies of
-the weights used by the bf16 linear layers (gruboros_amd.linear).
+the weights used by the bf16 linear layers (gruboros_amd.linear). Its tensor
+table (pointers and sizes) goes to the device from two pinned host buffers
+kept across steps, used in turn, so a step allocates no host memory.
 """
 import torch
 
 from ._lib import check, lib, require_cuda, stream_of
+
+
+class _TableBuffers:
+    """Pinned host rows for mg_sf_adamw_step's table, two buffers used in turn:
+    a buffer is rewritten only after the copy that last read it has run."""
+
+    def __init__(self, rows, device):
+        self.host = [torch.empty((rows, 7), dtype=torch.int64).pin_memory() for _ in range(2)]
+        self.done = [None, None]
+        self.dev = torch.empty((rows, 7), dtype=torch.int64, device=device)
+        self.turn = 0
+
+    def upload(self, rows, stream):
+        i = self.turn
+        self.turn ^= 1
+        if self.done[i] is not None:
+            self.done[i].synchronize()
+        n = len(rows)
+        self.host[i][:n].copy_(torch.tensor(rows, dtype=torch.int64))
+        self.dev[:n].copy_(self.host[i][:n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self.done[i] = ev
+        return self.dev
 
 
 class AdamWScheduleFree(torch.optim.Optimizer):
@@ -32,6 +58,7 @@ class AdamWScheduleFree(torch.optim.Optimizer):
         defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, warmup_steps=warmup_steps, r=r,
                         k=0, train_mode=False, weight_sum=0.0, lr_max=-1.0, weight_lr_power=weight_lr_power)
         super().__init__(params, defaults)
+        self._tables = {}
 
     @torch.no_grad()
     def eval(self):
@@ -102,8 +129,11 @@ class AdamWScheduleFree(torch.optim.Optimizer):
                 nchunks += (n + chunk - 1) // chunk
             if rows:
                 dev = group["params"][0].device
-                host = torch.tensor(rows, dtype=torch.int64).pin_memory()
-                table = host.to(dev, non_blocking=True)
+                key = id(group)
+                buf = self._tables.get(key)
+                if buf is None or buf.dev.shape[0] < len(rows) or buf.dev.device != dev:
+                    buf = self._tables[key] = _TableBuffers(len(group["params"]), dev)
+                table = buf.upload(rows, torch.cuda.current_stream(dev))
                 rc = lib().mg_sf_adamw_step(table.data_ptr(), len(rows), nchunks, b2, 1 - b2, bc2, group["eps"],
                                             group["weight_decay"], ckp1, y_lr, lr,
                                             stream_of(group["params"][0]))
