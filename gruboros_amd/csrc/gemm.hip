@@ -202,14 +202,16 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 }
 
 // The MFMA main loop of one workgroup tile BM x BN over k-tiles [kt0, kt1):
-// WM x WN waves each accumulate (BM/WM) x (BN/WN) as 32 x 32 blocks. The
-// loads of tile t+1 are issued at the start of tile t, the fragments of
-// k-step s+1 are read under the MFMAs of step s, one barrier per k-tile.
-// EARLY: the barrier comes before the MFMAs of the tile's last k-step; after
-//   it tile t+1 is visible to every wave, so its first fragments are read
-//   under those MFMAs (faster for 256 x 256 tiles).
-// otherwise: the barrier ends the tile, which leaves the loads the whole tile
-//   to land (faster for the 128 x 128 weight-gradient tiles, two per CU).
+// WM x WN waves each accumulate (BM/WM) x (BN/WN) as 32 x 32 blocks, one
+// barrier per k-tile.
+// EARLY: the loads of tile t+1 are issued at the start of tile t, the
+//   fragments of k-step s+1 are read under the MFMAs of step s, and the
+//   barrier comes before the MFMAs of the tile's last k-step; after it tile
+//   t+1 is visible to every wave, so its first fragments are read under those
+//   MFMAs (faster for 256 x 256 tiles).
+// otherwise: all of tile t's fragments are read, then tile t+1's loads are
+//   issued, then the MFMAs run; the barrier ends the tile (the 128 x 128
+//   weight-gradient tiles, two per CU).
 // Either way every wave is done reading stage t & 1 at the barrier, and the
 // next iteration's loads refill it.
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM, bool EARLY>
@@ -251,52 +253,75 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
 #pragma unroll
   for (int j = 0; j < NB; ++j) brow[j] = wn * (BN / WN) + j * 32;
 
-  bf16x8 af[2][MB], bfr[2][NB];
   if constexpr (EARLY) {
+    bf16x8 af[2][MB], bfr[2][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(smem, arow[i], 0, lane);
 #pragma unroll
     for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(smem + BM * 8, brow[j], 0, lane);
-  }
-  for (int t = 0; t < n; ++t) {
-    issue(t + 1);
-    const uint4* As = smem + (t & 1) * kStage;
-    const uint4* Bs = As + BM * 8;
-    if constexpr (!EARLY) {
+    for (int t = 0; t < n; ++t) {
+      issue(t + 1);
+      const uint4* As = smem + (t & 1) * kStage;
+      const uint4* Bs = As + BM * 8;
 #pragma unroll
-      for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(As, arow[i], 0, lane);
+      for (int s = 0; s < S; ++s) {
+        const int cur = s & 1;
+        if (s + 1 < S) {
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(Bs, brow[j], 0, lane);
-    }
+          for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(As, arow[i], s + 1, lane);
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const int cur = s & 1;
-      if (s + 1 < S) {
+          for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bs, brow[j], s + 1, lane);
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+          if (t + 1 < n) {
+            const uint4* An = smem + ((t + 1) & 1) * kStage;
+            const uint4* Bn = An + BM * 8;
 #pragma unroll
-        for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(As, arow[i], s + 1, lane);
+            for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(An, arow[i], 0, lane);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bs, brow[j], s + 1, lane);
-      } else if constexpr (EARLY) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t + 1 < n) {
-          const uint4* An = smem + ((t + 1) & 1) * kStage;
-          const uint4* Bn = An + BM * 8;
-#pragma unroll
-          for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(An, arow[i], 0, lane);
-#pragma unroll
-          for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bn, brow[j], 0, lane);
+            for (int j = 0; j < NB; ++j) bfr[cur ^ 1][j] = read_frag<BN, BKM>(Bn, brow[j], 0, lane);
+          }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    // Every fragment of tile t is read before tile t+1's loads are issued:
+    // the loads write LDS, and a read that follows them in program order
+    // waits for them (the compiler cannot tell the two stages apart), which
+    // would serialise each tile behind the next tile's loads. Read first, the
+    // loads then fly under all of tile t's MFMAs.
+    for (int t = 0; t < n; ++t) {
+      const uint4* As = smem + (t & 1) * kStage;
+      const uint4* Bs = As + BM * 8;
+      bf16x8 af[S][MB], bfr[S][NB];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) af[s][i] = read_frag<BM, AK>(As, arow[i], s, lane);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bfr[s][j] = read_frag<BN, BKM>(Bs, brow[j], s, lane);
+      }
+      issue(t + 1);
+      // keep the MFMAs between the issue and the wait (the scheduler would
+      // otherwise move them past the barrier, leaving the loads no time)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[s][j], af[s][i], acc[i][j], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (!EARLY) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
