@@ -45,6 +45,10 @@
 
 #include "mg_common.h"
 
+#ifndef MG_GEMM_INTERLEAVE
+#define MG_GEMM_INTERLEAVE 1
+#endif
+
 namespace mg {
 namespace gemm {
 
@@ -214,12 +218,11 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 //   weight-gradient tiles, two per CU).
 // Either way every wave is done reading stage t & 1 at the barrier, and the
 // next iteration's loads refill it.
-template <int BM, int BN, int WM, int WN, bool AK, bool BKM, bool EARLY>
-__device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, int n0, int kt0, int kt1,
-                                         f32x16 (&acc)[BM / WM / 32][BN / WN / 32]) {
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, bool EARLY, bool INTERLEAVE = false>
+__device__ __forceinline__ void mainloop(const Params& p, uint4* smem, uint4* s1, int m0, int n0, int kt0,
+                                         int kt1, f32x16 (&acc)[BM / WM / 32][BN / WN / 32]) {
   constexpr int T = 64 * WM * WN;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
-  constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
   constexpr int S = BK / 16;                            // k-steps per tile
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -238,7 +241,7 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
   // Loads of k-tile t (relative to kt0) into stage t & 1. Past kt1 they are
   // still issued (every wave waits on the same counts) but read as zero.
   auto issue = [&](int t) {
-    uint4* st = smem + ((t & 1) * kStage);
+    uint4* st = (t & 1) ? s1 : smem;
     la.load(oa, st, m0, p.M, (kt0 + t) * BK, kmax);
     lb.load(ob, st + BM * 8, n0, p.N, (kt0 + t) * BK, kmax);
   };
@@ -261,7 +264,7 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
     for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(smem + BM * 8, brow[j], 0, lane);
     for (int t = 0; t < n; ++t) {
       issue(t + 1);
-      const uint4* As = smem + (t & 1) * kStage;
+      const uint4* As = (t & 1) ? s1 : smem;
       const uint4* Bs = As + BM * 8;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -275,7 +278,7 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           __syncthreads();
           if (t + 1 < n) {
-            const uint4* An = smem + ((t + 1) & 1) * kStage;
+            const uint4* An = ((t + 1) & 1) ? s1 : smem;
             const uint4* Bn = An + BM * 8;
 #pragma unroll
             for (int i = 0; i < MB; ++i) af[cur ^ 1][i] = read_frag<BM, AK>(An, arow[i], 0, lane);
@@ -292,6 +295,45 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  } else if constexpr (INTERLEAVE) {
+    // stages smem and s1 are distinct __shared__ objects, run in pairs so
+    // that each is static: the reads of one then do not wait for the loads
+    // into the other, and the next tile's loads are issued first
+    bf16x8 af[2][MB], bfr[2][NB];
+    auto tile = [&](int t, const uint4* cur, uint4* nxt) __attribute__((always_inline)) {
+      la.load(oa, nxt, m0, p.M, (kt0 + t + 1) * BK, kmax);
+      lb.load(ob, nxt + BM * 8, n0, p.N, (kt0 + t + 1) * BK, kmax);
+      const uint4* Bs = cur + BM * 8;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(cur, arow[i], 0, lane);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, BKM>(Bs, brow[j], 0, lane);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int c = s & 1;
+        if (s + 1 < S) {
+#pragma unroll
+          for (int i = 0; i < MB; ++i) af[c ^ 1][i] = read_frag<BM, AK>(cur, arow[i], s + 1, lane);
+#pragma unroll
+          for (int j = 0; j < NB; ++j) bfr[c ^ 1][j] = read_frag<BN, BKM>(Bs, brow[j], s + 1, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[c][j], af[c][i], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+    int t = 0;
+    for (; t + 1 < n; t += 2) {
+      tile(t, smem, s1);
+      tile(t + 1, s1, smem);
+    }
+    if (t < n) tile(t, smem, s1);
   } else {
     // Every fragment of tile t is read before tile t+1's loads are issued:
     // the loads write LDS, and a read that follows them in program order
@@ -299,7 +341,7 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, int m0, i
     // would serialise each tile behind the next tile's loads. Read first, the
     // loads then fly under all of tile t's MFMAs.
     for (int t = 0; t < n; ++t) {
-      const uint4* As = smem + (t & 1) * kStage;
+      const uint4* As = (t & 1) ? s1 : smem;
       const uint4* Bs = As + BM * 8;
       bf16x8 af[S][MB], bfr[S][NB];
 #pragma unroll
@@ -465,7 +507,12 @@ template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename T
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
-  __shared__ uint4 smem[2 * kStage];
+  // 128 x 128 tiles keep their stages as two distinct objects (the
+  // interleaved schedule needs that); 256 x 256 tiles one array of two.
+  constexpr bool kSplit = BM != 256;
+  __shared__ uint4 smem[kSplit ? kStage : 2 * kStage];
+  __shared__ uint4 smem_b[kSplit ? kStage : 1];
+  uint4* const stage1 = kSplit ? smem_b : smem + kStage;
 
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -478,9 +525,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   const int L = lane & 31, half = lane >> 5;
   f32x16 acc[MB][NB];
   if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
-    mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);
+    mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);  // both stages in smem (kSplit is false)
   else
-    mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256)>(p, smem, m0, n0, kt0, kt1, acc);
+    mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256), kSplit && MG_GEMM_INTERLEAVE>(p, smem, stage1, m0, n0, kt0, kt1,
+                                                                                acc);
 
   // Epilogue, one 32-row block of the wave's (BM/2) x (BN/2) region at a
   // time: the accumulators go to a wave-private LDS block and come back as
@@ -494,7 +542,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int CQ = RB / 16;                // 16-byte chunks per row
   constexpr int EPC = 16 / int(sizeof(S));   // elements per chunk
   constexpr int RPI = 64 / CQ;               // rows per read instruction
-  static_assert(32 * RB * WM * WN <= int(sizeof(smem)), "staging fits in the operand stages");
+  static_assert(32 * RB * WM * WN <= int(sizeof(smem)), "staging fits in the first operand stage");
   unsigned char* stage = reinterpret_cast<unsigned char*>(smem) + wave * 32 * RB;
   const int row0 = m0 + wm * (BM / WM), col0 = n0 + wn * NW;
   // A lane reads back the same columns for every row: col0 + (lane % CQ) * EPC.
@@ -507,8 +555,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   // The GELU gradient's pre-activations (bf16) of block i+1 stream straight
   // into LDS (unswizzled [32 rows][NW]) while block i is written out.
   constexpr int PB = 32 * NW * 2;  // bytes per pre-activation block and wave
-  static_assert(EPI != EPI_GELU_GRAD || 32 * RB * WM * WN + 2 * PB * WM * WN <= int(sizeof(smem)), "aux staging");
-  unsigned char* pstage = reinterpret_cast<unsigned char*>(smem) + 32 * RB * WM * WN + wave * 2 * PB;
+  static_assert(EPI != EPI_GELU_GRAD || 2 * PB * WM * WN <= kStage * 16, "aux staging");
+  unsigned char* pstage = reinterpret_cast<unsigned char*>(stage1) + wave * 2 * PB;
   Operand oaux;
   if constexpr (EPI == EPI_GELU_GRAD) oaux = make_operand(p.aux, p.ldaux, p.aux_span);
   auto fetch_pre = [&](int i) {
@@ -632,7 +680,7 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int L = lane & 31, half = lane >> 5;
   f32x16 acc[MB][NB];
-  mainloop<BM, BN, WM, WN, true, true, false>(p, smem, m0, 0, 0, (p.K + BK - 1) / BK, acc);
+  mainloop<BM, BN, WM, WN, true, true, false>(p, smem, smem + kStage, m0, 0, 0, (p.K + BK - 1) / BK, acc);
 
   // logits tile [64][256] fp32 in LDS, 16-byte chunk c of row r at c ^ (r & 63)
   float* tile = reinterpret_cast<float*>(smem);
