@@ -523,8 +523,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
     mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);  // both stages in smem (kSplit is false)
   else
-    mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256), kSplit>(p, smem, stage1, m0, n0, kt0, kt1,
-                                                                                acc);
+    mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256), kSplit>(p, smem, stage1, m0, n0, kt0, kt1, acc);
 
   // Epilogue, one 32-row block of the wave's (BM/2) x (BN/2) region at a
   // time: the accumulators go to a wave-private LDS block and come back as
