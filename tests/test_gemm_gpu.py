@@ -97,7 +97,8 @@ def test_gemm_epilogues():
 
 
 def test_gemm_accumulate_and_split():
-    """fp32 dW-shaped product (long K): split along K with atomics; accumulate adds to C."""
+    """fp32 dW-shaped product (long K, 79 k-tiles): split along K into slices
+    of an odd k-tile count, summed by the reduction pass; accumulate adds to C."""
     from gruboros_amd.gemm import linear_dw
 
     gen = torch.Generator().manual_seed(9)
@@ -115,7 +116,7 @@ def test_gemm_accumulate_and_split():
 
 def test_gemm_deterministic_flag():
     """Weight-gradient product with and without the split along K (partials
-    summed in split order by the tile's last workgroup): both forms repeat bit
+    summed in split order by a separate reduction pass): both forms repeat bit
     for bit, also with other shapes run on the same workspace in between, and
     they agree with each other."""
     from gruboros_amd.gemm import linear_dw
