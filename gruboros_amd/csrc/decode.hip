@@ -143,11 +143,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
 
   // 1. the B input rows, as bf16, into LDS (rows B..BP-1 zero)
   if constexpr (MODE == FF2) {
-    for (int i = tid; i < BP * (K / 8); i += kThreads) {
-      const int b = i / (K / 8), c8 = i % (K / 8);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (b < a.B) v = *reinterpret_cast<const uint4*>(a.act + static_cast<int64_t>(b) * K + c8 * 8);
-      reinterpret_cast<uint4*>(s_in)[i] = v;
+    // kBatch 16-byte loads per thread in flight before their LDS stores (a
+    // load-store pair per iteration would wait out one memory latency each)
+    constexpr int kBatch = 8;
+    const int n16 = BP * (K / 8);
+    for (int i0 = 0; i0 < n16; i0 += kBatch * kThreads) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = i0 + u * kThreads + tid;
+        const int b = i / (K / 8), c8 = i % (K / 8);
+        v[u] = make_uint4(0, 0, 0, 0);
+        if (i < n16 && b < a.B) v[u] = *reinterpret_cast<const uint4*>(a.act + static_cast<int64_t>(b) * K + c8 * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = i0 + u * kThreads + tid;
+        if (i < n16) reinterpret_cast<uint4*>(s_in)[i] = v[u];
+      }
     }
   } else {
     // RMSNorm over D = K: the rows are read once into registers (column

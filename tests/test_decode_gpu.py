@@ -37,11 +37,13 @@ def _model(dim=256, depth=2, seed=0):
     return m.to(DEV).eval()
 
 
-@pytest.mark.parametrize("B", [1, 3, 8])
-def test_decoder_matches_one_token_model_calls(B):
+@pytest.mark.parametrize("B,dim", [(1, 256), (3, 256), (8, 256), (5, 1024), (8, 1024)])
+def test_decoder_matches_one_token_model_calls(B, dim):
+    """dim 1024 gives the FeedForward width 4096 of the cfg3 model (the
+    second product stages its [B, 4096] input in more than one batch of loads)."""
     from gruboros_amd.decode import Decoder
 
-    m = _model()
+    m = _model(dim=dim)
     gen = torch.Generator(device=DEV).manual_seed(B)
     prompt = torch.randint(0, 256, (B, 17), device=DEV, generator=gen)
     dec = Decoder(m, B)
@@ -55,7 +57,7 @@ def test_decoder_matches_one_token_model_calls(B):
             got = dec.step(tok)
             e_l = _rel(got, logits[:, -1])
             e_h = max(_rel(a, b) for a, b in zip(dec.hiddens(), hid))
-            print(f"B={B} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
+            print(f"B={B} dim={dim} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
             assert e_l < 1e-2 and e_h < 1e-2
 
 
