@@ -66,6 +66,22 @@ __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to
 // with the total of value (l >> (6 - log2 N)); 64 / N lanes hold each total.
 // (Stages are template-unrolled so every array index is a constant: a
 // runtime index would turn into compare/select chains over the registers.)
+// The partner of the exchange at bit o only has to differ from the lane in
+// bit o and agree in the bits above it: o = 32, 16 use lane ^ o (through
+// LDS's permute network), o = 8, 4, 2, 1 register-speed DPP moves within a
+// row of 16 lanes: lane ^ 15 (row mirror), lane ^ 7 (half-row mirror),
+// lane ^ 2 and lane ^ 1 (quad permutes). The partners across all stages
+// still span every lane, so each total covers the whole wave.
+template <int o>
+__device__ __forceinline__ float partner(float x) {
+  if constexpr (o >= 16) {
+    return __shfl_xor(x, o, 64);
+  } else {
+    constexpr int ctrl = o == 8 ? 0x140 : o == 4 ? 0x141 : o == 2 ? 0x4E : 0xB1;  // mirror, half mirror, [2301], [1032]
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+  }
+}
+
 template <int n, int o, int N>
 __device__ __forceinline__ void wave_sum_stage(float (&v)[N], int lane) {
   if constexpr (o >= 1) {
@@ -74,11 +90,11 @@ __device__ __forceinline__ void wave_sum_stage(float (&v)[N], int lane) {
 #pragma unroll
       for (int i = 0; i < n / 2; ++i) {
         const float lo = v[i], hi = v[i + n / 2];
-        v[i] = (up ? hi : lo) + __shfl_xor(up ? lo : hi, o, 64);
+        v[i] = (up ? hi : lo) + partner<o>(up ? lo : hi);
       }
       wave_sum_stage<n / 2, o / 2, N>(v, lane);
     } else {
-      v[0] += __shfl_xor(v[0], o, 64);
+      v[0] += partner<o>(v[0]);
       wave_sum_stage<1, o / 2, N>(v, lane);
     }
   }
