@@ -125,9 +125,28 @@ __device__ __forceinline__ float stream_at(const Args& a, int b, int c) {
   return x;
 }
 
+// The same for columns c .. c + 3 (c a multiple of 4; rows are 16-byte aligned).
+template <int SRC>
+__device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
+  f4 x;
+  if constexpr (SRC == SRC_TOKENS) {
+    const int64_t t = min(max(a.tokens[b], int64_t(0)), static_cast<int64_t>(a.V - 1));
+    x = io4<float>::load(a.emb + t * a.D + c);
+  } else {
+    x = io4<float>::load(a.x_in + static_cast<int64_t>(b) * a.D + c);
+  }
+  if constexpr (SRC == SRC_X_PENDING) {
+    const f4 p = io4<bf16_t>::load(a.pending + static_cast<int64_t>(b) * a.D + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x.v[e] += p.v[e];
+  }
+  return x;
+}
+
 // MODE: which step; BP: batch rows (padded); R: output rows per wave;
 // NC: 512-element chunks of the reduction a lane covers (K <= 512 NC); CPT:
-// columns per thread in the norm prologue (D <= 256 CPT).
+// columns per thread in the norm prologue (D <= 256 CPT; a multiple of 4, or
+// 1 where there is no norm).
 template <int MODE, int SRC, int BP, int R, int NC, int CPT>
 __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
   extern __shared__ uint4 lds[];
@@ -179,20 +198,25 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
       }
     }
   } else {
-    // RMSNorm over D = K: the rows are read once into registers (column
-    // tid + 256 i), the sum of squares reduced over the workgroup, then
-    // y = x r w goes to LDS
+    // RMSNorm over D = K: the rows are read once into registers (columns
+    // 4 (tid + 256 q) .. +3 in one 16-byte load per row and q), the sum of
+    // squares reduced over the workgroup, then y = x r w goes to LDS
+    static_assert(CPT % 4 == 0, "whole 4-column groups per thread");
+    constexpr int Q = CPT / 4;
     float xr[BP][CPT];
     float ss[BP];
 #pragma unroll
     for (int b = 0; b < BP; ++b) {
       ss[b] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kThreads;
-        const float x = stream_at<SRC>(a, min(b, a.B - 1), min(c, K - 1));  // unconditional load
-        xr[b][i] = (b < a.B && c < K) ? x : 0.0f;
-        ss[b] += xr[b][i] * xr[b][i];
+      for (int q = 0; q < Q; ++q) {
+        const int c = 4 * (tid + q * kThreads);
+        const f4 x = stream4_at<SRC>(a, min(b, a.B - 1), min(c, K - 4));  // unconditional load
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xr[b][4 * q + e] = (b < a.B && c < K) ? x.v[e] : 0.0f;
+          ss[b] += xr[b][4 * q + e] * xr[b][4 * q + e];
+        }
       }
     }
     {
@@ -209,12 +233,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * kThreads;
+    for (int q = 0; q < Q; ++q) {
+      const int c = 4 * (tid + q * kThreads);
       if (c < K) {
-        const float w = a.norm_w[c];
+        const f4 w = io4<float>::load(a.norm_w + c);
 #pragma unroll
-        for (int b = 0; b < BP; ++b) s_in[b * K + c] = f32_to_bf16(xr[b][i] * s_rstd[b] * w);
+        for (int b = 0; b < BP; ++b) {
+          f4 y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y.v[e] = xr[b][4 * q + e] * s_rstd[b] * w.v[e];
+          io4<bf16_t>::store(s_in + b * K + c, y);
+        }
       }
     }
   }
@@ -330,7 +359,9 @@ extern "C" int mg_decode_mingru(int B, int D, const int64_t* tokens, const float
   if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
   if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !x_out || !norm_w || !w_hg || !state)
     return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
-  if (!aligned(w_hg, 16)) return fail(MG_ERR_ARG, "%s: weight not 16-byte aligned", fn);
+  if (!aligned(w_hg, 16) || !aligned(norm_w, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
+      (pending && !aligned(pending, 8)))
+    return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
   decode::Args a{};
   a.B = B; a.D = D; a.K = D; a.rows = 2 * D; a.V = V;
   a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
@@ -348,8 +379,8 @@ extern "C" int mg_decode_ff(int B, int D, int F, const float* x, const float* no
   if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
   if (int rc = decode::check_shape(fn, B, F, 8192)) return rc;
   if (!x || !norm_w || !w1 || !b1 || !act || !w2 || !b2 || !pending_out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
-  if (F % 4 || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(act, 16))
-    return fail(MG_ERR_ARG, "%s: F %% 4, 16-byte weights and act required", fn);
+  if (F % 4 || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(act, 16) || !aligned(x, 16) || !aligned(norm_w, 16))
+    return fail(MG_ERR_ARG, "%s: F %% 4, 16-byte weights, act, x and norm weight required", fn);
   hipStream_t st = static_cast<hipStream_t>(stream);
   decode::Args a{};
   a.B = B; a.D = D; a.K = D; a.rows = F;
@@ -368,7 +399,8 @@ extern "C" int mg_decode_head(int B, int D, int V, const float* x_in, const void
   const char* fn = "mg_decode_head";
   if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
   if (V < 1 || !x_in || !norm_w || !w_out || !logits) return fail(MG_ERR_ARG, "%s: bad argument", fn);
-  if (!aligned(w_out, 16)) return fail(MG_ERR_ARG, "%s: weight not 16-byte aligned", fn);
+  if (!aligned(w_out, 16) || !aligned(x_in, 16) || !aligned(norm_w, 16) || (pending && !aligned(pending, 8)))
+    return fail(MG_ERR_ARG, "%s: weight, x_in or norm weight not 16-byte aligned, or pending not 8-byte aligned", fn);
   decode::Args a{};
   a.B = B; a.D = D; a.K = D; a.rows = V;
   a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending); a.norm_w = norm_w;

@@ -312,7 +312,8 @@ int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
  *     W_out^T) (W_out bf16 [V, D], logits bf16 [B, V]).
  * RMSNorm: x / sqrt(mean(x^2) + eps). D <= 2048, F <= 8192, both multiples
  * of 8, with the batch (rounded up to 1, 2, 4 or 8) times max(D, F) bf16
- * values within 64 KiB; weights 16-byte aligned.
+ * values within 64 KiB; weights, act, x / x_in / emb and norm_w 16-byte
+ * aligned, pending 8-byte aligned.
  * ---------------------------------------------------------------------- */
 int mg_decode_mingru(int B, int D, const int64_t* tokens, const float* emb, int V, const float* x_in,
                      const void* pending, float* x_out, const float* norm_w, const void* w_hg,
