@@ -83,6 +83,14 @@ def test_decode_argument_errors(L):
     assert L.mg_decode_ff(8, 64, 8192, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
     assert L.mg_decode_mingru(1, 64, 16, None, 256, None, None, 16, 16, 16, 16, eps, None) == 1  # no embedding
     assert L.mg_decode_head(1, 64, 0, 16, None, 16, 16, 16, eps, None) == 1
+    # the norm prologue reads 16-byte groups of x / emb / norm weight and 8 bytes of pending:
+    # misaligned pointers are refused before any launch
+    assert L.mg_decode_mingru(1, 64, None, None, 0, 20, None, 16, 16, 16, 16, eps, None) == 1  # x_in
+    assert L.mg_decode_mingru(1, 64, None, None, 0, 16, 20, 16, 16, 16, 16, eps, None) == 1  # pending
+    assert L.mg_decode_mingru(1, 64, 16, 24, 256, None, None, 16, 16, 16, 16, eps, None) == 1  # emb
+    assert L.mg_decode_ff(1, 64, 256, 24, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1  # x
+    assert L.mg_decode_head(1, 64, 256, 16, None, 24, 16, 16, eps, None) == 1  # norm weight
+    assert b"aligned" in L.mg_last_error()
 
 
 def test_product_refuses_cpu_tensors():
