@@ -96,6 +96,35 @@ def test_gemm_epilogues():
     assert _rel(dx, ref) < 4e-3
 
 
+def test_gemm_epilogues_256_tiles():
+    """The bias, bias+GELU and GELU-gradient epilogues of the 256 x 256 kernels
+    (chosen once a product has at least one 256 x 256 tile per CU): ragged M,
+    against torch's fp32 product of the same bf16 inputs on the GPU."""
+    from gruboros_amd.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD, KCONTIG, MNCONTIG, gemm
+
+    g = torch.Generator(device=DEV).manual_seed(21)
+    M, N, K = 4133, 4096, 192  # 17 x 16 = 272 tiles of 256 x 256
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=DEV, generator=g) * 0.1).to(torch.bfloat16)
+    bias = torch.randn(N, device=DEV, generator=g)
+    pre_ref = x.float() @ w.float().t() + bias
+    y = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(x, KCONTIG, w, KCONTIG, M, N, K, y, epilogue=EPI_BIAS, bias=bias)
+    assert _rel(y, pre_ref) < 4e-3
+    pre = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(x, KCONTIG, w, KCONTIG, M, N, K, y, epilogue=EPI_BIAS_GELU, bias=bias, aux=pre)
+    assert _rel(pre, pre_ref) < 4e-3
+    assert _rel(y, torch.nn.functional.gelu(pre.float())) < 4e-3
+    # GELU gradient: dX = (dY W) * gelu'(pre), dY [M, N], W [N, K] read MN-contiguous
+    dy = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    w2 = (torch.randn(K, N, device=DEV, generator=g) * 0.1).to(torch.bfloat16)
+    dx = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(dy, KCONTIG, w2, MNCONTIG, M, N, K, dx, epilogue=EPI_GELU_GRAD, aux=pre)
+    p = pre.float().requires_grad_(True)
+    torch.nn.functional.gelu(p).backward(torch.ones_like(p))
+    assert _rel(dx, (dy.float() @ w2.float()) * p.grad) < 4e-3
+
+
 def test_gemm_accumulate_and_split():
     """fp32 dW-shaped product (long K, 79 k-tiles): split along K into slices
     of an odd k-tile count, summed by the reduction pass; accumulate adds to C."""
