@@ -13,6 +13,7 @@ from .build import LIB_PATH
 
 MG_F32 = 0
 MG_BF16 = 1
+MG_ERR_STALL = 5
 
 _c_int, _c_i64, _c_size, _vp, _fp = (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p,
                                      ctypes.c_void_p)
@@ -23,7 +24,8 @@ SIGNATURES = {
     "mg_last_error": (ctypes.c_char_p, []),
     "mg_scan_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "mg_scan_workspace_init": (_c_int, [_vp, _c_size, _c_int, _c_int, _c_int, _vp]),
-    "mg_scan_workspace_release": (_c_int, [_vp]),
+    "mg_scan_workspace_set_max_polls": (_c_int, [_vp, ctypes.c_uint32, _vp]),
+    "mg_scan_workspace_check": (_c_int, [_vp, _vp]),
     "mg_decode_mingru": (_c_int, [_c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                                   _vp]),
     "mg_decode_ff": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
@@ -32,9 +34,12 @@ SIGNATURES = {
     "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
                              _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
     "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp,
-                             _vp, _c_i64, _c_i64, _fp, _vp, _vp, _fp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
-    "mg_add_rmsnorm_fwd": (_c_int, [_fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int,
+                             _vp, _c_i64, _c_i64, _fp, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _c_int, _c_int, _vp,
+                             _c_size, _vp]),
+    "mg_add_rmsnorm_fwd": (_c_int, [_fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _vp, _c_i64, _fp, _c_i64, _c_int,
                                     ctypes.c_float, _vp]),
+    "mg_split_hilo": (_c_int, [_fp, _c_i64, _c_i64, _c_int, _vp, _c_i64, _vp]),
+    "mg_round_bf16_sr": (_c_int, [_fp, _c_i64, _vp, ctypes.c_uint32, _vp]),
     "mg_add_rmsnorm_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_add_rmsnorm_bwd": (_c_int, [_fp, _fp, _fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int, _vp,
                                     _c_size, _vp]),
@@ -48,7 +53,7 @@ SIGNATURES = {
                                          ctypes.c_float, _vp]),
     "mg_column_sum_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_column_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_int, _fp, _vp, _c_size, _vp]),
-    "mg_gelu_bwd": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_size, _vp]),
+    "mg_gelu_bwd": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -89,7 +94,8 @@ def dtype_code(dt: torch.dtype) -> int:
         return MG_F32
     if dt == torch.bfloat16:
         return MG_BF16
-    raise MingruHipError(f"unsupported dtype {dt} (float32 and bfloat16 are supported)")
+    raise MingruHipError(f"unsupported dtype {dt}: the MI355X kernels take float32 and bfloat16 "
+                         "(cast a float16 model with .to(torch.bfloat16) instead)")
 
 
 def ptr(t):

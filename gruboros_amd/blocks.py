@@ -1,0 +1,210 @@
+"""Block-level autograd functions of the bf16 minLM training path.
+
+Reference mingru/minLM.py:107-149: per layer
+    x = minGRU(RMSNorm(x)) + x        (:119-125)
+    x = FeedForward(RMSNorm(x)) + x   (:127-130)
+then the final RMSNorm, the logits and the cross-entropy (:137-149).
+
+Here each of those three pieces is one torch.autograd.Function (bf16
+activations over fp32 master weights):
+
+  MinGRUBlock   x1 = x + pending; n = RMSNorm(x1) as a hi/lo pair;
+                hg = [n W_h^T (fp32-accurate) | n W_g^T]; h = scan(hg) in fp32;
+                out = h, or to_out(h) (fp32-accurate) when expansion != 1.
+  FFBlock       x2 = x1 + out; n2 = RMSNorm(x2); pending = FeedForward(n2) (bf16).
+  FinalNormCE   embed = RMSNorm(x + pending); mean cross-entropy of
+                embed W_out^T (streaming loss kernel).
+
+Why blocks rather than one Function per op: inside a block the gradients
+of the normalized inputs and of the GELU input are kept in fp32 (the
+input-gradient products write fp32, which the norm and GELU backward
+kernels read), and every gradient stored in bf16 (dlogits, the FeedForward
+output's gradient, dgate/dhidden, dpre) is rounded stochastically by the
+kernel that writes it. An autograd boundary at a bf16 tensor would cast its
+incoming gradient to bf16 with round-to-nearest, whose errors at a near-
+uniform softmax repeat across the rows of a label and add up in the weight
+gradients (measured on the fp64 restatement: 4-7% at the cfg3 row count
+against 0.5% for this arrangement). The gradients crossing block boundaries
+are the fp32 residual stream's, the fp32 minGRU output's, and the bf16
+FeedForward output's (stochastically rounded by the next block's norm).
+"""
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from . import gemm
+from .linear import bf16_copy, bf16_pair, column_sum, gelu_backward
+from .norm import FP32_EPS  # noqa: F401  (the kernels' eps; norm._fwd passes it)
+from .norm import _bwd as _norm_bwd
+from .norm import _fwd as _norm_fwd
+from .scan import _launch_bwd as _scan_bwd
+from .scan import _launch_fwd as _scan_fwd
+
+BF16 = torch.bfloat16
+
+
+class MinGRUBlock(torch.autograd.Function):
+    """(x, pending) -> (x1 = x + pending, out, h_last); see the module docstring.
+
+    x: fp32 [B, T, D] residual stream; pending: bf16 [B, T, D] (the previous
+    FeedForward's output, not yet added) or None; w_norm fp32 [D]; w_hg fp32
+    master [2 Di, D]; h0 fp32 [B, Di] or None; w_to fp32 master [D, Di] or None.
+    out: fp32 [B, T, Di] (h) or [B, T, D] (to_out(h)); h_last fp32 [B, 1, Di]."""
+
+    @staticmethod
+    def forward(ctx, x, pending, w_norm, w_hg, h0, w_to):
+        ctx.set_materialize_grads(False)
+        B, T, D = x.shape
+        N, Di = B * T, w_hg.shape[0] // 2
+        x2 = x.reshape(N, D)
+        p2 = pending.reshape(N, D) if pending is not None else None
+        x_out, n, rstd, pair = _norm_fwd(x2, p2, w_norm, BF16, with_lo=True)
+        xn = x_out if x_out is not None else x2
+        whp, whb = bf16_pair(w_hg), bf16_copy(w_hg)
+        hg = torch.empty(N, 2 * Di, dtype=BF16, device=x.device)
+        gemm.linear_fwd_hilo(pair, whp[:Di], hg[:, :Di], D)                    # minGRU.py:45, hidden half
+        gemm.gemm(n, gemm.KCONTIG, whb[Di:], gemm.KCONTIG, N, Di, D, hg[:, Di:])  # gate half
+        hg3 = hg.view(B, T, 2 * Di)
+        h, h_last, _ = _scan_fwd(hg3[..., :Di], hg3[..., Di:], h0, torch.float32)   # minGRU.py:47-69
+        saved = [xn, w_norm, rstd, pair, hg, h, h0, whb]
+        if w_to is not None:                                                   # minGRU.py:71
+            h_pair = gemm.split_hilo(h.view(N, Di))
+            out = torch.empty(N, D, dtype=torch.float32, device=x.device)
+            gemm.linear_fwd_hilo(h_pair, bf16_pair(w_to), out, Di)
+            out = out.view(B, T, D)
+            saved += [h_pair, bf16_copy(w_to)]
+        else:
+            out = h
+        ctx.save_for_backward(*saved)
+        ctx.dims = (B, T, D, Di)
+        ctx.has_pending, ctx.has_to = pending is not None, w_to is not None
+        x1 = x_out.view(B, T, D) if x_out is not None else x.view_as(x)
+        return x1, out, h_last
+
+    @staticmethod
+    def backward(ctx, dx1, dout, dh_last):
+        B, T, D, Di = ctx.dims
+        N = B * T
+        saved = ctx.saved_tensors
+        xn, w_norm, rstd, pair, hg, h, h0, whb = saved[:8]
+        dev = xn.device
+        dW_to = None
+        if dout is None:
+            dh = None
+        elif ctx.has_to:
+            h_pair, wtb = saved[8:10]
+            dob = gemm.round_bf16_sr(dout.reshape(N, D).contiguous().float())
+            dh = gemm.linear_dx(dob, wtb, out_dtype=torch.float32).view(B, T, Di)
+            if ctx.needs_input_grad[5]:
+                dW_to = gemm.linear_dw(dob, h_pair[:, :Di])
+        else:
+            dh = dout.float()
+        dhg = torch.empty(N, 2 * Di, dtype=BF16, device=dev)
+        hg3, dhg3 = hg.view(B, T, 2 * Di), dhg.view(B, T, 2 * Di)
+        want_dh0 = h0 is not None and ctx.needs_input_grad[4]
+        if dh is None and dh_last is None:
+            dhg.zero_()
+            dh0 = torch.zeros_like(h0) if want_dh0 else None
+        else:
+            dh0 = _scan_bwd(hg3[..., :Di], hg3[..., Di:], h0, h, None, dh, dh_last, dhg3[..., :Di], dhg3[..., Di:],
+                            want_dh0)
+        dn = gemm.linear_dx(dhg, whb, out_dtype=torch.float32)     # fp32: no rounding of n's gradient
+        dW_hg = gemm.linear_dw(dhg, pair[:, :D]) if ctx.needs_input_grad[3] else None
+        dres = dx1.reshape(N, D) if dx1 is not None else None
+        dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, dn, dres, True, BF16, ctx.has_pending)
+        return (dx.view(B, T, D), dpend.view(B, T, D) if dpend is not None else None,
+                dw_norm if ctx.needs_input_grad[2] else None, dW_hg,
+                dh0.reshape(h0.shape) if dh0 is not None else None, dW_to)
+
+
+class FFBlock(torch.autograd.Function):
+    """(x1, out) -> (x2 = x1 + out, pending = FeedForward(RMSNorm(x2))).
+
+    x1 fp32 [B, T, D]; out fp32 [B, T, D] (the minGRU branch); FeedForward =
+    Linear(D, F) -> GELU -> Linear(F, D) (reference mingru/minLM.py:17-23)
+    with fp32 masters; pending bf16."""
+
+    @staticmethod
+    def forward(ctx, x1, out, w_norm, w1, b1, w2, b2):
+        ctx.set_materialize_grads(False)
+        B, T, D = x1.shape
+        N = B * T
+        x2, n2, rstd, _ = _norm_fwd(x1.reshape(N, D), out.reshape(N, D), w_norm, BF16)
+        w1b, w2b = bf16_copy(w1), bf16_copy(w2)
+        pre = F.linear(n2, w1b, bf16_copy(b1))
+        act = F.gelu(pre)
+        pend = F.linear(act, w2b, bf16_copy(b2))
+        ctx.save_for_backward(x2, w_norm, rstd, n2, pre, act, w1b, w2b)
+        ctx.dims = (B, T, D)
+        return x2.view(B, T, D), pend.view(B, T, D)
+
+    @staticmethod
+    def backward(ctx, dx2, dpend):
+        B, T, D = ctx.dims
+        N = B * T
+        x2, w_norm, rstd, n2, pre, act, w1b, w2b = ctx.saved_tensors
+        dres = dx2.reshape(N, D) if dx2 is not None else None
+        dW1 = db1 = dW2 = db2 = None
+        if dpend is None:
+            dn2 = torch.zeros(N, D, dtype=torch.float32, device=x2.device)
+        else:
+            dp = dpend.reshape(N, D)
+            if dp.dtype != BF16 or not dp.is_contiguous():
+                dp = dp.to(BF16).contiguous()
+            dact = gemm.linear_dx(dp, w2b, out_dtype=torch.float32)    # fp32 into the GELU backward
+            dpre, db1 = gelu_backward(dact, pre)                        # bf16, stochastically rounded
+            dW2 = gemm.linear_dw(dp, act)
+            db2 = column_sum(dp)
+            dn2 = gemm.linear_dx(dpre, w1b, out_dtype=torch.float32)   # fp32 into the norm backward
+            dW1 = gemm.linear_dw(dpre, n2)
+        dx1, dout, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, True)
+        return dx1.view(B, T, D), dout.view(B, T, D), dw_norm, dW1, db1, dW2, db2
+
+
+class FinalNormCE(torch.autograd.Function):
+    """mean CE(RMSNorm(x + pending) W_out^T, labels) (reference mingru/minLM.py:137-149)
+    for V <= 256 classes on the streaming loss kernel (logits never in memory).
+    x fp32 [B, T, D], pending bf16 [B, T, D] or None, labels int64 [B, T]."""
+
+    @staticmethod
+    def forward(ctx, x, pending, w_norm, w_out, labels):
+        B, T, D = x.shape
+        N = B * T
+        V = w_out.shape[0]
+        x2 = x.reshape(N, D)
+        x_out, embed, rstd, _ = _norm_fwd(x2, pending.reshape(N, D) if pending is not None else None, w_norm, BF16)
+        xn = x_out if x_out is not None else x2
+        wob = bf16_copy(w_out)
+        L = _lib.lib()
+        dl = torch.empty(N, V, dtype=BF16, device=x.device)
+        part = torch.empty(L.mg_logits_cross_entropy_partials(N), dtype=torch.float32, device=x.device)
+        lab = labels.reshape(-1).contiguous()
+        _lib.check(L.mg_logits_cross_entropy(_lib.ptr(embed), embed.stride(0), _lib.ptr(wob), wob.stride(0),
+                                             _lib.ptr(lab), _lib.ptr(dl), V, _lib.ptr(part), None, N, D, V, 1.0 / N,
+                                             _lib.stream_of(embed)), "mg_logits_cross_entropy")
+        ctx.save_for_backward(xn, w_norm, rstd, embed, dl, wob)
+        ctx.dims = (B, T, D)
+        ctx.has_pending = pending is not None
+        return part.sum() / N
+
+    @staticmethod
+    def backward(ctx, g):
+        B, T, D = ctx.dims
+        xn, w_norm, rstd, embed, dl, wob = ctx.saved_tensors
+        de = gemm.linear_dx(dl, wob, out_dtype=torch.float32)         # fp32 into the norm backward
+        dW = gemm.linear_dw(dl, embed) if ctx.needs_input_grad[3] else None
+        de.mul_(g)  # upstream scale (1 / grad_accum in the reference loop), in fp32; no host sync
+        if dW is not None:
+            dW.mul_(g)
+        dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, de, None, True, BF16, ctx.has_pending)
+        return (dx.view(B, T, D), dpend.view(B, T, D) if dpend is not None else None,
+                dw_norm if ctx.needs_input_grad[2] else None, dW, None)
+
+
+def supported(model):
+    """Whether the block path applies: bf16 activations over fp32 masters, no
+    conv, no dropout, and a loss head the streaming kernel takes."""
+    D = model.dim
+    V = model.to_logits.weight.shape[0]
+    return (all(conv is None and dropout is None for conv, _, _, _, _, dropout in model.layers)
+            and model.token_emb.weight.dtype == torch.float32 and D % 8 == 0 and V % 8 == 0 and V <= 256)

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void ce_kernel(const Tl* __restrict__ log
         f4 d;
 #pragma unroll
         for (int j = 0; j < 4; ++j) d.v[j] = (x[i].v[j] * inv_s - (col + j == lab ? 1.0f : 0.0f)) * scale;
-        io4<Td>::store(dlogits + row * V + col, d);
+        io4<Td>::store_grad(dlogits + row * V + col, d, static_cast<uint32_t>(row * V + col), 0x8d4au);
       }
     }
   }

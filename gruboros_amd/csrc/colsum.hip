@@ -4,7 +4,8 @@
 // partial rows that the RMSNorm weight gradient also uses.
 //
 //   mg_column_sum:   out[c] = sum_n x[n, c]                        (x bf16 / fp32)
-//   mg_gelu_bwd:     dpre[n, c] = bf16(dh[n, c] gelu'(pre[n, c]))
+//   mg_gelu_bwd:     dpre[n, c] = bf16(dh[n, c] gelu'(pre[n, c]))  (dh fp32 or
+//                                 bf16; dpre rounded stochastically, mg_common.h)
 //                    dbias[c]   = sum_n dpre[n, c]   (of the rounded values,
 //                                 as summing the bf16 tensor gives)
 // Both make one pass over the rows: workgroup (cb, rg) owns 2048 columns
@@ -68,7 +69,8 @@ __global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ 
   reinterpret_cast<float4*>(o)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
-__global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const bf16_t* __restrict__ dh, int64_t ld_dh,
+template <typename Tg>
+__global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const Tg* __restrict__ dh, int64_t ld_dh,
                                                             const bf16_t* __restrict__ pre, int64_t ld_pre,
                                                             bf16_t* __restrict__ dpre, int64_t ld_out, int64_t N,
                                                             int C, float* __restrict__ part) {
@@ -77,12 +79,14 @@ __global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const bf16_t* __rest
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {  // not unrolled: measured fastest
     float g[8], x[8];
-    load8<bf16_t>(dh + n * ld_dh + c, g);
+    load8<Tg>(dh + n * ld_dh + c, g);
     load8<bf16_t>(pre + n * ld_pre + c, x);
     uint32_t w[4];
+    const uint32_t idx = static_cast<uint32_t>(n * C + c);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      w[q] = pack_bf16x2(g[2 * q] * gelu_grad(x[2 * q]), g[2 * q + 1] * gelu_grad(x[2 * q + 1]));
+      w[q] = pack_bf16x2_sr(g[2 * q] * gelu_grad(x[2 * q]), g[2 * q + 1] * gelu_grad(x[2 * q + 1]), idx + 2 * q,
+                            0xaf6cu);
       acc[2 * q] += __uint_as_float(w[q] << 16);
       acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
     }
@@ -167,10 +171,12 @@ extern "C" int mg_column_sum(int dtype, const void* x, int64_t ld, int64_t N, in
   return check_launch(fn);
 }
 
-extern "C" int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre, void* dpre, int64_t ld_out,
-                           float* dbias, int64_t N, int C, void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int mg_gelu_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre, void* dpre,
+                           int64_t ld_out, float* dbias, int64_t N, int C, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   const char* fn = "mg_gelu_bwd";
   if (!dh || !pre || !dpre) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (dh_dtype != MG_F32 && dh_dtype != MG_BF16) return fail(MG_ERR_DTYPE, "%s: dh dtype %d unsupported", fn, dh_dtype);
   if (N < 1 || C < 8 || C % 8 || ld_dh < C || ld_pre < C || ld_out < C || ld_dh % 8 || ld_pre % 8 || ld_out % 8)
     return fail(MG_ERR_ARG, "%s: bad shape N=%lld C=%d", fn, (long long)N, C);
   if (!aligned(dh, 16) || !aligned(pre, 16) || !aligned(dpre, 16) || (dbias && !aligned(dbias, 16)))
@@ -181,8 +187,14 @@ extern "C" int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = dbias ? static_cast<float*>(workspace) : nullptr;
   const dim3 grid((C + colsum::kCols - 1) / colsum::kCols, RG);
-  hipLaunchKernelGGL(colsum::gelu_bwd_kernel, grid, dim3(colsum::kThreads), 0, st, static_cast<const bf16_t*>(dh),
-                     ld_dh, static_cast<const bf16_t*>(pre), ld_pre, static_cast<bf16_t*>(dpre), ld_out, N, C, part);
+  if (dh_dtype == MG_BF16)
+    hipLaunchKernelGGL(colsum::gelu_bwd_kernel<bf16_t>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const bf16_t*>(dh), ld_dh, static_cast<const bf16_t*>(pre), ld_pre,
+                       static_cast<bf16_t*>(dpre), ld_out, N, C, part);
+  else
+    hipLaunchKernelGGL(colsum::gelu_bwd_kernel<float>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const float*>(dh), ld_dh, static_cast<const bf16_t*>(pre), ld_pre,
+                       static_cast<bf16_t*>(dpre), ld_out, N, C, part);
   if (dbias) launch_reduce_partials(part, RG, C, dbias, st);
   return check_launch(fn);
 }

@@ -1,0 +1,71 @@
+// fp32 -> bf16 hi/lo pairs, the operand form of mg_gemm's MG_GEMM_HILO
+// products: out[r, c] = hi = bf16(x[r, c]), out[r, cols + c] =
+// bf16(x[r, c] - hi). hi + lo equals x to ~2^-16 relative (x - hi is exact in
+// fp32). Used for the weights of the accurate products (once per weight
+// update) and for the fp32 scan output entering to_out (reference
+// mingru/minGRU.py:71).
+
+#include "mg_common.h"
+
+namespace mg {
+namespace convert {
+
+__global__ __launch_bounds__(256) void split_hilo_kernel(const float* __restrict__ x, int64_t ldx, int64_t rows,
+                                                         int cols, bf16_t* __restrict__ out, int64_t ldo) {
+  const int q = cols / 4;  // 4-column groups per row
+  const int64_t n = rows * q;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / q;
+    const int c = static_cast<int>(i - r * q) * 4;
+    const f4 v = io4<float>::load(x + r * ldx + c);
+    f4 lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lo.v[j] = v.v[j] - bf16_to_f32(f32_to_bf16(v.v[j]));
+    io4<bf16_t>::store(out + r * ldo + c, v);
+    io4<bf16_t>::store(out + r * ldo + cols + c, lo);
+  }
+}
+
+// fp32 -> bf16 with stochastic rounding (gradients entering a bf16 product).
+__global__ __launch_bounds__(256) void round_sr_kernel(const float* __restrict__ x, int64_t n4, bf16_t* __restrict__ out,
+                                                       uint32_t salt) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n4;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    io4<bf16_t>::store_grad(out + 4 * i, io4<float>::load(x + 4 * i), static_cast<uint32_t>(4 * i), salt);
+}
+
+}  // namespace convert
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" int mg_split_hilo(const float* x, int64_t ldx, int64_t rows, int cols, void* out, int64_t ldo,
+                             void* stream) {
+  const char* fn = "mg_split_hilo";
+  if (!x || !out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (rows < 0 || cols < 0 || cols % 4) return fail(MG_ERR_ARG, "%s: bad shape rows=%lld cols=%d (cols %% 4 == 0)", fn,
+                                                   (long long)rows, cols);
+  if (ldx < cols || ldx % 4 || ldo < 2 * static_cast<int64_t>(cols) || ldo % 4)
+    return fail(MG_ERR_ARG, "%s: bad strides ldx=%lld ldo=%lld", fn, (long long)ldx, (long long)ldo);
+  if (!aligned(x, 16) || !aligned(out, 8)) return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  if (rows == 0 || cols == 0) return MG_OK;
+  const int64_t n = rows * (cols / 4);
+  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(convert::split_hilo_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, ldx,
+                     rows, cols, static_cast<bf16_t*>(out), ldo);
+  return check_launch(fn);
+}
+
+extern "C" int mg_round_bf16_sr(const float* x, int64_t n, void* out, uint32_t salt, void* stream) {
+  const char* fn = "mg_round_bf16_sr";
+  if (!x || !out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (n < 0 || n % 4) return fail(MG_ERR_ARG, "%s: n=%lld must be a non-negative multiple of 4", fn, (long long)n);
+  if (!aligned(x, 16) || !aligned(out, 8)) return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  if (n == 0) return MG_OK;
+  const int64_t n4 = n / 4;
+  const int blocks = static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 4096));
+  hipLaunchKernelGGL(convert::round_sr_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, n4,
+                     static_cast<bf16_t*>(out), salt);
+  return check_launch(fn);
+}

@@ -21,8 +21,9 @@
 // captures.
 //
 // Rounding follows the bf16 training path: the norm output, the projection
-// outputs, the scan output, GELU's input and output and the FeedForward
-// output are bf16 values, the residual stream and the scan state fp32.
+// outputs, GELU's input and output and the FeedForward output are bf16
+// values; the residual stream and the scan state are fp32, and the scan
+// output joins the residual stream unrounded.
 
 #include <algorithm>
 
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     float* st = a.state + static_cast<int64_t>(b) * a.D + d;
     const float h = coef * *st + v;
     *st = h;
-    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + round_bf16(h);
+    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + h;
     return;
   }
   if (lane % kCopies || b >= a.B) return;

@@ -39,6 +39,12 @@
 // fp32 outputs may be split along K over several workgroups: each writes its
 // partial tile to a workspace, and a second kernel adds the partials in split
 // order into C, so the result does not depend on scheduling.
+//
+// Hi/lo products (MG_GEMM_HILO): each operand row holds K bf16 "hi" values
+// followed by K bf16 "lo" values (x = hi + lo to ~2^-16 relative), and the
+// k-loop runs three K segments, A_hi B_hi + A_lo B_hi + A_hi B_lo, into the
+// same fp32 accumulators: an fp32-accurate product (the dropped A_lo B_lo
+// term is ~2^-16 relative) at three times the MFMA work.
 
 #include <algorithm>
 #include <type_traits>
@@ -67,7 +73,35 @@ struct Params {
   int accumulate;    // C += (fp32 outputs)
   uint32_t a_span, b_span;  // bytes from A / B to one past their last element
   uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
+  int hilo;                 // 1: hi/lo operands, three K segments of nkt_seg k-tiles
+  int nkt_seg;              // k-tiles per K segment (ceil(K / 64))
 };
+
+// k-tiles of the whole k-loop (three segments for hi/lo products)
+__device__ __host__ __forceinline__ int total_ktiles(const Params& p) {
+  return p.hilo ? 3 * p.nkt_seg : (p.K + BK - 1) / BK;
+}
+
+// Where global k-tile tg reads: first k within the segment, the mask bound
+// (0 past kt1: those loads read zero) and the column offsets of A and B.
+struct KTile {
+  int k0, kmax, aofs, bofs;
+};
+__device__ __forceinline__ KTile ktile(const Params& p, int tg, int kt1) {
+  KTile r;
+  if (p.hilo) {
+    const int seg = tg / p.nkt_seg;
+    r.k0 = (tg - seg * p.nkt_seg) * BK;
+    r.kmax = tg < kt1 ? p.K : 0;
+    r.aofs = seg == 1 ? p.K : 0;
+    r.bofs = seg == 2 ? p.K : 0;
+  } else {
+    r.k0 = tg * BK;
+    r.kmax = min(p.K, kt1 * BK);
+    r.aofs = r.bofs = 0;
+  }
+  return r;
+}
 
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 3)) & 7); }
 
@@ -109,19 +143,22 @@ struct Loader<R, true, T> {
   static constexpr int kPerWave = R * 8 / 64 / (T / 64);  // wave instructions per tile and wave
   static_assert(kPerWave >= 1 && R * 8 % T == 0, "tile rows vs threads");
 
-  // all of this wave's load instructions for the tile at (r0, k0); k >= kmax reads zero
-  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax) {
+  // all of this wave's load instructions for the tile at (r0, k0); k >= kmax
+  // reads zero; kofs (hi/lo segments) shifts the columns read, not the mask
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax,
+                                       int kofs = 0) {
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) one(o, stage, r0, rmax, k0, kmax, i);
+    for (int i = 0; i < kPerWave; ++i) one(o, stage, r0, rmax, k0, kmax, i, kofs);
   }
   // load instruction i of this wave
-  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int, int k0, int kmax, int i) {
+  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int, int k0, int kmax, int i,
+                                      int kofs = 0) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = wave * kPerWave + i;
     const int r = b * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);  // global chunk stored at LDS chunk lane & 7
     const int kk = k0 + c * 8;
-    const uint32_t off = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(kk) * 2u;
+    const uint32_t off = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(kk + kofs) * 2u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(o.rsrc, (__attribute__((address_space(3))) void*)(stage + b * 64),
                                              16, kk < kmax ? off : kOutOfRange, 0, 0, 0);
   }
@@ -142,11 +179,13 @@ struct Loader<R, false, T> {
   static constexpr int kPerWave = 64 * kChunksRow / 64 / (T / 64);
   static_assert(kPerWave >= 1 && kChunksRow * 64 % T == 0, "tile rows vs threads");
 
-  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax) {
+  __device__ __forceinline__ void load(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax,
+                                       int = 0) {
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) one(o, stage, r0, rmax, k0, kmax, i);
   }
-  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax, int i) {
+  __device__ __forceinline__ void one(const Operand& o, uint4* stage, int r0, int rmax, int k0, int kmax, int i,
+                                      int = 0) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = wave * kPerWave + i;
     const int chunk = b * 64 + lane;
@@ -233,14 +272,14 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, uint4* s1
   const Operand ob = make_operand(p.B, p.ldb, p.b_span);
   Loader<BM, AK, T> la;
   Loader<BN, BKM, T> lb;
-  const int kmax = min(p.K, kt1 * BK);
   // Loads of k-tile t (relative to kt0) into stage t & 1. Past kt1 they are
   // still issued (every wave waits on the same counts) but read as zero.
-  auto issue = [&](int t) {
-    uint4* st = (t & 1) ? s1 : smem;
-    la.load(oa, st, m0, p.M, (kt0 + t) * BK, kmax);
-    lb.load(ob, st + BM * 8, n0, p.N, (kt0 + t) * BK, kmax);
+  auto issue_to = [&](int t, uint4* st) {
+    const KTile kt = ktile(p, kt0 + t, kt1);
+    la.load(oa, st, m0, p.M, kt.k0, kt.kmax, kt.aofs);
+    lb.load(ob, st + BM * 8, n0, p.N, kt.k0, kt.kmax, kt.bofs);
   };
+  auto issue = [&](int t) { issue_to(t, (t & 1) ? s1 : smem); };
   const int n = kt1 - kt0;
   issue(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -297,8 +336,7 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, uint4* s1
     // into the other, and the next tile's loads are issued first
     bf16x8 af[2][MB], bfr[2][NB];
     auto tile = [&](int t, const uint4* cur, uint4* nxt) __attribute__((always_inline)) {
-      la.load(oa, nxt, m0, p.M, (kt0 + t + 1) * BK, kmax);
-      lb.load(ob, nxt + BM * 8, n0, p.N, (kt0 + t + 1) * BK, kmax);
+      issue_to(t + 1, nxt);
       const uint4* Bs = cur + BM * 8;
 #pragma unroll
       for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, AK>(cur, arow[i], 0, lane);
@@ -400,7 +438,7 @@ __device__ __forceinline__ void mainloop_pp(const Params& p, uint4* smem, int m0
   Loader<BN, BKM, T> lb;
   constexpr int LA = decltype(la)::kPerWave, LB = decltype(lb)::kPerWave;
   static_assert(LA + LB == 2 * S, "two load instructions per k-step");
-  const int kmax = min(p.K, kt1 * BK);
+  const int kmax = min(p.K, kt1 * BK);  // (no hi/lo products on this loop)
   auto dma = [&](int t, int q) {  // load instruction q of k-tile t
     uint4* st = smem + ((t & 1) * kStage);
     if (q < LA) la.one(oa, st, m0, p.M, (kt0 + t) * BK, kmax, q);
@@ -513,7 +551,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nkt = (p.K + BK - 1) / BK;
+  const int nkt = total_ktiles(p);
   const int kt0 = blockIdx.y * p.kt_per_split;
   const int kt1 = min(nkt, kt0 + p.kt_per_split);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -628,7 +666,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x.v[e] = old.v[e] + x.v[e];
           }
-          io4<TC>::store(cp, x);
+          if constexpr (EPI == EPI_GELU_GRAD)  // a gradient: stochastic rounding (mg_common.h)
+            io4<TC>::store_grad(cp, x, static_cast<uint32_t>(static_cast<int64_t>(m) * p.N + n), 0x9e5bu);
+          else
+            io4<TC>::store(cp, x);
         } else {
           *reinterpret_cast<uint4*>(cp) = raw;
         }
@@ -728,7 +769,9 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
       f4 d;
 #pragma unroll
       for (int e = 0; e < 4; ++e) d.v[e] = (x.v[e] * inv - (col + e == lab ? 1.0f : 0.0f)) * scale;
-      io4<bf16_t>::store(dlogits + row * ldd + col, d);
+      // stochastic rounding of the bf16 gradient (mg_common.h): round-to-nearest errors of
+      // this near-uniform softmax repeat across the rows of a label
+      io4<bf16_t>::store_grad(dlogits + row * ldd + col, d, static_cast<uint32_t>(row * V + col), 0x8d4au);
     }
   }
   if (lane == 0) s_loss[wave] = lsum;
@@ -768,7 +811,7 @@ struct Plan {
   int tiles, kt_per_split, ysplits;
 };
 
-inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogue, bool deterministic) {
+inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogue, bool deterministic, bool hilo) {
   Plan pl;
   const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
@@ -776,7 +819,7 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   pl.big = !wgrad && t256 >= kCUs;
   const int64_t tiles = pl.big ? t256 : t128;
   pl.tiles = static_cast<int>(tiles);
-  const int nkt = (K + BK - 1) / BK;
+  const int nkt = (hilo ? 3 : 1) * ((K + BK - 1) / BK);
   const int64_t want_wgs = wgrad ? 2 * kCUs : kCUs;
   int splits = 1;
   if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
@@ -839,9 +882,11 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
                        int N, int K, int epilogue, const float* bias, void* aux, int64_t ldaux, int c_dtype, void* C,
                        int64_t ldc, int flags, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "mg_gemm";
-  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC)) return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
+  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC | MG_GEMM_HILO))
+    return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
   const bool accumulate = flags & MG_GEMM_ACCUMULATE;
   const bool deterministic = flags & MG_GEMM_DETERMINISTIC;
+  const bool hilo = flags & MG_GEMM_HILO;
   if (!A || !B || !C) return fail(MG_ERR_ARG, "%s: null operand", fn);
   if (M < 0 || N < 0 || K < 0) return fail(MG_ERR_ARG, "%s: negative size", fn);
   if ((a_layout != MG_KCONTIG && a_layout != MG_MNCONTIG) || (b_layout != MG_KCONTIG && b_layout != MG_MNCONTIG))
@@ -856,7 +901,10 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     return fail(MG_ERR_ARG, "%s: leading dimensions must span whole 16-byte chunks", fn);
   if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16) || (aux && !aligned(aux, 16)) || (bias && !aligned(bias, 16)))
     return fail(MG_ERR_ARG, "%s: operands must be 16-byte aligned", fn);
-  if (lda < (a_layout == MG_KCONTIG ? K : M) || ldb < (b_layout == MG_KCONTIG ? K : N) || ldc < N)
+  if (hilo && (a_layout != MG_KCONTIG || b_layout != MG_KCONTIG || K < 1))
+    return fail(MG_ERR_ARG, "%s: hi/lo products need K-contiguous A and B and K >= 1", fn);
+  const int krow = hilo ? 2 * K : K;  // elements of a K-contiguous row
+  if (lda < (a_layout == MG_KCONTIG ? krow : M) || ldb < (b_layout == MG_KCONTIG ? krow : N) || ldc < N)
     return fail(MG_ERR_ARG, "%s: leading dimension smaller than the row", fn);
   if ((epilogue == MG_EPI_BIAS || epilogue == MG_EPI_BIAS_GELU) && !bias)
     return fail(MG_ERR_ARG, "%s: epilogue needs bias", fn);
@@ -877,8 +925,8 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
   p.M = M; p.N = N; p.K = K;
   const bool ak = a_layout == MG_KCONTIG, bk = b_layout == MG_KCONTIG;
   // bytes spanned by each operand; buffer offsets are 32-bit
-  const int64_t a_span = ak ? (int64_t(M - 1) * lda + K) * 2 : (int64_t(std::max(K, 1) - 1) * lda + M) * 2;
-  const int64_t b_span = bk ? (int64_t(N - 1) * ldb + K) * 2 : (int64_t(std::max(K, 1) - 1) * ldb + N) * 2;
+  const int64_t a_span = ak ? (int64_t(M - 1) * lda + krow) * 2 : (int64_t(std::max(K, 1) - 1) * lda + M) * 2;
+  const int64_t b_span = bk ? (int64_t(N - 1) * ldb + krow) * 2 : (int64_t(std::max(K, 1) - 1) * ldb + N) * 2;
   if (a_span + 256 * lda * 2 >= (int64_t(1) << 31) || b_span + 256 * ldb * 2 >= (int64_t(1) << 31))
     return fail(MG_ERR_ARG, "%s: operands must span less than 2 GiB", fn);
   p.a_span = static_cast<uint32_t>(a_span);
@@ -889,9 +937,11 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     p.aux_span = static_cast<uint32_t>(aux_span);
   }
 
+  p.hilo = hilo ? 1 : 0;
+  p.nkt_seg = (K + gemm::BK - 1) / gemm::BK;
   if (K == 0 && accumulate) return MG_OK;
   // Without a workspace the product runs unsplit.
-  gemm::Plan pl = gemm::plan(M, N, K, ak, bk, c_dtype, epilogue, deterministic || !workspace);
+  gemm::Plan pl = gemm::plan(M, N, K, ak, bk, c_dtype, epilogue, deterministic || !workspace, hilo);
   if (pl.ysplits > 1) {
     const size_t need = gemm::ws_bytes(pl, M, N);
     if (workspace_bytes < need)
@@ -914,7 +964,7 @@ extern "C" size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int
                                           int c_dtype, int flags) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const gemm::Plan pl = gemm::plan(M, N, K, a_layout == MG_KCONTIG, b_layout == MG_KCONTIG, c_dtype, epilogue,
-                                   flags & MG_GEMM_DETERMINISTIC);
+                                   flags & MG_GEMM_DETERMINISTIC, flags & MG_GEMM_HILO);
   return gemm::ws_bytes(pl, M, N);
 }
 

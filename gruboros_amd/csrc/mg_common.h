@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mingru_hip.h"
@@ -46,6 +47,46 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
+// ---------------------------------------------------------------- stochastic rounding
+//
+// Gradients stored in bf16 are rounded stochastically: up (in magnitude)
+// with probability equal to the dropped fraction of a bf16 ulp, so the
+// expected value is the fp32 value. With round-to-nearest each element's
+// error is a fixed function of its value. At a nearly uniform softmax (the
+// untrained model) every row of the logits gradient is (1/V - onehot)/N up
+// to small deviations, so the rows of one label share one rounding error, and
+// those errors add up over the rows of a weight gradient instead of
+// cancelling: on the fp64 restatement at the cfg3 model size they moved the
+// FeedForward and norm weight gradients by 4-7% at 8-16 k rows, growing with
+// the row count; with stochastic rounding by 0.5%, independent of it.
+// The 16 random bits are a hash of the element's index, its value and a salt
+// per call site, so the result is a deterministic function of the inputs (no
+// generator state: replays and resumed runs repeat bit for bit).
+
+// MurmurHash3's 32-bit finaliser (fmix32, A. Appleby, public domain).
+__device__ __forceinline__ uint32_t hash32(uint32_t h) {
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return h;
+}
+
+// fp32 -> bf16, rounded stochastically (non-finite values pass through
+// round-to-nearest). idx: the element's index in its tensor.
+__device__ __forceinline__ bf16_t f32_to_bf16_sr(float f, uint32_t idx, uint32_t salt) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return f32_to_bf16(f);
+  const uint32_t r = hash32(idx * 0x9e3779b9u ^ u ^ salt) & 0xffffu;
+  return static_cast<bf16_t>((u + r) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2_sr(float lo, float hi, uint32_t idx, uint32_t salt) {
+  return static_cast<uint32_t>(f32_to_bf16_sr(lo, idx, salt)) |
+         (static_cast<uint32_t>(f32_to_bf16_sr(hi, idx + 1, salt)) << 16);
+}
+
 // N consecutive channels of one row, loaded/stored as one vector access
 // (N = 4: 8-byte bf16 / 16-byte fp32; N = 8: 16-byte bf16 / 2 x 16-byte fp32).
 template <int N>
@@ -82,6 +123,11 @@ template <int N> struct iov<float, N> {
   __device__ __forceinline__ static void store_nt(float* p, const fv<N>& a) {
 #pragma unroll
     for (int j = 0; j < N; ++j) __builtin_nontemporal_store(a.v[j], p + j);
+  }
+  // Gradient stores (fp32: exact; the bf16 versions round stochastically).
+  __device__ __forceinline__ static void store_grad(float* p, const fv<N>& a, uint32_t, uint32_t) { store(p, a); }
+  __device__ __forceinline__ static void store_grad_nt(float* p, const fv<N>& a, uint32_t, uint32_t) {
+    store_nt(p, a);
   }
 };
 
@@ -121,6 +167,20 @@ template <int N> struct iov<bf16_t, N> {
 #pragma unroll
     for (int q = 0; q < N / 2; ++q)
       __builtin_nontemporal_store(pack_bf16x2(a.v[2 * q], a.v[2 * q + 1]), reinterpret_cast<uint32_t*>(p) + q);
+  }
+  // Gradient stores: stochastic rounding (f32_to_bf16_sr); idx = index of element 0.
+  __device__ __forceinline__ static void store_grad(bf16_t* p, const fv<N>& a, uint32_t idx, uint32_t salt) {
+    raw x;
+    uint32_t* w = reinterpret_cast<uint32_t*>(&x);
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) w[q] = pack_bf16x2_sr(a.v[2 * q], a.v[2 * q + 1], idx + 2 * q, salt);
+    *reinterpret_cast<raw*>(p) = x;
+  }
+  __device__ __forceinline__ static void store_grad_nt(bf16_t* p, const fv<N>& a, uint32_t idx, uint32_t salt) {
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q)
+      __builtin_nontemporal_store(pack_bf16x2_sr(a.v[2 * q], a.v[2 * q + 1], idx + 2 * q, salt),
+                                  reinterpret_cast<uint32_t*>(p) + q);
   }
 };
 

@@ -8,6 +8,9 @@
 //   xn = x + delta                  (the residual stream, fp32)
 //   r  = 1 / sqrt(mean(xn^2) + eps)
 //   y  = xn * r * w                 (bf16 or fp32, the next op's input)
+//   y_lo = bf16(y - bf16(y))        (optional, with a bf16 y: y as a hi/lo
+//                                    pair, hi + lo = y to ~2^-16 relative,
+//                                    for products that need fp32 accuracy)
 // Backward, with dy the gradient of y and dres that of xn from later
 // residual uses:
 //   g  = dy * w,  m = mean(g * xn * r)
@@ -46,7 +49,8 @@ __device__ __forceinline__ f4 load_cols(const T* p, int col, int D) {
 template <typename Td, typename Ty, int kSteps>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
     const float* __restrict__ x, const Td* __restrict__ delta, const float* __restrict__ w,
-    float* __restrict__ x_out, Ty* __restrict__ y, float* __restrict__ rstd, int64_t N, int D, float eps) {
+    float* __restrict__ x_out, Ty* __restrict__ y, bf16_t* __restrict__ y_lo, int64_t ldy,
+    float* __restrict__ rstd, int64_t N, int D, float eps) {
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
   f4 wv[kSteps];
@@ -74,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
       for (int j = 0; j < 4; ++j) ss += xv[i].v[j] * xv[i].v[j];
     ss = wave_sum(ss);
     const float r = __builtin_amdgcn_rsqf(ss * inv_d + eps);
+    const int64_t ybase = row * ldy;
 #pragma unroll
     for (int i = 0; i < kSteps; ++i) {
       const int col = 4 * lane + kColsPerStep * i;
@@ -81,7 +86,13 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
         f4 yv;
 #pragma unroll
         for (int j = 0; j < 4; ++j) yv.v[j] = xv[i].v[j] * r * wv[i].v[j];
-        io4<Ty>::store(y + base + col, yv);
+        io4<Ty>::store(y + ybase + col, yv);
+        if (y_lo) {
+          f4 lo;  // y - bf16(y) is exact in fp32
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lo.v[j] = yv.v[j] - bf16_to_f32(f32_to_bf16(yv.v[j]));
+          io4<bf16_t>::store(y_lo + ybase + col, lo);
+        }
         if (delta && x_out) io4<float>::store(x_out + base + col, xv[i]);
       }
     }
@@ -134,7 +145,8 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_kernel(
           dwa[i].v[j] += dyv[i].v[j] * xh[i].v[j];
         }
         if (dx) io4<float>::store(dx + base + col, d);
-        if (ddelta) io4<Td>::store(ddelta + base + col, d);
+        // a bf16 ddelta rounds stochastically (mg_common.h)
+        if (ddelta) io4<Td>::store_grad(ddelta + base + col, d, static_cast<uint32_t>(base + col), 0x7c39u);
       }
     }
   }
@@ -174,8 +186,8 @@ inline int grid_for(int64_t N) {
 }
 
 template <typename Td, typename Ty>
-int launch_fwd(const float* x, const void* delta, const float* w, float* x_out, void* y, float* rstd, int64_t N,
-               int D, float eps, hipStream_t st) {
+int launch_fwd(const float* x, const void* delta, const float* w, float* x_out, void* y, void* y_lo, int64_t ldy,
+               float* rstd, int64_t N, int D, float eps, hipStream_t st) {
   const int grid = grid_for(N);
   const Td* dl = static_cast<const Td*>(delta);
   Ty* yy = static_cast<Ty*>(y);
@@ -183,7 +195,7 @@ int launch_fwd(const float* x, const void* delta, const float* w, float* x_out, 
 #define MG_NORM_FWD(S)                                                                                  \
   case S:                                                                                              \
     hipLaunchKernelGGL((add_rmsnorm_fwd_kernel<Td, Ty, S>), dim3(grid), dim3(kThreads), 0, st, x, dl, w, \
-                       x_out, yy, rstd, N, D, eps);                                                    \
+                       x_out, yy, static_cast<bf16_t*>(y_lo), ldy, rstd, N, D, eps);                   \
     break;
     MG_NORM_FWD(1) MG_NORM_FWD(2) MG_NORM_FWD(4) MG_NORM_FWD(8) MG_NORM_FWD(16)
 #undef MG_NORM_FWD
@@ -235,8 +247,8 @@ extern "C" size_t mg_add_rmsnorm_bwd_workspace_bytes(int64_t N, int D) {
 }
 
 extern "C" int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* delta, const float* w,
-                                  float* x_out, int y_dtype, void* y, float* rstd, int64_t N, int D, float eps,
-                                  void* stream) {
+                                  float* x_out, int y_dtype, void* y, void* y_lo, int64_t ldy, float* rstd,
+                                  int64_t N, int D, float eps, void* stream) {
   const char* fn = "mg_add_rmsnorm_fwd";
   int rc;
   if (N < 1 || D < 4 || D % 4) return fail(MG_ERR_ARG, "%s: bad shape N=%lld D=%d (D %% 4 == 0)", fn, (long long)N, D);
@@ -245,6 +257,11 @@ extern "C" int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* d
   if ((rc = norm::check_ptr(fn, "y", y, y_dtype == MG_F32 ? 16 : 8, true))) return rc;
   if ((rc = norm::check_ptr(fn, "rstd", rstd, 4, false))) return rc;
   if ((rc = norm::check_dtype(fn, "y", y_dtype))) return rc;
+  if (ldy < D || ldy % 4) return fail(MG_ERR_ARG, "%s: ldy=%lld must be >= D=%d and a multiple of 4", fn, (long long)ldy, D);
+  if (y_lo) {
+    if (y_dtype != MG_BF16) return fail(MG_ERR_DTYPE, "%s: y_lo needs a bf16 y", fn);
+    if ((rc = norm::check_ptr(fn, "y_lo", y_lo, 8, true))) return rc;
+  }
   if (delta) {
     if ((rc = norm::check_dtype(fn, "delta", delta_dtype))) return rc;
     if ((rc = norm::check_ptr(fn, "delta", delta, delta_dtype == MG_F32 ? 16 : 8, true))) return rc;
@@ -253,10 +270,10 @@ extern "C" int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* d
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dbf = delta && delta_dtype == MG_BF16;
   if (y_dtype == MG_BF16)
-    return dbf ? norm::launch_fwd<bf16_t, bf16_t>(x, delta, w, x_out, y, rstd, N, D, eps, st)
-               : norm::launch_fwd<float, bf16_t>(x, delta, w, x_out, y, rstd, N, D, eps, st);
-  return dbf ? norm::launch_fwd<bf16_t, float>(x, delta, w, x_out, y, rstd, N, D, eps, st)
-             : norm::launch_fwd<float, float>(x, delta, w, x_out, y, rstd, N, D, eps, st);
+    return dbf ? norm::launch_fwd<bf16_t, bf16_t>(x, delta, w, x_out, y, y_lo, ldy, rstd, N, D, eps, st)
+               : norm::launch_fwd<float, bf16_t>(x, delta, w, x_out, y, y_lo, ldy, rstd, N, D, eps, st);
+  return dbf ? norm::launch_fwd<bf16_t, float>(x, delta, w, x_out, y, nullptr, ldy, rstd, N, D, eps, st)
+             : norm::launch_fwd<float, float>(x, delta, w, x_out, y, nullptr, ldy, rstd, N, D, eps, st);
 }
 
 extern "C" int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* rstd, int dy_dtype, const void* dy,

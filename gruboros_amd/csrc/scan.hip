@@ -27,6 +27,14 @@
 //     them. Every word a call reads was written by the previous call of the
 //     same direction (or is zero), so stale words never look ready and no
 //     clearing kernel runs per call.
+//   * The workspace starts with a header (magic, shape, error word, wait
+//     limit) written by the initialisation. Every workgroup checks the
+//     header against its launch and returns at once on a mismatch; every
+//     look-back wait gives up after the header's poll limit. Either event
+//     sets a bit in the header's error word (read by
+//     mg_scan_workspace_check), so a workspace that was never initialised,
+//     was initialised for another shape, or is shared by overlapping calls
+//     ends the kernel with an error instead of a wait that never ends.
 //   * The backward walks tiles in reverse time order with the adjoint
 //     recurrence. It needs h_{t-1}: it reads the state entering each 8-step
 //     pair of runs once (the forward's fp32 checkpoint when the output is
@@ -36,8 +44,6 @@
 //     g(hidden) - h_{t-1}, a difference of two nearly equal numbers.)
 
 #include <algorithm>
-#include <mutex>
-#include <unordered_map>
 
 #include "mg_common.h"
 
@@ -78,10 +84,35 @@ struct Geometry {
   int64_t BD;    // B * Di
 };
 
-// Workspace: ticket counters (one per chain and direction), then one
-// look-back word per (tile, channel) for the forward tiles, then the same for
-// the backward tiles.
-inline size_t ws_header_bytes(int ncb) { return (static_cast<size_t>(ncb) * 2 * 4 + 255) / 256 * 256; }
+// Workspace: a 256-byte header, ticket counters (one per chain and
+// direction), then one look-back word per (tile, channel) for the forward
+// tiles, then the same for the backward tiles.
+constexpr uint32_t kWsMagic = 0x4d475343u;  // "MGSC"
+constexpr uint32_t kErrShape = 1u;          // header missing or for another shape
+constexpr uint32_t kErrTicket = 2u;         // a ticket past the chain's last tile
+constexpr uint32_t kErrStall = 4u;          // a look-back wait gave up
+constexpr uint32_t kDefaultPolls = 1u << 22;  // ~1-4 s of polling
+
+struct WsHeader {
+  uint32_t magic;
+  int32_t B, T, Di;
+  uint32_t err;          // kErr* bits, set by the kernels (atomic or)
+  uint32_t max_polls;    // look-back polls of one word before giving up
+  uint32_t pad[58];
+};
+static_assert(sizeof(WsHeader) == 256, "header size");
+
+inline size_t ws_header_bytes(int ncb) {
+  return sizeof(WsHeader) + (static_cast<size_t>(ncb) * 2 * 4 + 255) / 256 * 256;
+}
+
+// The header matches this launch; otherwise the error bit is set (by one
+// thread) and the caller returns. Wave-uniform.
+__device__ __forceinline__ bool header_ok(WsHeader* h, const Geometry& g) {
+  const bool ok = h->magic == kWsMagic && h->B == g.B && h->T == g.T && h->Di == g.Di;
+  if (!ok && threadIdx.x == 0) atomicOr(&h->err, kErrShape);
+  return ok;
+}
 
 // Chain and tile of this workgroup. The chain comes from the block index; the
 // tile (time position) from the chain's ticket counter, in start order. The
@@ -91,7 +122,9 @@ inline size_t ws_header_bytes(int ncb) { return (static_cast<size_t>(ncb) * 2 * 
 // other draw of this call follows it, and the next call starts after this
 // kernel has finished).
 constexpr uint32_t kParityBit = 0x80000000u;
-__device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters, uint32_t* s_ticket,
+// Returns false (after setting the error bit) for a ticket past the chain's
+// last tile, which only a corrupted counter gives; the workgroup then exits.
+__device__ __forceinline__ bool take_tile(const Geometry& g, WsHeader* hdr, uint32_t* counters, uint32_t* s_ticket,
                                           bool reverse, int& k, int& b, int& d0, uint32_t& parity) {
   const int cbi = static_cast<int>(blockIdx.x % static_cast<uint32_t>(g.ncb));
   if (threadIdx.x == 0) {
@@ -103,31 +136,49 @@ __device__ __forceinline__ void take_tile(const Geometry& g, uint32_t* counters,
   const uint32_t t = __builtin_amdgcn_readfirstlane(*s_ticket);
   parity = t >> 31;
   const int kk = static_cast<int>(t & ~kParityBit);
+  if (kk >= g.ntiles) {
+    if (threadIdx.x == 0) atomicOr(&hdr->err, kErrTicket);
+    return false;
+  }
   k = reverse ? (g.ntiles - 1 - kk) : kk;
   b = cbi / g.nblk_d;
   d0 = (cbi % g.nblk_d) * kTileCh;
+  return true;
 }
 
 // Walk from tile k + step in direction `step` (-1: earlier tiles, forward
 // scan; +1: later tiles, backward scan) until an inclusive prefix is found,
 // folding aggregates on the way. Returns the state entering tile k of
-// channel c (one channel per lane).
-__device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step,
-                                            uint32_t parity) {
+// channel c (one channel per lane). `last` is the chain's end tile in that
+// direction (0 or ntiles - 1), which only ever publishes an inclusive
+// prefix: the walk never steps past it. A word that stays not-ready for
+// max_polls polls ends the wait: the error bit is set and the prefix folded
+// so far is returned (the results are then wrong, and the caller learns it
+// from mg_scan_workspace_check).
+__device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step, int last,
+                                            uint32_t parity, uint32_t max_polls, uint32_t* err) {
   float accA = 1.0f, accV = 0.0f;
-  const uint64_t* w = status + static_cast<int64_t>(k + step) * BD + c;
+  int j = k + step;
+  const uint64_t* w = status + static_cast<int64_t>(j) * BD + c;
   const int64_t dw = step * BD;
   const uint32_t par = parity ? kTagParity : 0u;
+  uint32_t polls = 0;
   while (true) {
     const uint64_t x = poll_word(w);
     const uint32_t tag = static_cast<uint32_t>(x);
     const float val = __uint_as_float(static_cast<uint32_t>(x >> 32));
     if (tag == (kTagIncl | par)) return accA * val + accV;
-    if ((tag & (kTagAggBit | kTagParity)) == (kTagAggBit | par)) {
+    if (j != last && (tag & (kTagAggBit | kTagParity)) == (kTagAggBit | par)) {
       accV = accA * val + accV;
       accA = accA * __uint_as_float(tag & ~(kTagAggBit | kTagParity));
       w += dw;
+      j += step;
+      polls = 0;
     } else {
+      if (++polls > max_polls) {
+        atomicOr(err, kErrStall);
+        return accV;
+      }
       __builtin_amdgcn_s_sleep(2);
     }
   }
@@ -212,8 +263,8 @@ template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
     const float* __restrict__ h0, Tout* __restrict__ hout, int64_t out_sb, int64_t out_ld,
-    float* __restrict__ h_last, float* __restrict__ ckpt, Geometry g, uint32_t* __restrict__ counters,
-    uint64_t* __restrict__ status) {
+    float* __restrict__ h_last, float* __restrict__ ckpt, Geometry g, WsHeader* __restrict__ hdr,
+    uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
   constexpr int kSubs = kFwdSubs, kRows = kFwdRows;
   __shared__ uint32_t s_ticket;
   __shared__ RunMaps<kSubs> s_maps;
@@ -224,7 +275,9 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
   const int s = tid / kChLanes;
   int k, b, d0;
   uint32_t parity;
-  take_tile(g, counters, &s_ticket, false, k, b, d0, parity);
+  if (!header_ok(hdr, g)) return;
+  const uint32_t max_polls = hdr->max_polls;
+  if (!take_tile(g, hdr, counters, &s_ticket, false, k, b, d0, parity)) return;
   const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
   const int t0 = k * kFwdTileRows + s * kRows;
@@ -261,7 +314,7 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
       carry = h0 ? h0[c + s] : 0.0f;
     } else {
       publish_agg(st, TA, TV, parity);
-      carry = look_back1(status, g.BD, c + s, k, -1, parity);
+      carry = look_back1(status, g.BD, c + s, k, -1, 0, parity, max_polls, &hdr->err);
     }
     if (k + 1 < g.ntiles) publish_incl(st, TA * carry + TV, parity);
     reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
@@ -338,8 +391,8 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     const float* __restrict__ h0, const Th* __restrict__ hout, int64_t out_sb, int64_t out_ld,
     const float* __restrict__ ckpt, const Th* __restrict__ dh, int64_t g_sb, int64_t g_ld,
     const float* __restrict__ dh_last,
-    Tin* __restrict__ dhidden, Tin* __restrict__ dgate, float* __restrict__ dh0, Geometry g,
-    uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
+    Tin* __restrict__ dhidden, Tin* __restrict__ dgate, int64_t d_sb, int64_t d_ld, float* __restrict__ dh0,
+    Geometry g, WsHeader* __restrict__ hdr, uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
   constexpr int kSubs = kBwdSubs, kRows = kBwdRows;
   __shared__ uint32_t s_ticket;
   __shared__ RunMaps<kSubs> s_maps;
@@ -354,7 +407,9 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   const int s = ((tid / kChLanes) % (kSubs / 2)) * 2 + tid / (kChLanes * kSubs / 2);
   int k, b, d0;
   uint32_t parity;
-  take_tile(g, counters, &s_ticket, true, k, b, d0, parity);
+  if (!header_ok(hdr, g)) return;
+  const uint32_t max_polls = hdr->max_polls;
+  if (!take_tile(g, hdr, counters, &s_ticket, true, k, b, d0, parity)) return;
   const int d = d0 + cl * kVec;
   const bool ok = d < g.Di;
   const int t0 = k * kBwdTileRows + s * kRows;
@@ -440,7 +495,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     float carry = 0.0f;
     if (k != g.ntiles - 1) {
       publish_agg(st, TA, TM, parity);
-      carry = look_back1(status, g.BD, c + q, k, +1, parity);
+      carry = look_back1(status, g.BD, c + q, k, +1, g.ntiles - 1, parity, max_polls, &hdr->err);
     }
     if (k > 0) publish_incl(st, TA * carry + TM, parity);
     reinterpret_cast<float*>(&s_carry[cl])[q] = carry;
@@ -466,8 +521,11 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   }
   if (dh0 && t0 == 0) io4<float>::store(dh0 + c, mu);
 
-  Tin* dhb = dhidden + in_tile;
-  Tin* dgb = dgate + in_tile;
+  const int dld = static_cast<int>(d_ld);
+  const int64_t d_tile = b * d_sb + static_cast<int64_t>(k) * kBwdTileRows * d_ld + d0;
+  const int d_off = s * kRows * dld + cl * kVec;
+  Tin* dhb = dhidden + d_tile;
+  Tin* dgb = dgate + d_tile;
 #pragma unroll
   for (int i = 0; i < kRows; ++i) {
     f4 og, oh;
@@ -486,19 +544,32 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
       hc.v[j] = a[i][j] * hc.v[j] + vv;
     }
     if (t0 + i < g.T) {
-      io4<Tin>::store_nt(dgb + (in_off + i * ild), og);
-      io4<Tin>::store_nt(dhb + (in_off + i * ild), oh);
+      // bf16 gradients round stochastically (mg_common.h), keyed by the element's (b, t, d) index
+      const uint32_t idx = static_cast<uint32_t>((static_cast<int64_t>(b) * g.T + t0 + i) * g.Di + d);
+      io4<Tin>::store_grad_nt(dgb + (d_off + i * dld), og, idx, 0x5a17u);
+      io4<Tin>::store_grad_nt(dhb + (d_off + i * dld), oh, idx, 0x6b28u);
     }
   }
 }
 
 // ------------------------------------------------------------------ host
 
-__global__ void zero_kernel(uint4* __restrict__ p, int64_t n16) {  // workspace initialisation
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n16;
+// Workspace initialisation: zeros, then the header (one thread; the header
+// block is skipped by the zero fill).
+__global__ void init_kernel(uint4* __restrict__ p, int64_t n16, int B, int T, int Di, uint32_t max_polls) {
+  constexpr int64_t kHdr16 = sizeof(WsHeader) / 16;
+  for (int64_t i = kHdr16 + blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n16;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
     p[i] = make_uint4(0, 0, 0, 0);
+  if (blockIdx.x == 0 && threadIdx.x < kHdr16) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x == 0) v = make_uint4(kWsMagic, static_cast<uint32_t>(B), static_cast<uint32_t>(T), static_cast<uint32_t>(Di));
+    if (threadIdx.x == 1) v = make_uint4(0u, max_polls, 0u, 0u);
+    p[threadIdx.x] = v;
+  }
 }
+
+__global__ void set_polls_kernel(WsHeader* h, uint32_t max_polls) { h->max_polls = max_polls; }
 
 inline void make_geometry(int B, int T, int Di, int tile_rows, Geometry& g) {
   g.B = B; g.T = T; g.Di = Di;
@@ -518,13 +589,6 @@ inline size_t ws_bytes_any(int B, int T, int Di) {
   return ws_header_bytes(f.ncb) + static_cast<size_t>(f.ntiles + b.ntiles) * f.BD * sizeof(uint64_t);
 }
 
-// Host-side record of initialised workspaces (address -> shape), so that a
-// call on a workspace that was not initialised for its shape is refused
-// rather than reading stale look-back words.
-struct WsShape { int B, T, Di; size_t bytes; };
-std::mutex g_ws_mu;
-std::unordered_map<uintptr_t, WsShape> g_ws;
-
 inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, void* ws, size_t ws_size,
                         Geometry& g) {
   if (B < 1 || T < 1 || Di < 4) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
@@ -536,16 +600,6 @@ inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, voi
   if (!ws || ws_size < need)
     return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, ws_size, need);
   if (!aligned(ws, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
-  return MG_OK;
-}
-
-// The last check before a launch: the workspace was initialised for this shape.
-inline int check_registered(const char* fn, void* ws, int B, int T, int Di) {
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  const auto it = g_ws.find(reinterpret_cast<uintptr_t>(ws));
-  if (it == g_ws.end() || it->second.B != B || it->second.T != T || it->second.Di != Di)
-    return fail(MG_ERR_WORKSPACE, "%s: workspace not initialised for B=%d T=%d Di=%d (mg_scan_workspace_init)", fn, B,
-                T, Di);
   return MG_OK;
 }
 
@@ -568,8 +622,9 @@ inline int check_f32vec(const char* fn, const char* name, const void* p) {
 }
 
 // Forward or backward counters and look-back words of a workspace.
+inline WsHeader* ws_header(void* ws) { return static_cast<WsHeader*>(ws); }
 inline uint32_t* ws_counters(void* ws, const Geometry& g, bool bwd) {
-  return static_cast<uint32_t*>(ws) + (bwd ? g.ncb : 0);
+  return reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + sizeof(WsHeader)) + (bwd ? g.ncb : 0);
 }
 inline uint64_t* ws_status(void* ws, const Geometry& g, bool bwd) {
   uint64_t* w = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + ws_header_bytes(g.ncb));
@@ -583,21 +638,21 @@ void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_
                 hipStream_t st) {
   hipLaunchKernelGGL((scan_fwd_kernel<Tin, Tout>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kFwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
-                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_counters(ws, g, false),
-                     ws_status(ws, g, false));
+                     static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_header(ws),
+                     ws_counters(ws, g, false), ws_status(ws, g, false));
 }
 
 template <typename Tin, typename Th>
 void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0,
                 const void* h, int64_t out_sb, int64_t out_ld, const float* ckpt, const void* dh, int64_t g_sb,
                 int64_t g_ld,
-                const float* dh_last, void* dhidden, void* dgate, float* dh0, const Geometry& g, void* ws,
-                hipStream_t st) {
+                const float* dh_last, void* dhidden, void* dgate, int64_t d_sb, int64_t d_ld, float* dh0,
+                const Geometry& g, void* ws, hipStream_t st) {
   hipLaunchKernelGGL((scan_bwd_kernel<Tin, Th>), dim3(g.ncb * g.ntiles), dim3(kChLanes * kBwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
                      static_cast<const Th*>(h), out_sb, out_ld, ckpt, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
-                     static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), dh0, g, ws_counters(ws, g, true),
-                     ws_status(ws, g, true));
+                     static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), d_sb, d_ld, dh0, g, ws_header(ws),
+                     ws_counters(ws, g, true), ws_status(ws, g, true));
 }
 
 }  // namespace scan
@@ -624,17 +679,39 @@ extern "C" int mg_scan_workspace_init(void* workspace, size_t workspace_bytes, i
   if (!aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
   const int64_t n16 = static_cast<int64_t>(need / 16);
   const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
-  hipLaunchKernelGGL(scan::zero_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<uint4*>(workspace), n16);
-  if (int rc = check_launch(fn)) return rc;
-  std::lock_guard<std::mutex> lock(scan::g_ws_mu);
-  scan::g_ws[reinterpret_cast<uintptr_t>(workspace)] = scan::WsShape{B, T, Di, workspace_bytes};
-  return MG_OK;
+  hipLaunchKernelGGL(scan::init_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint4*>(workspace), n16, B, T, Di, scan::kDefaultPolls);
+  return check_launch(fn);
 }
 
-extern "C" int mg_scan_workspace_release(void* workspace) {
-  std::lock_guard<std::mutex> lock(scan::g_ws_mu);
-  scan::g_ws.erase(reinterpret_cast<uintptr_t>(workspace));
+extern "C" int mg_scan_workspace_set_max_polls(void* workspace, uint32_t max_polls, void* stream) {
+  const char* fn = "mg_scan_workspace_set_max_polls";
+  if (!workspace || !aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: bad workspace pointer", fn);
+  if (max_polls < 1) return fail(MG_ERR_ARG, "%s: max_polls must be at least 1", fn);
+  hipLaunchKernelGGL(scan::set_polls_kernel, dim3(1), dim3(1), 0, static_cast<hipStream_t>(stream),
+                     scan::ws_header(workspace), max_polls);
+  return check_launch(fn);
+}
+
+extern "C" int mg_scan_workspace_check(const void* workspace, void* stream) {
+  const char* fn = "mg_scan_workspace_check";
+  if (!workspace) return fail(MG_ERR_ARG, "%s: NULL workspace", fn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  scan::WsHeader h;
+  hipError_t e = hipStreamSynchronize(st);
+  if (e == hipSuccess) e = hipMemcpy(&h, workspace, sizeof(h), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(MG_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+  if (h.magic != scan::kWsMagic) return fail(MG_ERR_WORKSPACE, "%s: workspace was never initialised", fn);
+  if (h.err & scan::kErrShape)
+    return fail(MG_ERR_WORKSPACE, "%s: a scan call used this workspace (initialised for B=%d T=%d Di=%d) with "
+                "another shape; its results are invalid", fn, h.B, h.T, h.Di);
+  if (h.err & scan::kErrStall)
+    return fail(MG_ERR_STALL, "%s: a look-back wait gave up after %u polls%s (overlapping calls on one workspace, "
+                "or a corrupted workspace); results invalid, initialise it again", fn, h.max_polls,
+                (h.err & scan::kErrTicket) ? " and a ticket past the last tile was drawn" : "");
+  if (h.err & scan::kErrTicket)
+    return fail(MG_ERR_WORKSPACE, "%s: ticket counters corrupted (overlapping calls on one workspace?); results "
+                "invalid, initialise it again", fn);
   return MG_OK;
 }
 
@@ -652,9 +729,6 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "h_last", h_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
-  if (!((in_dtype == MG_BF16 || in_dtype == MG_F32) && (out_dtype == MG_F32 || in_dtype == out_dtype)))
-    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
-  if ((rc = scan::check_registered(fn, workspace, B, T, Di))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
     scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
@@ -670,9 +744,8 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
 extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
                            const float* h0, int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
                            const float* ckpt, const void* dh, int64_t g_sb, int64_t g_ld, const float* dh_last,
-                           void* dhidden,
-                           void* dgate, float* dh0, int B, int T, int Di, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+                           void* dhidden, void* dgate, int64_t d_sb, int64_t d_ld, float* dh0, int B, int T, int Di,
+                           void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "mg_scan_bwd";
   scan::Geometry g;
   int rc;
@@ -681,25 +754,22 @@ extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dh", dh, out_dtype, g_sb, g_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "dhidden", dhidden, in_dtype, in_sb, in_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "dgate", dgate, in_dtype, in_sb, in_ld))) return rc;
+  if ((rc = scan::check_tensor(fn, "dhidden", dhidden, in_dtype, d_sb, d_ld))) return rc;
+  if ((rc = scan::check_tensor(fn, "dgate", dgate, in_dtype, d_sb, d_ld))) return rc;
   if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh_last", dh_last))) return rc;
   if ((rc = scan::check_f32vec(fn, "dh0", dh0))) return rc;
   if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
-  if (!((in_dtype == MG_BF16 || in_dtype == MG_F32) && (out_dtype == MG_F32 || in_dtype == out_dtype)))
-    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
-  if ((rc = scan::check_registered(fn, workspace, B, T, Di))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
     scan::launch_bwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
-                                     dhidden, dgate, dh0, g, workspace, st);
+                                     dhidden, dgate, d_sb, d_ld, dh0, g, workspace, st);
   else if (in_dtype == MG_F32 && out_dtype == MG_F32)
     scan::launch_bwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
-                                   dhidden, dgate, dh0, g, workspace, st);
+                                   dhidden, dgate, d_sb, d_ld, dh0, g, workspace, st);
   else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
     scan::launch_bwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, ckpt, dh, g_sb, g_ld, dh_last,
-                                    dhidden, dgate, dh0, g, workspace, st);
+                                    dhidden, dgate, d_sb, d_ld, dh0, g, workspace, st);
   else
     return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
   return check_launch(fn);

@@ -12,7 +12,7 @@ from . import _lib
 
 KCONTIG, MNCONTIG = 0, 1
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD = 0, 1, 2, 3
-FLAG_ACCUMULATE, FLAG_DETERMINISTIC = 1, 2
+FLAG_ACCUMULATE, FLAG_DETERMINISTIC, FLAG_HILO = 1, 2, 4
 
 
 def _rows(t, name):
@@ -54,13 +54,15 @@ def _workspace(device, nbytes):
 
 
 def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False,
-         deterministic=None):
+         deterministic=None, hilo=False):
     """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm).
     Results repeat bit for bit. deterministic (default: torch.are_deterministic_algorithms_enabled())
-    also rules out the split along K, so the sum order depends only on K."""
+    also rules out the split along K, so the sum order depends only on K. hilo: A and B rows are
+    [hi (K) | lo (K)] bf16 pairs and the product is fp32-accurate (three MFMA passes)."""
     if deterministic is None:
         deterministic = torch.are_deterministic_algorithms_enabled()
-    flags = (FLAG_ACCUMULATE if accumulate else 0) | (FLAG_DETERMINISTIC if deterministic else 0)
+    flags = (FLAG_ACCUMULATE if accumulate else 0) | (FLAG_DETERMINISTIC if deterministic else 0) | \
+        (FLAG_HILO if hilo else 0)
     _lib.require_cuda(a, b, out)
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise _lib.MingruHipError(f"mg_gemm operands must be bfloat16 (got {a.dtype}, {b.dtype})")
@@ -93,11 +95,38 @@ def linear_fwd(x, w, bias=None, *, gelu_pre=None, out_dtype=torch.bfloat16):
     return gemm(x, KCONTIG, w, KCONTIG, n, o, k, y, epilogue=epi, bias=bias, aux=gelu_pre)
 
 
-def linear_dx(dy, w, *, gelu_pre=None):
-    """dy [N, out] bf16, w [out, in] bf16 -> dy w [N, in] bf16; times gelu'(gelu_pre) when given."""
+def split_hilo(x, out=None):
+    """fp32 [rows, cols] (unit inner stride) -> bf16 [rows, 2 cols] = [bf16(x) | bf16(x - bf16(x))]
+    (mg_split_hilo), the operand form of hilo products."""
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty(rows, 2 * cols, dtype=torch.bfloat16, device=x.device)
+    L = _lib.lib()
+    _lib.check(L.mg_split_hilo(_lib.ptr(x), _rows(x, "x"), rows, cols, _lib.ptr(out), _rows(out, "out"),
+                               _lib.stream_of(x)), "mg_split_hilo")
+    return out
+
+
+def round_bf16_sr(x, salt=0x3c1d):
+    """fp32 tensor (contiguous, numel % 4 == 0) -> bf16, rounded stochastically (mg_round_bf16_sr)."""
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.lib().mg_round_bf16_sr(_lib.ptr(x), x.numel(), _lib.ptr(out), salt, _lib.stream_of(x)),
+               "mg_round_bf16_sr")
+    return out
+
+
+def linear_fwd_hilo(x_pair, w_pair, out, K):
+    """out[N, O] = x w^T to fp32 accuracy from hi/lo pairs: x_pair [N, 2K], w_pair [O, 2K] (bf16);
+    out bf16 or fp32, any row stride."""
+    n, o = x_pair.shape[0], w_pair.shape[0]
+    return gemm(x_pair, KCONTIG, w_pair, KCONTIG, n, o, K, out, hilo=True)
+
+
+def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16):
+    """dy [N, out] bf16, w [out, in] bf16 -> dy w [N, in] (bf16 or fp32); times gelu'(gelu_pre) when given."""
     n, o = dy.shape
     k = w.shape[1]
-    dx = torch.empty(n, k, device=dy.device, dtype=torch.bfloat16)
+    dx = torch.empty(n, k, device=dy.device, dtype=out_dtype)
     return gemm(dy, KCONTIG, w, MNCONTIG, n, k, o, dx,
                 epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre)
 

@@ -11,6 +11,17 @@ a bf16 copy next to its fp32 master:
   * the backward produces the weight gradient directly in fp32 (bf16 x bf16
     GEMM with fp32 output), so no cast of the gradient either.
 With fp32 activations this is plain F.linear.
+
+Two products are computed to fp32 accuracy from bf16 hi/lo pairs (mg_gemm
+HILO: A_hi B_hi + A_lo B_hi + A_hi B_lo on MFMA): the hidden half of
+to_hidden_and_gate (reference mingru/minGRU.py:45) and to_out (:71). The
+reference's g(x) has a kink at 0 (g' jumps from 1/4 to 1), so a bf16-rounded
+pre-activation that lands on the wrong side of 0 changes that element's
+gradient by 75%; measured on the fp64 restatement at the cfg3 model size,
+bf16-rounded inputs and weights there alone move the to_hidden_and_gate and
+norm-weight gradients by ~3% (norm-relative), the accurate products bring
+every gradient to ~1.3%. The gate half has no kink and stays a plain bf16
+product.
 """
 import torch
 import torch.nn.functional as F
@@ -57,15 +68,16 @@ def column_sum(x2):
 
 
 def gelu_backward(dh, pre, want_bias_grad=True):
-    """(bf16(dh * gelu'(pre)), its fp32 column sums) for bf16 [N, C] inputs (mg_gelu_bwd)."""
+    """(bf16(dh * gelu'(pre)) rounded stochastically, its fp32 column sums) for a bf16 or fp32
+    dh and bf16 pre, [N, C] (mg_gelu_bwd)."""
     N, C = pre.shape
     L = lib()
     dpre = torch.empty_like(pre)
     db = torch.empty(C, dtype=torch.float32, device=pre.device) if want_bias_grad else None
     ws = torch.empty(L.mg_column_sum_workspace_bytes(N, C) if want_bias_grad else 16, dtype=torch.uint8,
                      device=pre.device)
-    check(L.mg_gelu_bwd(ptr(dh), dh.stride(0), ptr(pre), pre.stride(0), ptr(dpre), dpre.stride(0), ptr(db), N, C,
-                        ptr(ws), ws.numel(), stream_of(pre)), "mg_gelu_bwd")
+    check(L.mg_gelu_bwd(dtype_code(dh.dtype), ptr(dh), dh.stride(0), ptr(pre), pre.stride(0), ptr(dpre),
+                        dpre.stride(0), ptr(db), N, C, ptr(ws), ws.numel(), stream_of(pre)), "mg_gelu_bwd")
     return dpre, db
 
 
@@ -76,6 +88,89 @@ def bf16_copy(w):
         cache = (w._version, w.detach().to(torch.bfloat16))
         w._mg_bf16 = cache
     return cache[1]
+
+
+def bf16_pair(w):
+    """The hi/lo pair [rows, 2 cols] of fp32 parameter w (gemm.split_hilo), re-made if w
+    changed in place. The fused optimizer step drops it (it rewrites w through a raw
+    pointer, which torch's version counter does not see)."""
+    cache = getattr(w, "_mg_pair", None)
+    if cache is None or cache[0] != w._version or cache[1].device != w.device or \
+            cache[1].shape != (w.shape[0], 2 * w.shape[1]):
+        cache = (w._version, gemm.split_hilo(w.detach()))
+        w._mg_pair = cache
+    return cache[1]
+
+
+class HiddenGateProjection(torch.autograd.Function):
+    """hg = [n W_hidden^T | n W_gate^T] (reference mingru/minGRU.py:45) in bf16, its hidden
+    half computed to fp32 accuracy from the hi/lo pairs of n and W_hidden.
+
+    n: [N, D] bf16, the hi half of `pair` ([N, 2D], from the norm kernel); w: fp32 master
+    [2 Di, D] with its pair and bf16 copy. Backward: dn = dhg W (bf16), dW = dhg^T n (fp32)."""
+
+    @staticmethod
+    def forward(ctx, n, pair, w, w_pair, wb):
+        N, D = n.shape
+        Di = w.shape[0] // 2
+        hg = torch.empty(N, 2 * Di, dtype=torch.bfloat16, device=n.device)
+        gemm.linear_fwd_hilo(pair, w_pair[:Di], hg[:, :Di], D)
+        gemm.gemm(n, gemm.KCONTIG, wb[Di:], gemm.KCONTIG, N, Di, D, hg[:, Di:])
+        ctx.save_for_backward(n, wb)
+        return hg
+
+    @staticmethod
+    def backward(ctx, dhg):
+        n, wb = ctx.saved_tensors
+        dhg = dhg.contiguous()
+        dn = torch.mm(dhg, wb) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[2]:
+            dw = gemm.linear_dw(dhg, n) if _dw_ok(dhg, n) else _mm_f32(dhg.t(), n)
+        return dn, None, dw, None, None
+
+
+def hidden_gate_projection(n, pair, layer):
+    """to_hidden_and_gate(n) with the accurate hidden half; n [..., D] bf16 (hi half of pair)."""
+    w = layer.weight
+    shape = n.shape
+    hg = HiddenGateProjection.apply(n.reshape(-1, shape[-1]), pair.reshape(-1, 2 * shape[-1]), w, bf16_pair(w),
+                                    bf16_copy(w))
+    return hg.view(*shape[:-1], w.shape[0])
+
+
+class AccurateLinearF32(torch.autograd.Function):
+    """y = x W^T to fp32 accuracy (hi/lo products) for an fp32 x [N, K] and fp32 master W;
+    y fp32. Backward: dx = dy W in fp32, dW = dy^T x on bf16 operands (fp32 result)."""
+
+    @staticmethod
+    def forward(ctx, x, w, w_pair, wb):
+        N, K = x.shape
+        x_pair = gemm.split_hilo(x)
+        y = torch.empty(N, w.shape[0], dtype=torch.float32, device=x.device)
+        gemm.linear_fwd_hilo(x_pair, w_pair, y, K)
+        ctx.save_for_backward(x_pair, wb)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x_pair, wb = ctx.saved_tensors
+        K = wb.shape[1]
+        dyb = dy.to(torch.bfloat16).contiguous()
+        dx = gemm.linear_dx(dyb, wb, out_dtype=torch.float32) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            xh = x_pair[:, :K]
+            dw = gemm.linear_dw(dyb, xh) if _dw_ok(dyb, xh) else _mm_f32(dyb.t(), xh)
+        return dx, dw, None, None
+
+
+def accurate_linear_f32(x, layer):
+    """layer(x) (no bias) for an fp32 x, to fp32 accuracy on MFMA; fp32 output."""
+    w = layer.weight
+    shape = x.shape
+    y = AccurateLinearF32.apply(x.reshape(-1, shape[-1]).contiguous(), w, bf16_pair(w), bf16_copy(w))
+    return y.view(*shape[:-1], w.shape[0])
 
 
 class BF16Linear(torch.autograd.Function):
@@ -104,13 +199,15 @@ class BF16Linear(torch.autograd.Function):
 
 
 def linear(x, layer):
-    """layer(x) in x's dtype: fp32 -> F.linear; bf16 -> BF16Linear over the cached bf16 weight."""
+    """layer(x) in x's dtype: same dtypes -> F.linear; bf16 activations over fp32 masters ->
+    BF16Linear over the cached bf16 weight; parameters in another dtype (a model cast to
+    float16) -> the product in the parameters' dtype, the result back in x's."""
     w, b = layer.weight, layer.bias
     if x.dtype == w.dtype:
         return F.linear(x, w, b)
-    if x.dtype != torch.bfloat16 or w.dtype != torch.float32:
-        raise TypeError(f"unsupported linear: activations {x.dtype}, weight {w.dtype}")
-    return BF16Linear.apply(x, w, b, bf16_copy(w))
+    if x.dtype == torch.bfloat16 and w.dtype == torch.float32:
+        return BF16Linear.apply(x, w, b, bf16_copy(w))
+    return F.linear(x.to(w.dtype), w, b).to(x.dtype)
 
 
 # Where the GELU of the FeedForward runs (measured on MI355X in the cfg3
@@ -175,7 +272,9 @@ def feed_forward(x, ff):
     l1, l2 = ff[0], ff[2]
     if x.dtype == l1.weight.dtype:
         return l2(F.gelu(l1(x)))
-    if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32 or l1.bias is None or l2.bias is None:
-        raise TypeError(f"unsupported feed-forward: activations {x.dtype}, weight {l1.weight.dtype}")
+    if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32:
+        return l2(F.gelu(l1(x.to(l1.weight.dtype)))).to(x.dtype)  # parameters cast to another dtype
+    if l1.bias is None or l2.bias is None:
+        raise TypeError("the bf16 feed-forward needs both biases (reference mingru/minLM.py:17-23)")
     return BF16FeedForward.apply(x, l1.weight, l1.bias, l2.weight, l2.bias, bf16_copy(l1.weight),
                                  bf16_copy(l2.weight), bf16_copy(l1.bias), bf16_copy(l2.bias))

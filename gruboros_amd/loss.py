@@ -79,5 +79,5 @@ def logits_cross_entropy(embed, to_logits, labels):
     w = to_logits.weight
     if embed.dtype == torch.bfloat16 and w.dtype == torch.float32:
         return LogitsCrossEntropy.apply(e2.contiguous(), w, bf16_copy(w), lab)
-    logits = torch.nn.functional.linear(e2, w)
+    logits = torch.nn.functional.linear(e2.to(w.dtype), w)  # (parameters cast to another dtype: product in it)
     return CrossEntropyFromLogits.apply(logits.float().contiguous(), lab)

@@ -11,6 +11,7 @@ import torch
 import torch.nn.functional as F
 from torch.nn import Identity, Linear, Module
 
+from ..linear import accurate_linear_f32, hidden_gate_projection
 from ..linear import linear as _linear
 from ..scan import gate_scan_packed
 
@@ -68,6 +69,27 @@ class minGRU(Module):
             out = _linear(out, self.to_out)                # :71
         if not return_next_prev_hidden:
             return out
+        return out, next_prev_hidden
+
+    def block_forward(self, n, pair, prev_hidden=None):
+        """The minLM block's call (reference mingru/minLM.py:121-123): returns
+        (out, next_prev_hidden) with `out` in fp32 when the activations are
+        bf16, so the residual stream receives the scan state unrounded.
+
+        pair: the hi/lo buffer of the normalized input n (bf16 activations over
+        fp32 master weights) or None. With it, the hidden half of the projection
+        and to_out are fp32-accurate products (see gruboros_amd.linear)."""
+        if pair is not None:
+            hg = hidden_gate_projection(n, pair, self.to_hidden_and_gate)
+        else:
+            hg = _linear(n, self.to_hidden_and_gate)
+        out_dtype = torch.float32 if hg.dtype == torch.bfloat16 else None
+        out, next_prev_hidden = gate_scan_packed(hg, prev_hidden, out_dtype)
+        if isinstance(self.to_out, Linear):
+            if pair is not None:
+                out = accurate_linear_f32(out, self.to_out)
+            else:
+                out = _linear(out.to(n.dtype), self.to_out)
         return out, next_prev_hidden
 
 

@@ -6,9 +6,13 @@ initialisation and forward signature as the reference
 indices and the TBPTT caller (train.py:783-809) carry over unchanged.
 
 Compute: parameters stay fp32 masters; activations run in `compute_dtype`
-(default: the parameters' dtype; bfloat16 for the MI355X training
-configuration) with the residual stream kept in fp32. The minGRU scan runs
-in the fused HIP kernel.
+(default: the process default set by gruboros_amd.mingru.set_default_compute_dtype
+or install_alias(compute_dtype=...), else the parameters' dtype; bfloat16 for
+the MI355X training configuration) with the residual stream kept in fp32. The
+minGRU scan runs in the fused HIP kernel. A model whose parameters were cast
+to bfloat16 (reference generate.py:140-142) runs its activations in bf16; one
+cast to float16 (generate.py:143-144) runs its products in float16 and the
+kernels (norm, scan) in fp32.
 """
 import math
 
@@ -17,10 +21,13 @@ import torch.nn.functional as F
 from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
+from .. import blocks
 from ..linear import feed_forward
 from ..linear import linear as _linear
 from ..loss import logits_cross_entropy
 from ..norm import add_rms_norm, rms_norm, rms_norm_residual
+from ..scan import _prep_h0
+from . import _defaults
 from .minGRU import minGRU
 
 
@@ -108,6 +115,20 @@ class minLM(Module):
         if exists(prev_hiddens) and not return_loss:
             x = x[:, -1:]  # single-step decoding (reference :101-102; per-token ops commute with the slice)
 
+        cd, accurate = self._dtypes()
+        if accurate and blocks.supported(self):
+            # bf16 training path: block-level autograd functions (gruboros_amd.blocks)
+            xs, pending, next_prev_hiddens = self._trunk_blocks(x, prev_hiddens)
+            if return_loss:
+                loss = blocks.FinalNormCE.apply(xs, pending, self.norm.weight, self.to_logits.weight, labels)
+                return (loss, next_prev_hiddens) if return_prev_hiddens else loss
+            if pending is None:
+                embed = rms_norm(xs, self.norm.weight, cd)
+            else:
+                _, embed, _ = add_rms_norm(xs, pending, self.norm.weight, cd)
+            logits = _linear(embed, self.to_logits)
+            return (logits, next_prev_hiddens) if return_prev_hiddens else logits
+
         embed, next_prev_hiddens = self._trunk(x, prev_hiddens)
 
         if not return_loss:
@@ -126,13 +147,48 @@ class minLM(Module):
     def logits_and_hiddens(self, ids, prev_hiddens=None):
         """Logits for every position of `ids` and the next prev_hiddens
         (reference mingru/minLM.py:97-138, the body shared by all forward modes)."""
+        cd, accurate = self._dtypes()
+        if accurate and blocks.supported(self):
+            xs, pending, hiddens = self._trunk_blocks(ids, prev_hiddens)
+            _, embed, _ = add_rms_norm(xs, pending, self.norm.weight, cd)
+            return _linear(embed, self.to_logits), hiddens
         embed, hiddens = self._trunk(ids, prev_hiddens)
         return _linear(embed, self.to_logits), hiddens
 
+    def _dtypes(self):
+        """(activation dtype of the kernels, whether the bf16 path over fp32 masters applies)."""
+        param_dtype = self.token_emb.weight.dtype
+        cd = default(self.compute_dtype, default(_defaults.COMPUTE_DTYPE, param_dtype))
+        if param_dtype not in (torch.float32, torch.bfloat16):
+            cd = torch.float32  # float16 parameters: products in float16 (linear.linear), kernels in fp32
+        elif param_dtype == torch.bfloat16:
+            cd = torch.bfloat16
+        return cd, cd == torch.bfloat16 and param_dtype == torch.float32
+
+    def _trunk_blocks(self, ids, prev_hiddens):
+        """Embedding and the blocks (reference :97-135) as block-level autograd
+        functions: returns (x, pending, next_prev_hiddens), x the fp32 residual
+        stream and pending the last FeedForward output, not yet added."""
+        x = self.token_emb(ids).float()
+        prev_hiddens = iter(default(prev_hiddens, []))
+        next_prev_hiddens = []
+        pending = None
+        for _, norm, mingru, ff_norm, ff, _ in self.layers:
+            B, T, _ = x.shape
+            w_hg = mingru.to_hidden_and_gate.weight
+            h0 = _prep_h0(next(prev_hiddens, None), B, w_hg.shape[0] // 2, x.device)
+            w_to = mingru.to_out.weight if isinstance(mingru.to_out, nn.Linear) else None
+            x, out, h_last = blocks.MinGRUBlock.apply(x, pending, norm.weight, w_hg, h0, w_to)
+            next_prev_hiddens.append(h_last)
+            x, pending = blocks.FFBlock.apply(x, out, ff_norm.weight, ff[0].weight, ff[0].bias, ff[2].weight,
+                                              ff[2].bias)
+        return x, pending, next_prev_hiddens
+
     def _trunk(self, ids, prev_hiddens):
-        """Embedding, blocks and final norm (reference :97-137): (embed, next_prev_hiddens)."""
+        """Embedding, blocks and final norm (reference :97-137) op by op:
+        (embed, next_prev_hiddens)."""
         x = self.token_emb(ids)
-        cd = default(self.compute_dtype, x.dtype)
+        cd, accurate = self._dtypes()
         x = x.float()  # fp32 residual stream
 
         next_prev_hiddens = []
@@ -150,15 +206,15 @@ class minLM(Module):
                     x, pending = x + pending.float(), None
                 x = conv(x) + x
             if pending is None:
-                x, n = rms_norm_residual(x, norm.weight, cd)
+                x, n, pair = rms_norm_residual(x, norm.weight, cd, with_lo=accurate)
             else:
-                x, n = add_rms_norm(x, pending, norm.weight, cd)
+                x, n, pair = add_rms_norm(x, pending, norm.weight, cd, with_lo=accurate)
 
             prev_hidden = next(prev_hiddens, None)
-            min_gru_out, next_prev_hidden = mingru(n, prev_hidden, return_next_prev_hidden=True)
+            min_gru_out, next_prev_hidden = mingru.block_forward(n, pair, prev_hidden)
             next_prev_hiddens.append(next_prev_hidden)
 
-            x, n2 = add_rms_norm(x, min_gru_out, ff_norm.weight, cd)
+            x, n2, _ = add_rms_norm(x, min_gru_out, ff_norm.weight, cd)
             pending = _ff(n2, ff)
 
             if exists(dropout):
@@ -167,7 +223,7 @@ class minLM(Module):
         if pending is None:
             embed = rms_norm(x, self.norm.weight, cd)
         else:
-            _, embed = add_rms_norm(x, pending, self.norm.weight, cd)
+            _, embed, _ = add_rms_norm(x, pending, self.norm.weight, cd)
         return embed, next_prev_hiddens
 
     def _initialize_weights(self):

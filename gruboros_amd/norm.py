@@ -4,8 +4,15 @@
 Reference semantics: torch.nn.RMSNorm(dim) as used by mingru/minLM.py:67,
 :69, :74 (eps=None -> float32 machine epsilon) and the residual adds at
 mingru/minLM.py:125 and :130. The residual stream is kept in fp32; the
-normalized output is produced in the activation dtype.
+normalized output is produced in the activation dtype, optionally (bf16) as
+a hi/lo pair [N, 2D] = [bf16(y) | bf16(y - bf16(y))] whose hi half is the
+usual output: the operand of the fp32-accurate products (gemm HILO).
+Weights of any floating dtype are accepted (a model cast with
+.to(torch.bfloat16), as reference generate.py:140-142 does); the kernels read
+them as fp32.
 """
+import ctypes
+
 import torch
 
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
@@ -18,16 +25,24 @@ def _rows(t):
     return t.numel() // D, D
 
 
-def _fwd(x, delta, w, out_dtype):
+def _fwd(x, delta, w, out_dtype, with_lo=False):
+    """Returns (x_out, y, rstd, pair): pair is the [..., 2D] hi/lo buffer
+    (y is its first half) when with_lo, else None."""
     N, D = _rows(x)
-    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    pair = None
+    if with_lo:
+        pair = torch.empty(*x.shape[:-1], 2 * D, dtype=torch.bfloat16, device=x.device)
+        y = pair[..., :D]
+    else:
+        y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     rstd = torch.empty(N, dtype=torch.float32, device=x.device)
     x_out = torch.empty_like(x) if delta is not None else None
     rc = lib().mg_add_rmsnorm_fwd(ptr(x), dtype_code(delta.dtype) if delta is not None else 0, ptr(delta), ptr(w),
-                                  ptr(x_out), dtype_code(out_dtype), ptr(y), ptr(rstd), N, D, FP32_EPS,
-                                  stream_of(x))
+                                  ptr(x_out), dtype_code(y.dtype), ptr(y),
+                                  ctypes.c_void_p(pair.data_ptr() + 2 * D) if with_lo else None,
+                                  2 * D if with_lo else D, ptr(rstd), N, D, FP32_EPS, stream_of(x))
     check(rc, "mg_add_rmsnorm_fwd")
-    return x_out, y, rstd
+    return x_out, y, rstd, pair
 
 
 def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta):
@@ -58,19 +73,21 @@ class RMSNormResidualFn(torch.autograd.Function):
     gradient inside the backward kernel instead of in a separate add."""
 
     @staticmethod
-    def forward(ctx, x, w, out_dtype):
-        _, y, rstd = _fwd(x, None, w, out_dtype)
+    def forward(ctx, x, w, out_dtype, with_lo):
+        _, y, rstd, pair = _fwd(x, None, w, out_dtype, with_lo)
         ctx.save_for_backward(x, w, rstd)
         ctx.set_materialize_grads(False)
-        return x.view_as(x), y
+        if pair is not None:
+            ctx.mark_non_differentiable(pair)
+        return x.view_as(x), y, pair
 
     @staticmethod
-    def backward(ctx, dx_res, dy):
+    def backward(ctx, dx_res, dy, _dpair):
         x, w, rstd = ctx.saved_tensors
         if dx_res is None and dy is None:
-            return None, None, None
+            return None, None, None, None
         dx, _, dw = _bwd(x, w, rstd, dy, dx_res, ctx.needs_input_grad[0], None, False)
-        return dx, (dw if ctx.needs_input_grad[1] else None), None
+        return dx, (dw if ctx.needs_input_grad[1] else None), None, None
 
 
 class RMSNormFn(torch.autograd.Function):
@@ -78,7 +95,7 @@ class RMSNormFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w, out_dtype):
-        _, y, rstd = _fwd(x, None, w, out_dtype)
+        _, y, rstd, _ = _fwd(x, None, w, out_dtype)
         ctx.save_for_backward(x, w, rstd)
         return y
 
@@ -93,47 +110,63 @@ class AddRMSNormFn(torch.autograd.Function):
     """(x + delta, rmsnorm(x + delta) * w): the residual add fused with the next norm."""
 
     @staticmethod
-    def forward(ctx, x, delta, w, out_dtype):
-        x_out, y, rstd = _fwd(x, delta, w, out_dtype)
+    def forward(ctx, x, delta, w, out_dtype, with_lo):
+        x_out, y, rstd, pair = _fwd(x, delta, w, out_dtype, with_lo)
         ctx.save_for_backward(x_out, w, rstd)
         ctx.delta_dtype = delta.dtype
         ctx.set_materialize_grads(False)  # an unused x_out (the final norm's) gets no zero tensor
-        return x_out, y
+        if pair is not None:
+            ctx.mark_non_differentiable(pair)
+        return x_out, y, pair
 
     @staticmethod
-    def backward(ctx, dx_out, dy):
+    def backward(ctx, dx_out, dy, _dpair):
         xn, w, rstd = ctx.saved_tensors
         if dx_out is None and dy is None:
-            return None, None, None, None
+            return None, None, None, None, None
         want_dx, want_dd = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dx, dd, dw = _bwd(xn, w, rstd, dy, dx_out, want_dx, ctx.delta_dtype, want_dd)
-        return dx, dd, (dw if ctx.needs_input_grad[2] else None), None
+        return dx, dd, (dw if ctx.needs_input_grad[2] else None), None, None
 
 
 def _check(x, w, delta=None):
+    """Validates the operands; returns the weight as fp32 (a cast that autograd
+    differentiates, for models whose parameters are bf16 or fp16)."""
     require_cuda(x, w, delta)
     if x.dtype != torch.float32:
         raise ValueError(f"the residual stream must be float32, got {x.dtype}")
-    if w.dtype != torch.float32 or w.dim() != 1 or w.shape[0] != x.shape[-1]:
-        raise ValueError(f"weight must be float32 [{x.shape[-1]}], got {w.dtype} {tuple(w.shape)}")
+    if not w.is_floating_point() or w.dim() != 1 or w.shape[0] != x.shape[-1]:
+        raise ValueError(f"weight must be a floating [{x.shape[-1]}] vector, got {w.dtype} {tuple(w.shape)}")
     if delta is not None and delta.shape != x.shape:
         raise ValueError(f"delta {tuple(delta.shape)} must match x {tuple(x.shape)}")
+    return w if w.dtype == torch.float32 else w.float()
+
+
+def _lo_ok(out_dtype, with_lo):
+    if with_lo and out_dtype != torch.bfloat16:
+        raise ValueError("the hi/lo pair output needs a bfloat16 output")
+    return with_lo
 
 
 def rms_norm(x, w, out_dtype=None):
     """RMSNorm of an fp32 tensor over its last dim with fp32 epsilon; output in out_dtype."""
-    _check(x, w)
+    w = _check(x, w)
     return RMSNormFn.apply(x.contiguous(), w, out_dtype or x.dtype)
 
 
-def rms_norm_residual(x, w, out_dtype=None):
-    """Returns (x, rms_norm(x, w)) where the first output carries x on as the
-    residual stream (one backward kernel for both uses of x)."""
-    _check(x, w)
-    return RMSNormResidualFn.apply(x.contiguous(), w, out_dtype or x.dtype)
+def rms_norm_residual(x, w, out_dtype=None, with_lo=False):
+    """Returns (x, rms_norm(x, w), pair) where the first output carries x on as
+    the residual stream (one backward kernel for both uses of x); pair is the
+    hi/lo buffer when with_lo (bf16 output; the second output is its hi half),
+    else None."""
+    w = _check(x, w)
+    out_dtype = out_dtype or x.dtype
+    return RMSNormResidualFn.apply(x.contiguous(), w, out_dtype, _lo_ok(out_dtype, with_lo))
 
 
-def add_rms_norm(x, delta, w, out_dtype=None):
-    """Returns (x + delta, rms_norm(x + delta, w)); x fp32, delta fp32 or bf16."""
-    _check(x, w, delta)
-    return AddRMSNormFn.apply(x.contiguous(), delta.contiguous(), w, out_dtype or x.dtype)
+def add_rms_norm(x, delta, w, out_dtype=None, with_lo=False):
+    """Returns (x + delta, rms_norm(x + delta, w), pair); x fp32, delta fp32 or
+    bf16; pair as in rms_norm_residual."""
+    w = _check(x, w, delta)
+    out_dtype = out_dtype or x.dtype
+    return AddRMSNormFn.apply(x.contiguous(), delta.contiguous(), w, out_dtype, _lo_ok(out_dtype, with_lo))

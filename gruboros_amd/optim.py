@@ -11,9 +11,14 @@ Per parameter, p holds y (the gradient-evaluation point) in train mode;
 state z is the base sequence and v the second moment. With step k (from 0),
 c = weight_k / sum(weight), weight_k = (k+1)^r * lr_max^weight_lr_power:
     v   <- b2 v + (1 - b2) g^2
-    u    = g / (sqrt(v / (1 - b2^(k+1))) + eps) + wd * y
-    y   <- (1 - c) y + c z  +  lr (b1 (1 - c) - 1) u
-    z   <- z - lr u
+    u    = g / (sqrt(v / bc) + eps) + wd * y
+    y   <- (1 - c) y + c z  +  lr_k (b1 (1 - c) - 1) u
+    z   <- z - lr_k u
+bias_correction selects the scalar schedule: "denominator" (default; the
+package's releases since late 2024): bc = 1 - b2^(k+1), lr_k = lr * warmup;
+"lr" (Algorithm 1 of the paper, the package's first releases): bc = 1,
+lr_k = lr * warmup * sqrt(1 - b2^(k+1)), so the average weights follow
+lr_k^2. The element-wise update is the same kernel either way.
 eval() moves p to x = (y - (1 - b1) z) / b1 and train() moves it back,
 exactly as the package's mode switch does.
 
@@ -54,10 +59,13 @@ class _TableBuffers:
 
 class AdamWScheduleFree(torch.optim.Optimizer):
     def __init__(self, params, lr=0.0025, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, warmup_steps=0,
-                 r=0.0, weight_lr_power=2.0):
+                 r=0.0, weight_lr_power=2.0, bias_correction="denominator"):
+        if bias_correction not in ("denominator", "lr"):
+            raise ValueError(f"bias_correction must be 'denominator' or 'lr', got {bias_correction!r}")
         defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, warmup_steps=warmup_steps, r=r,
                         k=0, train_mode=False, weight_sum=0.0, lr_max=-1.0, weight_lr_power=weight_lr_power)
         super().__init__(params, defaults)
+        self.bias_correction = bias_correction
         self._tables = {}
 
     @torch.no_grad()
@@ -97,6 +105,8 @@ class AdamWScheduleFree(torch.optim.Optimizer):
             sched = (k + 1) / warm if k < warm else 1.0
             bc2 = 1 - b2 ** (k + 1)
             lr = group["lr"] * sched
+            if self.bias_correction == "lr":
+                lr, bc2 = lr * bc2 ** 0.5, 1.0
             group["scheduled_lr"] = lr
             lr_max = group["lr_max"] = max(lr, group["lr_max"])
             weight = ((k + 1) ** group["r"]) * (lr_max ** group["weight_lr_power"])
@@ -138,6 +148,9 @@ class AdamWScheduleFree(torch.optim.Optimizer):
                                             group["weight_decay"], ckp1, y_lr, lr,
                                             stream_of(group["params"][0]))
                 check(rc, "mg_sf_adamw_step")
+                for p in group["params"]:
+                    if hasattr(p, "_mg_pair"):  # hi/lo pairs follow the new weights on next use
+                        del p._mg_pair
             del keep
             group["k"] = k + 1
         return loss

@@ -32,10 +32,18 @@ def _workspace(device, B, T, Di):
 
 def release_workspaces():
     """Free the cached look-back workspaces (they are re-made on demand)."""
-    L = lib()
-    for ws in _WORKSPACES.values():
-        L.mg_scan_workspace_release(ptr(ws))
     _WORKSPACES.clear()
+
+
+def check_workspaces():
+    """Synchronise and read the error word of every cached look-back workspace
+    (mg_scan_workspace_check); raises if a scan gave up a wait or found a bad
+    header. The kernels never hang on a bad workspace: they set the error word
+    and exit, and this is where the error surfaces."""
+    L = lib()
+    for (dev, sid, B, T, Di), ws in list(_WORKSPACES.items()):
+        rc = L.mg_scan_workspace_check(ptr(ws), stream_of(ws))
+        check(rc, f"scan workspace (device {dev}, B={B} T={T} Di={Di})")
 
 
 def _vec_ok(t: torch.Tensor) -> bool:
@@ -71,6 +79,7 @@ def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt=False):
 
 
 def _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0):
+    """dhidden, dgate: outputs with a shared layout (their strides are passed)."""
     B, T, Di = hidden.shape
     L = lib()
     dev = hidden.device
@@ -84,8 +93,9 @@ def _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0
     ws = _workspace(dev, B, T, Di)
     rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
                        ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1), ptr(ckpt),
-                       ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate), ptr(dh0),
-                       B, T, Di, ptr(ws), ws.numel(), stream_of(hidden))
+                       ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate),
+                       dhidden.stride(0), dhidden.stride(1), ptr(dh0), B, T, Di, ptr(ws), ws.numel(),
+                       stream_of(hidden))
     check(rc, "mg_scan_bwd")
     return dh0
 
@@ -99,12 +109,12 @@ class GateScanPacked(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, hg, h0):
+    def forward(ctx, hg, h0, out_dtype):
         ctx.set_materialize_grads(False)
         B, T, D2 = hg.shape
         Di = D2 // 2
         hidden, gate = hg[..., :Di], hg[..., Di:]
-        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, hg.dtype, need_ckpt=True)
+        h, h_last, ckpt = _launch_fwd(hidden, gate, h0, out_dtype or hg.dtype, need_ckpt=True)
         ctx.save_for_backward(hg, h0, h, ckpt)
         return h, h_last
 
@@ -114,12 +124,12 @@ class GateScanPacked(torch.autograd.Function):
         B, T, D2 = hg.shape
         Di = D2 // 2
         if dh is None and dh_last is None:
-            return None, None
+            return None, None, None
         dhg = torch.empty_like(hg, memory_format=torch.contiguous_format)
         want_dh0 = h0 is not None and ctx.needs_input_grad[1]
         dh0 = _launch_bwd(hg[..., :Di], hg[..., Di:], h0, h, ckpt, dh, dh_last, dhg[..., :Di], dhg[..., Di:],
                           want_dh0)
-        return dhg, (dh0.reshape(h0.shape) if want_dh0 else None)
+        return dhg, (dh0.reshape(h0.shape) if want_dh0 else None), None
 
 
 class GateScan(torch.autograd.Function):
@@ -163,12 +173,14 @@ def gate_scan(hidden, gate, prev_hidden=None):
     return GateScan.apply(hidden, gate, h0)
 
 
-def gate_scan_packed(hg, prev_hidden=None):
-    """minGRU gate math + scan on the packed projection output hg = [hidden | gate]."""
+def gate_scan_packed(hg, prev_hidden=None, out_dtype=None):
+    """minGRU gate math + scan on the packed projection output hg = [hidden | gate].
+    out_dtype: dtype of the hidden sequence (default hg's; float32 keeps the
+    scan state unrounded for the residual stream)."""
     require_cuda(hg, prev_hidden)
     if hg.dim() != 3 or hg.shape[-1] % 2:
         raise ValueError(f"hg must be [B,T,2*Di], got {tuple(hg.shape)}")
     hg = hg.contiguous()  # the gradient buffer is written with hg's strides
     B, T, D2 = hg.shape
     h0 = _prep_h0(prev_hidden, B, D2 // 2, hg.device)
-    return GateScanPacked.apply(hg, h0)
+    return GateScanPacked.apply(hg, h0, out_dtype)

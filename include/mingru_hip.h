@@ -13,7 +13,16 @@
  *     that may run concurrently.
  *   - Return 0 on success, a nonzero MG_ERR_* code otherwise; the message of
  *     the last failure on the calling thread is returned by mg_last_error().
- *   - dtype codes: MG_F32 = 0 (float), MG_BF16 = 1 (bfloat16, RNE rounding).
+ *   - dtype codes: MG_F32 = 0 (float), MG_BF16 = 1 (bfloat16).
+ *   - Rounding to bf16: round-to-nearest-even for activations and weights.
+ *     Gradients written in bf16 (mg_scan_bwd's dhidden/dgate,
+ *     mg_add_rmsnorm_bwd's ddelta, the loss heads' dlogits, mg_gelu_bwd's
+ *     dpre, mg_gemm's GELU-gradient epilogue) round stochastically: up with
+ *     probability equal to the dropped fraction of a bf16 ulp, from a hash of
+ *     the element's index and value (deterministic, no generator state).
+ *     Round-to-nearest errors of a near-uniform softmax's gradient repeat
+ *     across the rows of a label and add up in the weight gradients;
+ *     stochastic rounding keeps them unbiased.
  */
 #ifndef MINGRU_HIP_H
 #define MINGRU_HIP_H
@@ -33,6 +42,7 @@ extern "C" {
 #define MG_ERR_DTYPE 2    /* unsupported dtype combination */
 #define MG_ERR_WORKSPACE 3 /* workspace missing, too small or not initialised */
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
+#define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int mg_version(void);
@@ -71,17 +81,30 @@ const char* mg_last_error(void);
  * ---------------------------------------------------------------------- */
 size_t mg_scan_ckpt_elems(int B, int T, int Di);
 
-/* Look-back workspace (ticket counters and look-back words; serves both
- * directions). It is zero-filled once by mg_scan_workspace_init, on
- * `stream`, for one (B, T, Di); the kernels then keep it consistent from
- * call to call, so calls do no clearing of their own. Calls of that shape on
- * it must be ordered (one stream, or synchronised): concurrent calls need
- * separate workspaces. mg_scan_fwd/bwd refuse (MG_ERR_WORKSPACE) a workspace
- * not initialised for their shape. Memory that is freed and reused must be
- * initialised again; mg_scan_workspace_release forgets an address. */
+/* Look-back workspace (a header, ticket counters and look-back words; serves
+ * both directions). mg_scan_workspace_init zero-fills it on `stream` and
+ * writes the header for one (B, T, Di); the kernels then keep it consistent
+ * from call to call, so calls do no clearing of their own.
+ *
+ * One stream per workspace: the calls on a workspace must run one after the
+ * other (one stream, or ordered by events). Calls that may overlap need
+ * separate workspaces. The library keeps no record of workspaces: each
+ * kernel checks the header on the device. A workspace that was never
+ * initialised, was initialised for another shape, or was corrupted (for
+ * instance by overlapping calls) makes the kernel exit early. A look-back
+ * wait that stays unanswered for max_polls polls gives up. Either way the
+ * results are invalid and a bit is set in the header's error word, which
+ * mg_scan_workspace_check reads: it synchronises `stream` and returns
+ * MG_OK, MG_ERR_WORKSPACE (uninitialised or wrong shape), MG_ERR_STALL (a
+ * wait gave up; corrupted counters end this way, sometimes also drawing a
+ * ticket past the last tile) or MG_ERR_WORKSPACE for such a ticket alone.
+ * The error stays until the workspace is
+ * initialised again. mg_scan_workspace_set_max_polls changes the poll limit
+ * (default 2^22 polls, about a second; at least 1), on `stream`. */
 size_t mg_scan_workspace_bytes(int B, int T, int Di);
 int mg_scan_workspace_init(void* workspace, size_t workspace_bytes, int B, int T, int Di, void* stream);
-int mg_scan_workspace_release(void* workspace);
+int mg_scan_workspace_set_max_polls(void* workspace, uint32_t max_polls, void* stream);
+int mg_scan_workspace_check(const void* workspace, void* stream);
 
 int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
@@ -102,7 +125,10 @@ int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
  * else once per 4 steps from h, and rebuilt in fp32 in between.
  * dh: gradient of h, dtype out_dtype, element (b,t,d) at b*g_sb + t*g_ld + d.
  * dh_last (nullable): fp32 [B, Di], gradient of h_last, added to dh_{T-1}.
- * dhidden/dgate: same layout and dtype as hidden/gate (in_sb, in_ld).
+ * dhidden/dgate: dtype in_dtype, element (b,t,d) at b*d_sb + t*d_ld + d
+ *   (for the packed [B, T, 2*Di] gradient buffer: dhidden = base,
+ *   dgate = base + Di, d_ld = 2*Di, d_sb = T*2*Di). The caller's buffers
+ *   must hold every element so addressed.
  * dh0 (nullable): fp32 [B, Di]. */
 int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
@@ -111,7 +137,7 @@ int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
                 const float* ckpt,
                 const void* dh, int64_t g_sb, int64_t g_ld,
                 const float* dh_last,
-                void* dhidden, void* dgate, float* dh0,
+                void* dhidden, void* dgate, int64_t d_sb, int64_t d_ld, float* dh0,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
 
@@ -127,6 +153,10 @@ int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
  * Rows of D contiguous elements (D % 4 == 0, D <= 4096), N rows.
  * Forward:  xn = x + delta (delta nullable: xn = x, x_out unused),
  *           x_out = xn (fp32), y = xn * rstd * w (y_dtype), rstd[row] (nullable).
+ *           y and y_lo rows have stride ldy (>= D, % 4 == 0). y_lo (nullable,
+ *           bf16 y only) receives bf16(y_fp32 - y): with y it forms a hi/lo
+ *           pair equal to the fp32 value to ~2^-16 relative, the operand
+ *           form of mg_gemm's MG_GEMM_HILO products.
  * Backward: dx = rstd * (dy*w - xn*rstd * mean(dy*w * xn*rstd)) + dres
  *           (dres nullable), written to dx (fp32, nullable) and to ddelta
  *           (ddelta_dtype, nullable); dw = sum over rows of dy * xn * rstd
@@ -136,6 +166,7 @@ int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate,
  * ---------------------------------------------------------------------- */
 int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* delta,
                        const float* w, float* x_out, int y_dtype, void* y,
+                       void* y_lo, int64_t ldy,
                        float* rstd, int64_t N, int D, float eps, void* stream);
 
 size_t mg_add_rmsnorm_bwd_workspace_bytes(int64_t N, int D);
@@ -223,6 +254,14 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  * flags (bit set):
  *   MG_GEMM_ACCUMULATE (fp32 C, no epilogue): C += A B.
  *   MG_GEMM_DETERMINISTIC: never split along K.
+ *   MG_GEMM_HILO: fp32-accurate product of operands stored as bf16 hi/lo
+ *     pairs. A and B must both be K-contiguous; each row holds K hi values
+ *     followed by K lo values (x = hi + lo; lda, ldb >= 2K), as written by
+ *     mg_add_rmsnorm_fwd's y/y_lo or mg_split_hilo. Computes
+ *     A_hi B_hi + A_lo B_hi + A_hi B_lo in fp32 (three times the MFMA work;
+ *     the dropped A_lo B_lo term is ~2^-16 relative). Used where bf16
+ *     rounding of a product would move a result across the kink of the
+ *     reference's g(x) at 0 (the hidden half of to_hidden_and_gate, to_out).
  * Split along K: fp32 outputs with few output tiles are split along K over
  *   several workgroups when a workspace is given. Each writes its partial
  *   tile there and a second kernel adds the partials, in split order, into C
@@ -244,6 +283,7 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
 #define MG_EPI_GELU_GRAD 3
 #define MG_GEMM_ACCUMULATE 1
 #define MG_GEMM_DETERMINISTIC 2
+#define MG_GEMM_HILO 4
 
 int mg_gemm(int a_layout, const void* A, int64_t lda,
             int b_layout, const void* B, int64_t ldb,
@@ -253,6 +293,19 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
             void* workspace, size_t workspace_bytes, void* stream);
 size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
                                int c_dtype, int flags);
+
+/* fp32 -> bf16 hi/lo pairs for MG_GEMM_HILO operands: out[r, c] =
+ * bf16(x[r, c]) (RNE), out[r, cols + c] = bf16(x[r, c] - out[r, c]), for
+ * rows x cols (cols % 4 == 0; ldx >= cols, ldo >= 2 cols, both % 4 == 0;
+ * x 16-byte and out 8-byte aligned). No reference counterpart: it prepares
+ * the operands of the accurate forms of reference mingru/minGRU.py:45 and :71. */
+int mg_split_hilo(const float* x, int64_t ldx, int64_t rows, int cols, void* out, int64_t ldo, void* stream);
+
+/* fp32 -> bf16 with stochastic rounding (as the gradient stores, keyed by the
+ * element index and `salt`), n % 4 == 0 dense elements; x 16-byte and out
+ * 8-byte aligned. For an fp32 gradient that must enter a bf16 product (the
+ * backward of to_out, reference mingru/minGRU.py:71). */
+int mg_round_bf16_sr(const float* x, int64_t n, void* out, uint32_t salt, void* stream);
 
 /* ------------------------------------------------------------------------
  * Streaming loss head: logits GEMM + log-softmax + cross-entropy + gradient.
@@ -281,9 +334,10 @@ int mg_logits_cross_entropy(const void* embed, int64_t lde, const void* w, int64
  *
  * mg_column_sum: out[c] = sum_n x[n, c]  (x fp32 or bf16, row stride ld;
  *   out fp32 [C], written).
- * mg_gelu_bwd:   dpre[n, c] = bf16(dh[n, c] * gelu'(pre[n, c])) (bf16 in and
- *   out, gelu(x) = x/2 (1 + erf(x/sqrt 2))), and when dbias is given,
- *   dbias[c] = sum_n dpre[n, c] (of the bf16 values; fp32 [C], written).
+ * mg_gelu_bwd:   dpre[n, c] = bf16(dh[n, c] * gelu'(pre[n, c])) (dh fp32 or
+ *   bf16 per dh_dtype, pre and dpre bf16, gelu(x) = x/2 (1 + erf(x/sqrt 2))),
+ *   and when dbias is given, dbias[c] = sum_n dpre[n, c] (of the bf16
+ *   values; fp32 [C], written).
  * Both sum in a fixed order (reproducible) through a workspace of
  * mg_column_sum_workspace_bytes(N, C) bytes. C % 8 == 0, strides % 8 == 0,
  * 16-byte aligned pointers.
@@ -291,7 +345,7 @@ int mg_logits_cross_entropy(const void* embed, int64_t lde, const void* w, int64
 size_t mg_column_sum_workspace_bytes(int64_t N, int C);
 int mg_column_sum(int dtype, const void* x, int64_t ld, int64_t N, int C, float* out,
                   void* workspace, size_t workspace_bytes, void* stream);
-int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
+int mg_gelu_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
                 void* dpre, int64_t ld_out, float* dbias, int64_t N, int C,
                 void* workspace, size_t workspace_bytes, void* stream);
 
@@ -304,7 +358,7 @@ int mg_gelu_bwd(const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
  *   mg_decode_mingru: x = (tokens ? emb[tokens] : x_in) + pending (bf16,
  *     nullable); n = bf16(RMSNorm(x) * norm_w); [hidden | gate] = bf16(n W_hg^T)
  *     (W_hg bf16 [2D, D]); state = a state + z g(hidden) (fp32 [B, D], in
- *     place); x_out = x + bf16(state). Tokens are clamped into [0, V).
+ *     place); x_out = x + state. Tokens are clamped into [0, V).
  *   mg_decode_ff: n = bf16(RMSNorm(x) * norm_w); act = bf16(gelu(bf16(n W1^T
  *     + b1))) (W1 bf16 [F, D], b1 bf16 [F], act bf16 [B, F] scratch);
  *     pending_out = bf16(act W2^T + b2) (W2 bf16 [D, F], b2 bf16 [D]).

@@ -214,10 +214,14 @@ def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=Fals
     Returns (logits, next_prev_hiddens).
 
     bf16_points=True evaluates the same mathematics (in p's dtype) with every
-    tensor rounded to bf16 where a bf16-activation implementation with fp32
-    residual stream, fp32 scan state and fp32 logits stores it: the GEMM
-    weights and biases, the normalized block inputs, the GEMM, scan and GELU
-    outputs, and the gradients of all of those and of the logits."""
+    tensor rounded to bf16 where the build's bf16-activation path (fp32
+    residual stream, fp32 scan state, fp32 logits) stores it: the GEMM
+    weights and biases, the normalized block inputs, the GEMM and GELU
+    outputs, and the gradients of all of those and of the logits. Two
+    products are fp32-accurate there and stay unrounded here: the hidden half
+    of to_hidden_and_gate (its input n and weight rows) and to_out; the scan
+    output enters the residual stream (or to_out) in fp32. Its gradient is
+    rounded to bf16 on the way back, as the build's backward stores it."""
     r = _RoundBF16.apply if bf16_points else (lambda t: t)
     rg = _RoundGradBF16.apply if bf16_points else (lambda t: t)
     x = F.embedding(ids, p["token_emb.weight"])                            # :97
@@ -228,13 +232,17 @@ def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=Fals
         prev = next(hiddens, None)
         if prev is not None:
             prev = prev.to(x.dtype)
-        n = r(rms_norm(x, p[pre + "1.weight"]))                            # :121
-        hg = r(F.linear(n, r(p[pre + "2.to_hidden_and_gate.weight"])))     # minGRU.py:45
+        n = rg(rms_norm(x, p[pre + "1.weight"]))                           # :121
+        w_hg = p[pre + "2.to_hidden_and_gate.weight"]
+        di = w_hg.shape[0] // 2
+        hidden = F.linear(n, w_hg[:di])                                    # minGRU.py:45, hidden half (accurate)
+        gate = F.linear(r(n), r(w_hg[di:]))                                #   gate half (bf16 operands)
+        hg = r(torch.cat([hidden, gate], dim=-1))
         hidden, gate = hg.chunk(2, dim=-1)
         out, h_next = mingru_scan(hidden, gate, prev)
-        out = r(out)
+        out = rg(out)
         if expansion != 1.0:
-            out = r(F.linear(out, r(p[pre + "2.to_out.weight"])))          # minGRU.py:71
+            out = rg(F.linear(out, p[pre + "2.to_out.weight"]))            # minGRU.py:71 (accurate)
         x = out + x                                                        # :125
         nxt.append(h_next)
         n2 = r(rms_norm(x, p[pre + "3.weight"]))

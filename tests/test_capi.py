@@ -40,11 +40,11 @@ def test_every_declared_symbol_is_exported(L):
 
 def test_version_and_queries(L):
     assert L.mg_version() >= 100
-    # ticket counters per chain and direction (rounded to 256 B) + one 8-byte
-    # look-back word per (tile, channel) for the forward (128-step tiles) and
-    # the backward (64-step tiles)
-    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + (3 + 5) * 2 * 64 * 8
-    assert L.mg_scan_workspace_bytes(16, 8192, 2048) == 4096 + (64 + 128) * 16 * 2048 * 8
+    # a 256-byte header, ticket counters per chain and direction (rounded to
+    # 256 B) + one 8-byte look-back word per (tile, channel) for the forward
+    # (128-step tiles) and the backward (64-step tiles)
+    assert L.mg_scan_workspace_bytes(2, 300, 64) == 256 + 256 + (3 + 5) * 2 * 64 * 8
+    assert L.mg_scan_workspace_bytes(16, 8192, 2048) == 256 + 4096 + (64 + 128) * 16 * 2048 * 8
 
 
 def _fwd(L, **kw):
@@ -65,12 +65,37 @@ def test_argument_errors(L):
     assert _fwd(L, in_ld=66) == 1
     assert _fwd(L, hidden=18) == 1  # misaligned
     assert _fwd(L, out_dtype=1, in_dtype=0) == 2  # f32 -> bf16 not offered
-    # every argument valid, but the workspace was never initialised
-    assert _fwd(L) == 3
-    assert "not initialised" in L.mg_last_error().decode()
+    # (a workspace that was never initialised is refused by the kernel itself, on the
+    # device: tests/test_scan_gpu.py::test_workspace_errors_end_the_kernel)
     assert L.mg_scan_workspace_init(None, 1 << 20, 2, 8, 64, None) == 3
     assert L.mg_scan_workspace_init(16, 8, 2, 8, 64, None) == 3
     assert L.mg_scan_workspace_init(16, 1 << 20, 2, 8, 62, None) == 1
+    assert L.mg_scan_workspace_check(None, None) == 1
+    assert L.mg_scan_workspace_set_max_polls(None, 5, None) == 1
+    assert L.mg_scan_workspace_set_max_polls(16, 0, None) == 1
+    # backward output strides are checked like the inputs'
+    bwd = dict(in_dtype=1, hidden=16, gate=16, in_sb=1024, in_ld=64, h0=None, out_dtype=1, h=16, out_sb=512,
+               out_ld=64, ckpt=None, dh=16, g_sb=512, g_ld=64, dh_last=None, dhid=16, dgat=16, d_sb=512, d_ld=66,
+               dh0=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
+    assert L.mg_scan_bwd(*bwd.values()) == 1 and b"dhidden" in L.mg_last_error()
+
+
+def test_hilo_and_norm_argument_errors(L):
+    # hi/lo products need K-contiguous operands and K >= 1; rows must hold 2K values
+    g = dict(al=0, A=16, lda=128, bl=0, B=16, ldb=128, M=64, N=64, K=64, epi=0, bias=None, aux=None, ldaux=0,
+             cd=0, C=16, ldc=64, flags=4, ws=None, wsb=0, stream=None)
+    assert L.mg_gemm(*{**g, "al": 1}.values()) == 1 and b"K-contiguous" in L.mg_last_error()
+    assert L.mg_gemm(*{**g, "K": 0}.values()) == 1
+    assert L.mg_gemm(*{**g, "lda": 64}.values()) == 1 and b"leading dimension" in L.mg_last_error()
+    assert L.mg_gemm(*{**g, "flags": 64}.values()) == 1
+    assert L.mg_split_hilo(16, 8, 4, 6, 16, 16, None) == 1  # cols % 4
+    assert L.mg_split_hilo(16, 8, 4, 8, 16, 8, None) == 1   # ldo < 2 cols
+    assert L.mg_split_hilo(20, 8, 4, 8, 16, 16, None) == 1  # x misaligned
+    eps = ctypes.c_float(1e-7)
+    n = dict(x=16, ddt=0, delta=None, w=16, x_out=None, ydt=1, y=16, y_lo=None, ldy=60, rstd=None, N=4, D=64, eps=eps,
+             stream=None)
+    assert L.mg_add_rmsnorm_fwd(*n.values()) == 1 and b"ldy" in L.mg_last_error()
+    assert L.mg_add_rmsnorm_fwd(*{**n, "ldy": 128, "ydt": 0, "y_lo": 16}.values()) == 2  # lo needs a bf16 y
 
 
 def test_decode_argument_errors(L):

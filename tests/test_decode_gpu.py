@@ -100,3 +100,37 @@ def test_decoder_graph_replays_the_launches():
         assert torch.equal(a, b), i
         for x, y in zip(eager.hiddens(), graph.hiddens()):
             assert torch.equal(x, y), i
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_decoder_matches_fp64_oracle_cfg3_shape(B):
+    """Decoder.prefill + Decoder.step at the cfg3 model shape (d1024 L8 ff4,
+    expansion 1.0) against the fp64 restatement of the reference's generation
+    calls (oracle.minlm_forward with return_loss=False: the prompt's parallel
+    forward, then one token per call with prev_hiddens, reference
+    generate.py:184-207, mingru/minLM.py:101-102, minGRU.py:47-52) on the same
+    parameters: logits and per-layer states within 2e-2 (bf16 weights and
+    activations against unrounded fp64) over 8 generated tokens."""
+    from gruboros_amd.decode import Decoder
+    from oracle import mingru_oracle as O
+
+    m = _model(dim=1024, depth=8, seed=5)
+    with torch.no_grad():
+        for layer in m.layers:  # FF2 at a scale that keeps the blocks' outputs comparable
+            layer[4][2].weight.normal_(0, 0.02 / 32)
+    sd = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    gen = torch.Generator(device=DEV).manual_seed(11 + B)
+    prompt = torch.randint(0, 256, (B, 17), device=DEV, generator=gen)
+    dec = Decoder(m, B)
+    with torch.no_grad():
+        last = dec.prefill(prompt)
+        ref_logits, ref_hid = O.minlm_forward(sd, prompt.cpu(), 8, return_loss=False)
+        assert _rel(last, ref_logits[:, -1]) < 2e-2
+        for step in range(8):
+            tok = torch.randint(0, 256, (B,), device=DEV, generator=gen)
+            got = dec.step(tok)
+            ref_logits, ref_hid = O.minlm_forward(sd, tok[:, None].cpu(), 8, return_loss=False, prev_hiddens=ref_hid)
+            e_l = _rel(got, ref_logits[:, -1])
+            e_h = max(_rel(a, b) for a, b in zip(dec.hiddens(), ref_hid))
+            print(f"decode vs fp64 B={B} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
+            assert e_l < 2e-2 and e_h < 2e-2

@@ -226,3 +226,50 @@ def test_feed_forward_bf16_matches_fp64(fused_fwd, fused_bwd, monkeypatch):
                       (ff[2].weight.grad, w2.grad), (ff[2].bias.grad, b2.grad)):
         assert got.dtype == (torch.bfloat16 if got is x.grad else torch.float32)
         assert _rel(got, want) < 2e-2
+
+
+def test_split_hilo_matches_torch_rounding():
+    from gruboros_amd.gemm import split_hilo
+
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(77, 136, device=DEV, generator=gen) * torch.logspace(-6, 6, 136, device=DEV)
+    pair = split_hilo(x)
+    hi = x.to(torch.bfloat16)
+    lo = (x - hi.float()).to(torch.bfloat16)
+    assert torch.equal(pair[:, :136], hi) and torch.equal(pair[:, 136:], lo)
+    err = (pair[:, :136].double() + pair[:, 136:].double() - x.double()).abs()
+    assert bool((err <= x.double().abs() * 2.0 ** -16).all())
+
+
+@pytest.mark.parametrize("M,N,K,out_dtype", [(300, 200, 136, torch.float32), (16376, 1024, 1024, torch.bfloat16),
+                                              (16376, 1024, 1536, torch.float32), (1000, 96, 72, torch.float32)])
+def test_hilo_product_is_fp32_accurate(M, N, K, out_dtype):
+    """MG_GEMM_HILO from fp32 operands split into hi/lo pairs: the fp32 result
+    is within 2e-5 (norm-relative; expected ~7e-6 from the pair's 2^-16
+    representation error and the dropped lo*lo term) of the fp64 product of
+    the fp32 operands, where a plain bf16 product of the same operands is
+    ~3e-3 off; bf16
+    outputs are one rounding of that value. Shapes: ragged, the cfg3 hidden
+    half (written into the packed [N, 2 Di] projection buffer), the cfg3
+    expansion-1.5 to_out (fp32 out), and a small K."""
+    from gruboros_amd.gemm import KCONTIG, gemm, linear_fwd_hilo, split_hilo
+
+    gen = torch.Generator(device=DEV).manual_seed(M + N + K)
+    a = torch.randn(M, K, device=DEV, generator=gen)
+    b = torch.randn(N, K, device=DEV, generator=gen) * 0.02
+    ref = (a.double() @ b.double().t()).cpu()
+    buf = torch.full((M, 2 * N), 3.0, device=DEV, dtype=out_dtype)
+    out = buf[:, :N]
+    linear_fwd_hilo(split_hilo(a), split_hilo(b), out, K)
+    plain = torch.empty(M, N, device=DEV)
+    gemm(a.to(torch.bfloat16), KCONTIG, b.to(torch.bfloat16), KCONTIG, M, N, K, plain)
+    torch.cuda.synchronize()
+    e_plain = _rel(plain, ref)
+    if out_dtype == torch.float32:
+        e = _rel(out, ref)
+        print(f"hilo {M}x{N}x{K}: {e:.2e} (plain bf16 {e_plain:.2e})", flush=True)
+        assert e <= 2e-5 and e_plain > 1e-3
+    else:
+        got = out.double().cpu()
+        assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+    assert bool((buf[:, N:] == 3.0).all())  # the other half of the packed buffer is untouched

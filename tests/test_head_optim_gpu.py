@@ -80,17 +80,21 @@ def test_cross_entropy_flags_bad_labels():
     assert int(bad) == 1
 
 
+@pytest.mark.parametrize("form", ["denominator", "lr"])
 @pytest.mark.parametrize("wd", [0.0, 0.01])
-def test_sf_adamw_fused_matches_restatement(wd):
+def test_sf_adamw_fused_matches_restatement(wd, form):
+    """Both scalar schedules: the package's ("denominator") and Algorithm 1 of
+    the paper ("lr"; the restatement of that form is pinned to Algorithm 1 by
+    tests/test_oracle_sf.py)."""
     from gruboros_amd.optim import AdamWScheduleFree
 
     torch.manual_seed(1)
     shapes = [(1000, 33), (257,), (4, 4), (8192, 3), (7,)]
     ps = [torch.nn.Parameter(torch.randn(s, device=DEV)) for s in shapes]
     ref_ps = [p.detach().double().cpu().clone() for p in ps]
-    opt = AdamWScheduleFree(ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2)
+    opt = AdamWScheduleFree(ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2, bias_correction=form)
     opt.train()
-    ref = S.RefAdamWScheduleFree(ref_ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2)
+    ref = S.RefAdamWScheduleFree(ref_ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=wd, warmup_steps=2, form=form)
     for step in range(5):
         grads = [torch.randn(s, device=DEV) for s in shapes]
         for p, g in zip(ps, grads):
@@ -194,3 +198,27 @@ def test_column_sum_and_gelu_backward(N, C):
     assert _rel(dpre, p64.grad) < 4e-3
     # the bias gradient sums the rounded dpre values
     assert (db.double() - dpre.double().sum(0)).abs().max() <= 1e-5 * (dpre.double().abs().sum(0).max() + 1)
+
+
+def test_gradient_rounding_is_stochastic_and_deterministic():
+    """bf16 gradient stores round stochastically (as mg_gelu_bwd's dpre does):
+    4 M equal fp32 values 0.3 ulp above a bf16 value round up in 30% of the
+    elements (round-to-nearest would round all of them down), so the mean
+    keeps the fp32 value; the result is a function of the inputs (a second
+    call gives the same bits); values that are bf16 already stay exact."""
+    from gruboros_amd.linear import gelu_backward
+
+    N, C = 4096, 1024
+    v = 1.0 + 0.3 * 2.0 ** -7  # bf16 spacing at 1.0 is 2^-7
+    dh = torch.full((N, C), v, device=DEV)
+    pre = torch.full((N, C), 8.0, device=DEV, dtype=torch.bfloat16)  # gelu'(8) = 1 in fp32
+    dpre, _ = gelu_backward(dh, pre, want_bias_grad=False)
+    vals = dpre.float()
+    assert set(vals.unique().tolist()) == {1.0, 1.0 + 2.0 ** -7}
+    frac_up = float((vals > 1.0).float().mean())
+    assert abs(frac_up - 0.3) < 0.005, frac_up
+    assert abs(float(vals.double().mean()) - v) < 1e-5
+    again, _ = gelu_backward(dh, pre, want_bias_grad=False)
+    assert torch.equal(again, dpre)
+    exact, _ = gelu_backward(torch.full((N, C), 1.0 + 2.0 ** -7, device=DEV), pre, want_bias_grad=False)
+    assert bool((exact.float() == 1.0 + 2.0 ** -7).all())

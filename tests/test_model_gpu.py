@@ -4,17 +4,20 @@ and mingru/minLM.py, with one shared state dict.
 
 Tolerances (gradients norm-relative, per parameter tensor):
   * fp32 activations: 1e-4 against the float64 oracle.
-  * bf16 activations (fp32 master weights, fp32 scan state, residual stream
-    and logits): 2e-2 against the float64 oracle evaluated with bf16 rounding
-    at the same tensors (oracle minlm_core(bf16_points=True)): that is the
-    parity check of the kernels. Against the unrounded float64 oracle the
-    loss and hidden states stay within 2e-2, the gradients within 6e-2: bf16
-    storage itself moves the gradients of this small randomly initialised
-    model by 2-5% (the emulation reproduces it; rounding only the GEMM
-    weights to bf16 accounts for 3.5e-2 of it). For scale, the reference
-    formulation evaluated purely in bf16 (what reference generate.py does) is
-    off by ~650% on the same gradients, and in fp32 by ~1e-4.
+  * bf16 activations (fp32 master weights; fp32 scan state, residual stream
+    and logits; fp32-accurate hidden projection and to_out): 2e-2 against
+    the plain float64 oracle for the loss, the hidden states and every
+    parameter gradient. Also 2e-2 against the float64 oracle evaluated with
+    bf16 rounding where the build stores bf16 (minlm_core(bf16_points=True)).
+    Why the accurate products: the reference's g(x) has a kink at 0 (g'
+    jumps from 1/4 to 1), so bf16 rounding of the hidden pre-activations
+    flips ~0.2% of their signs and moved the to_hidden_and_gate and norm
+    gradients by 3-5% (measured on the fp64 restatement). For scale, the
+    reference formulation evaluated purely in bf16 is off by ~650% on the
+    same gradients.
 """
+import math
+
 import pytest
 import torch
 
@@ -85,7 +88,7 @@ def test_minlm_loss_and_grads(dtype, expansion):
     if dtype == torch.float32:
         assert e_loss <= 1e-4 and e_hid <= 1e-4 and worst[0] <= 1e-4
     else:
-        assert e_loss <= 2e-2 and e_hid <= 2e-2 and worst[0] <= 6e-2
+        assert e_loss <= 2e-2 and e_hid <= 2e-2 and worst[0] <= 2e-2
         e_loss, e_hid, worst = errors(*oracle(True))
         print(f"{dtype} exp={expansion} vs fp64 with bf16 rounding points: loss {e_loss:.2e}, hiddens {e_hid:.2e}, "
               f"worst grad {worst[0]:.2e} ({worst[1]})", flush=True)
@@ -263,3 +266,137 @@ def _checkpoint_resume(config, batches, make, train):
         assert losses == losses_a
         for (n, pa), pb in zip(a.named_parameters(), m.parameters()):
             assert torch.equal(pb, pa), n
+
+
+def _oracle_fp64_on_device(sd, ids, depth, expansion=1.0):
+    """The fp64 restatement of reference mingru/minLM.py:86-155 with plain torch
+    ops on the GPU (float64 everywhere, no library of this build), loss and
+    gradients by autograd."""
+    p = {k: v.detach().to(DEV, torch.float64).requires_grad_(True) for k, v in sd.items()}
+    loss, hid = O.minlm_forward(p, ids, depth, return_loss=True, expansion=expansion, dtype=torch.float64)
+    loss.backward()
+    return float(loss), [h.detach() for h in hid], {k: v.grad for k, v in p.items()}
+
+
+def test_cfg3_training_step_matches_fp64_oracle():
+    """The north-star step at its real size: minLM d1024
+    L8 ff4 expansion 1.0, batch 8 x 2048 byte ids (uniform, seed 0), bf16
+    activations: forward with return_loss (reference mingru/minLM.py:86-155),
+    backward, and one Schedule-Free AdamW step (train.py:795-808, lr 1e-3,
+    betas (0.9, 0.999), wd 0.01). One shared state dict (the reference init's
+    scales with non-zero second FF weights, so every block contributes).
+    Checks, against the fp64 restatement evaluated with plain torch ops on the
+    device: loss, per-layer next_prev_hiddens and every parameter gradient
+    within 2e-2 (norm-relative); the optimizer step against the fp64
+    restatement of the step on the same gradients: second moments within
+    1e-6, parameter updates within 2e-4 (an fp32 master near 1.0, the norm
+    weights, holds a 1e-3 update to ~6e-5 relative: its spacing there is
+    6e-8; a wrong formula is off by O(1))."""
+    from gruboros_amd.optim import AdamWScheduleFree
+    from oracle import sf_adamw as SF
+
+    torch.cuda.empty_cache()
+    m, sd = _model(1024, 8, 1.0, torch.bfloat16, seed=0)
+    ids = torch.randint(0, 256, (8, 2048), device=DEV, generator=torch.Generator(device=DEV).manual_seed(0))
+    opt = AdamWScheduleFree(m.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    opt.train()
+    loss, hid = m(ids, return_loss=True, return_prev_hiddens=True)
+    loss.backward()
+    p0 = {n: p.detach().double().clone() for n, p in m.named_parameters()}
+    g0 = {n: p.grad.detach().double().clone() for n, p in m.named_parameters()}
+    opt.step()
+    torch.cuda.synchronize()
+
+    ref_loss, ref_hid, ref_grad = _oracle_fp64_on_device(sd, ids, 8)
+    e_loss = abs(float(loss) - ref_loss) / abs(ref_loss)
+    e_hid = max(_rel(a, b) for a, b in zip(hid, ref_hid))
+    errs = sorted(((_rel(g0[n], ref_grad[n]), n) for n in g0), reverse=True)
+    print(f"cfg3 step vs fp64: loss {float(loss):.6f} vs {ref_loss:.6f} ({e_loss:.2e}), hiddens {e_hid:.2e}, "
+          f"worst grads {[(f'{e:.2e}', n) for e, n in errs[:3]]}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2
+    assert errs[0][0] <= 2e-2, errs[:3]
+
+    ref_opt = SF.RefAdamWScheduleFree([p0[n].clone() for n in p0], lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    ref_opt.step([g0[n] for n in p0])
+    worst = worst_v = 0.0
+    for i, ((n, p), pr) in enumerate(zip(m.named_parameters(), ref_opt.params)):
+        worst = max(worst, _rel(p.detach().double() - p0[n], pr - p0[n]))
+        worst_v = max(worst_v, _rel(opt.state[p]["exp_avg_sq"], ref_opt.v[i]))
+    print(f"cfg3 SF-AdamW vs fp64 restatement: update {worst:.2e}, second moment {worst_v:.2e}", flush=True)
+    assert worst <= 2e-4 and worst_v <= 1e-6
+
+
+def test_cfg5_micro_steps_and_accumulation():
+    """cfg5: minLM d2048 L24 ff4 expansion 1.0 (1.008 B
+    parameters), bf16, batch 4 x 4096, gradient accumulation 4
+    (train.py:795-808: loss / grad_accum, backward per micro-step). From the
+    product's own seeded init: loss ~ ln 256 at init, finite gradients, and the
+    four accumulated micro-step gradients equal the gradient of the one
+    16 x 4096 batch (mean loss) within 1e-2."""
+    from gruboros_amd.mingru.minLM import minLM
+
+    torch.cuda.empty_cache()
+    torch.manual_seed(0)
+    m = minLM(num_tokens=256, dim=2048, depth=24, ff_mult=4, expansion=1.0, compute_dtype=torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        for layer in m.layers:  # non-zero second FF weights: every block contributes to the gradients
+            layer[4][2].weight.normal_(0, 0.02 / 45.0)
+    ids = torch.randint(0, 256, (16, 4096), device=DEV, generator=torch.Generator(device=DEV).manual_seed(0))
+    losses = []
+    for i in range(4):
+        loss = m(ids[4 * i:4 * i + 4], return_loss=True)
+        (loss / 4).backward()
+        losses.append(float(loss.detach()))
+    acc = {n: p.grad.detach().clone() for n, p in m.named_parameters()}
+    print(f"cfg5 micro-step losses {losses} (ln 256 = {math.log(256):.4f})", flush=True)
+    assert all(abs(x - math.log(256)) < 0.05 for x in losses)
+    assert all(bool(torch.isfinite(g).all()) for g in acc.values())
+    m.zero_grad(set_to_none=True)
+    big = m(ids, return_loss=True)
+    big.backward()
+    assert abs(float(big) - sum(losses) / 4) <= 1e-4 * abs(float(big))
+    errs = sorted(((_rel(acc[n], p.grad), n) for n, p in m.named_parameters() if p.grad.norm() > 0), reverse=True)
+    print(f"cfg5 accumulated vs one batch: worst {errs[:2]}", flush=True)
+    assert errs[0][0] <= 1e-2
+    del m, acc
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("cast", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_generate_py_load_and_decode_path(cast):
+    """Reference generate.py:126-144 then :184-207, as written there: build
+    minLM from the checkpoint's model_config, load_state_dict, .eval(), cast
+    the whole model (.to(torch.bfloat16) by default, .to(torch.float16) with
+    --use-fp16), .to(device); then one parallel forward over the prompt with
+    return_prev_hiddens=True and single-token calls carrying prev_hiddens.
+    Checked per step against the fp64 restatement evaluated on the same cast
+    parameter values (the cast model's parameters are what it computes with):
+    logits and hiddens within 2e-2 (bf16 activations) / 5e-3 (fp16 products,
+    fp32 kernels)."""
+    from gruboros_amd.mingru.minLM import minLM
+
+    cfg = {"num_tokens": 256, "dim": 128, "depth": 2, "ff_mult": 4.0, "expansion": 1.5, "enable_conv": False,
+           "dropout": 0.0}
+    _, sd = _model(128, 2, 1.5, torch.float32, seed=4)
+    model = minLM(**cfg)
+    model.load_state_dict(sd)
+    model = model.eval()
+    model = model.to(cast)
+    model = model.to(DEV)
+    p_cast = {k: v.to(cast).double() for k, v in sd.items()}
+    prompt = torch.randint(0, 256, (1, 40), generator=torch.Generator().manual_seed(3))
+    tol = 2e-2 if cast == torch.bfloat16 else 5e-3
+    with torch.no_grad():
+        logits, hidden_states = model(prompt.to(DEV), return_prev_hiddens=True)
+        ref_logits, ref_hid = O.minlm_forward(p_cast, prompt, 2, return_loss=False, expansion=1.5)
+        assert _rel(logits[:, -1], ref_logits[:, -1]) <= tol
+        prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)
+        for step in range(8):
+            logits, hidden_states = model(prev_token, return_prev_hiddens=True, prev_hiddens=hidden_states)
+            ref_logits, ref_hid = O.minlm_forward(p_cast, prev_token.cpu(), 2, return_loss=False,
+                                                  prev_hiddens=ref_hid, expansion=1.5)
+            e_l = _rel(logits[:, -1], ref_logits[:, -1])
+            e_h = max(_rel(a, b) for a, b in zip(hidden_states, ref_hid))
+            print(f"{cast} step {step}: logits {e_l:.2e} hiddens {e_h:.2e}", flush=True)
+            assert e_l <= tol and e_h <= tol
+            prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)

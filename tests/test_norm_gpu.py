@@ -40,7 +40,7 @@ def test_add_rmsnorm_parity(shape, delta_dtype, out_dtype):
         y = rms_norm(xg, wg, out_dtype)
         (y.float() * dy.to(DEV)).sum().backward()
     else:
-        xo, y = add_rms_norm(xg, dg, wg, out_dtype)
+        xo, y, _ = add_rms_norm(xg, dg, wg, out_dtype)
         ((y.float() * dy.to(DEV)).sum() + (xo * dres.to(DEV)).sum()).backward()
     assert y.dtype == out_dtype
 
@@ -77,3 +77,31 @@ def test_rmsnorm_matches_torch_module_fp32():
     ref = m(x)
     out = rms_norm(x, m.weight, torch.float32)
     torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(3, 5, 64), (4, 33, 1024), (2, 9, 2048)])
+def test_norm_hilo_pair(shape):
+    """with_lo: the bf16 output comes as the hi half of a [.., 2D] buffer whose
+    lo half holds bf16(y - hi); hi equals the plain bf16 output bit for bit and
+    hi + lo is within 2^-15 of the fp64 norm (the fp32 kernel value to ~2^-16)."""
+    from gruboros_amd.norm import add_rms_norm, rms_norm_residual
+
+    gen = torch.Generator().manual_seed(sum(shape))
+    D = shape[-1]
+    x = (torch.randn(shape, generator=gen) * 1e-3).to(DEV)
+    w = torch.randn(D, generator=gen).to(DEV)
+    delta = (torch.randn(shape, generator=gen) * 1e-3).to(torch.bfloat16).to(DEV)
+    for with_delta in (False, True):
+        if with_delta:
+            xo, y, pair = add_rms_norm(x, delta, w, torch.bfloat16, with_lo=True)
+            _, y_plain, none = add_rms_norm(x, delta, w, torch.bfloat16)
+            xn = x.double() + delta.double()
+        else:
+            xo, y, pair = rms_norm_residual(x, w, torch.bfloat16, with_lo=True)
+            _, y_plain, none = rms_norm_residual(x, w, torch.bfloat16)
+            xn = x.double()
+        assert none is None and pair.shape == (*shape[:-1], 2 * D)
+        assert torch.equal(y, pair[..., :D]) and torch.equal(y, y_plain)
+        ref = O.rms_norm(xn, w.double())
+        err = (pair[..., :D].double() + pair[..., D:].double() - ref).abs()
+        assert bool((err <= ref.abs() * 2.0 ** -15 + 1e-30).all())

@@ -55,3 +55,73 @@ def test_x_is_the_average_iterate():
         x = (1 - c) * x + c * opt.z[0]
         # the iterate p is y = (1 - b1) z + b1 x
     torch.testing.assert_close(p, (1 - 0.9) * opt.z[0] + 0.9 * x, rtol=1e-10, atol=1e-12)
+
+
+def _algorithm1(p0, grads, lr, b1, b2, eps, wd, warmup=0):
+    """Algorithm 1 of Defazio et al. (2024), "The Road Less Scheduled", for one
+    scalar, written out as the paper states it (x, z, y sequences, t from 1):
+      y_t = (1 - b1) z_t + b1 x_t;  g_t = grad at y_t
+      v_t = b2 v_{t-1} + (1 - b2) g_t^2
+      gamma_t = lr sqrt(1 - b2^t) min(1, t / warmup)
+      z_{t+1} = z_t - gamma_t g_t / (sqrt(v_t) + eps) - gamma_t wd y_t
+      c_{t+1} = gamma_t^2 / sum_{i <= t} gamma_i^2
+      x_{t+1} = (1 - c_{t+1}) x_t + c_{t+1} z_{t+1}
+    grads: callable y -> gradient. Returns the list of y_{t+1}."""
+    x = z = p0
+    v = 0.0
+    gsum = 0.0
+    ys = []
+    for t in range(1, len(grads) + 1):
+        y = (1 - b1) * z + b1 * x
+        g = grads[t - 1](y)
+        v = b2 * v + (1 - b2) * g * g
+        gamma = lr * math.sqrt(1 - b2 ** t) * (min(1.0, t / warmup) if warmup else 1.0)
+        z = z - gamma * g / (math.sqrt(v) + eps) - gamma * wd * y
+        gsum += gamma * gamma
+        c = gamma * gamma / gsum
+        x = (1 - c) * x + c * z
+        ys.append((1 - b1) * z + b1 * x)
+    return ys
+
+
+def test_paper_algorithm1_three_steps_by_hand():
+    """The restatement's "lr" form equals Algorithm 1 step by step. The
+    gradients depend on the point y (g = 3 y - 1 + a step constant), so a
+    wrong evaluation point, a dropped weight-decay term, a wrong c or a wrong
+    bias correction changes the sequence. The first step is also checked
+    against its value derived by hand: v_1 = (1 - b2) g_1^2 and c_2 = 1, so
+    y_2 = z_2 = p0 - gamma_1 (g_1 / (sqrt(1 - b2) |g_1| + eps) + wd p0) with
+    gamma_1 = lr sqrt(1 - b2), i.e. about p0 - lr (sign(g_1) + sqrt(1 - b2) wd p0)."""
+    lr, b1, b2, eps, wd = 0.05, 0.9, 0.999, 1e-8, 0.1
+    p0 = 0.7
+    grads = [lambda y: 3 * y - 1, lambda y: 3 * y - 0.5, lambda y: -2 * y + 0.25]
+    ys = _algorithm1(p0, grads, lr, b1, b2, eps, wd)
+    g1 = 3 * p0 - 1
+    y2 = p0 - lr * math.sqrt(1 - b2) * (g1 / (math.sqrt(1 - b2) * abs(g1) + eps) + wd * p0)
+    assert math.isclose(ys[0], y2, rel_tol=1e-14)
+    # restatement, one tensor, "lr" form
+    p = torch.tensor([p0], dtype=torch.float64)
+    opt = S.RefAdamWScheduleFree([p], lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd, form="lr")
+    for t, grad in enumerate(grads):
+        opt.step([torch.tensor([grad(float(p))], dtype=torch.float64)])
+        assert math.isclose(float(p), ys[t], rel_tol=1e-12), (t, float(p), ys[t])
+    # the averaging weights of the "lr" form are gamma_t^2: c_3 = (1 - b2^2) / ((1 - b2) + (1 - b2^2))
+    _, _, c2, _, lm, ws = S.sf_scalars(0, lr, b1, b2, form="lr")
+    _, _, c3, _, _, _ = S.sf_scalars(1, lr, b1, b2, lr_max=lm, weight_sum=ws, form="lr")
+    assert math.isclose(c2, 1.0) and math.isclose(c3, (1 - b2 ** 2) / ((1 - b2) + (1 - b2 ** 2)), rel_tol=1e-12)
+
+
+def test_package_form_differs_from_algorithm1():
+    """The default ("denominator") form is not Algorithm 1: after the first
+    step they part (uniform c = 1/2 against gamma-weighted c, and the eps
+    term scaled differently), so the pin above would catch a silent switch."""
+    lr, b1, b2, eps, wd = 0.05, 0.9, 0.999, 1e-8, 0.1
+    grads = [lambda y: 3 * y - 1, lambda y: 3 * y - 0.5, lambda y: -2 * y + 0.25]
+    ys = _algorithm1(0.7, grads, lr, b1, b2, eps, wd)
+    p = torch.tensor([0.7], dtype=torch.float64)
+    opt = S.RefAdamWScheduleFree([p], lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd, form="denominator")
+    got = []
+    for grad in grads:
+        opt.step([torch.tensor([grad(float(p))], dtype=torch.float64)])
+        got.append(float(p))
+    assert abs(got[2] - ys[2]) > 1e-4

@@ -205,3 +205,122 @@ def test_workspace_reuse_across_calls():
         for x, y in zip(got, fresh):
             assert (x is None and y is None) or torch.equal(x, y), (B, T, Di, dt, s)
         _check(got, _oracle(*args), dt, f"reuse {B}x{T}x{Di} seed {s}")
+
+
+def _capi_fwd(L, hd, gt, h, ws, B, T, Di, ckpt=None):
+    from gruboros_amd import _lib
+
+    P = _lib.ptr
+    return L.mg_scan_fwd(1, P(hd), P(gt), T * Di, Di, None, 1, P(h), T * Di, Di, None, P(ckpt), B, T, Di, P(ws),
+                         ws.numel(), _lib.stream_of(hd))
+
+
+def _capi_bwd(L, hd, gt, h, dh, dhid, dgat, ws, B, T, Di):
+    from gruboros_amd import _lib
+
+    P = _lib.ptr
+    return L.mg_scan_bwd(1, P(hd), P(gt), T * Di, Di, None, 1, P(h), T * Di, Di, None, P(dh), T * Di, Di, None,
+                         P(dhid), P(dgat), T * Di, Di, None, B, T, Di, P(ws), ws.numel(), _lib.stream_of(hd))
+
+
+def test_workspace_errors_end_the_kernel():
+    """Misused look-back workspaces end the kernels with an error word, not a
+    wait without end, and mg_scan_workspace_check reports them:
+      * a workspace that was never initialised (its header is not there): every
+        workgroup returns at once;
+      * one initialised for another shape: the same;
+      * one whose ticket counters were corrupted (set to 1, as overlapping calls
+        on one workspace could leave them), so every chain waits on a word that
+        is never published: run with a poll limit of 64 (set from the host) so
+        every wait ends after 64 polls, in both directions.
+    After mg_scan_workspace_init the same memory gives bit for bit the results
+    of a fresh workspace."""
+    from gruboros_amd import _lib
+
+    L, P = _lib.lib(), _lib.ptr
+    B, T, Di = 2, 1024, 128  # 8 forward / 16 backward tiles per chain, 4 chains
+    hidden, gate, _, dh, _ = _make(B, T, Di, torch.bfloat16, False, seed=3)
+    hd, gt, dhd = hidden.to(DEV), gate.to(DEV), dh.to(DEV)
+    h = torch.empty_like(hd)
+    dhid, dgat = torch.empty_like(hd), torch.empty_like(hd)
+    need = L.mg_scan_workspace_bytes(B, T, Di)
+    ws = torch.zeros(need + 65536, dtype=torch.uint8, device=DEV)
+    st = _lib.stream_of(hd)
+    ncb = B * Di // 64
+
+    print("case: never initialised", flush=True)
+    assert _capi_fwd(L, hd, gt, h, ws, B, T, Di) == 0
+    assert L.mg_scan_workspace_check(P(ws), st) == 3 and b"never initialised" in L.mg_last_error()
+
+    print("case: initialised for another shape", flush=True)
+    assert L.mg_scan_workspace_init(P(ws), ws.numel(), B, T // 2, Di, st) == 0
+    assert _capi_fwd(L, hd, gt, h, ws, B, T, Di) == 0
+    assert _capi_bwd(L, hd, gt, h, dhd, dhid, dgat, ws, B, T, Di) == 0
+    assert L.mg_scan_workspace_check(P(ws), st) == 3 and b"another shape" in L.mg_last_error()
+
+    for direction in ("forward", "backward"):
+        print(f"case: corrupted {direction} ticket counters, 64 polls", flush=True)
+        assert L.mg_scan_workspace_init(P(ws), ws.numel(), B, T, Di, st) == 0
+        assert L.mg_scan_workspace_set_max_polls(P(ws), 64, st) == 0
+        if direction == "forward":
+            ws[256:256 + 4 * ncb].view(torch.int32).fill_(1)
+            assert _capi_fwd(L, hd, gt, h, ws, B, T, Di) == 0
+        else:
+            assert _capi_fwd(L, hd, gt, h, ws, B, T, Di) == 0
+            ws[256 + 4 * ncb:256 + 8 * ncb].view(torch.int32).fill_(1)
+            assert _capi_bwd(L, hd, gt, h, dhd, dhid, dgat, ws, B, T, Di) == 0
+        assert L.mg_scan_workspace_check(P(ws), st) == _lib.MG_ERR_STALL
+        assert b"gave up after 64 polls" in L.mg_last_error()
+
+    print("case: re-initialised", flush=True)
+    fresh = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    for w in (ws, fresh):
+        assert L.mg_scan_workspace_init(P(w), w.numel(), B, T, Di, st) == 0
+        ho, gh, gg = torch.empty_like(hd), torch.empty_like(hd), torch.empty_like(hd)
+        assert _capi_fwd(L, hd, gt, ho, w, B, T, Di) == 0
+        assert _capi_bwd(L, hd, gt, ho, dhd, gh, gg, w, B, T, Di) == 0
+        assert L.mg_scan_workspace_check(P(w), st) == 0
+        outs.append((ho, gh, gg))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_backward_output_strides():
+    """mg_scan_bwd writes dhidden/dgate with their own strides: reading the
+    packed projection output [B, T, 2 Di] and writing two dense [B, T, Di]
+    gradients gives the values of the packed gradient buffer."""
+    from gruboros_amd import scan as S
+
+    B, T, Di = 3, 700, 132
+    hidden, gate, h0, dh, dlast = _make(B, T, Di, torch.bfloat16, True, seed=21)
+    hg = torch.cat([hidden, gate], -1).to(DEV)
+    h0d, dhd, dl = h0.to(DEV), dh.to(DEV), dlast.to(DEV)
+    hv, gv = hg[..., :Di], hg[..., Di:]
+    h, _, ckpt = S._launch_fwd(hv, gv, h0d, torch.bfloat16, need_ckpt=True)
+    packed = torch.empty_like(hg)
+    S._launch_bwd(hv, gv, h0d, h, ckpt, dhd, dl, packed[..., :Di], packed[..., Di:], False)
+    dhid, dgat = torch.empty(B, T, Di, dtype=torch.bfloat16, device=DEV), torch.empty(B, T, Di, dtype=torch.bfloat16,
+                                                                                       device=DEV)
+    S._launch_bwd(hv, gv, h0d, h, ckpt, dhd, dl, dhid, dgat, False)
+    assert torch.equal(dhid, packed[..., :Di]) and torch.equal(dgat, packed[..., Di:])
+    S.check_workspaces()
+
+
+def test_fp32_output_from_bf16_inputs():
+    """The minLM block scans bf16 projections into an fp32 hidden sequence
+    (out_dtype=float32): fp32-accurate states, and gradients through the fp32
+    output path (dh fp32), against the fp64 oracle on the same bf16 inputs."""
+    from gruboros_amd.scan import gate_scan_packed
+
+    B, T, Di = 2, 515, 132
+    hidden, gate, h0, dh, dlast = _make(B, T, Di, torch.bfloat16, True, seed=33)
+    hg = torch.cat([hidden, gate], -1).to(DEV).requires_grad_(True)
+    out, nxt = gate_scan_packed(hg, h0.to(DEV), out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    ((out * dh.to(DEV).float()).sum() + (nxt * dlast.to(DEV)).sum()).backward()
+    ref = _oracle(hidden, gate, h0, dh.float(), dlast)
+    assert _rel_elem(out.detach().cpu(), ref[0]) <= 1e-5
+    assert _rel_elem(nxt.detach().cpu(), ref[1]) <= 1e-5
+    assert _rel_norm(hg.grad[..., :Di].float().cpu(), ref[2]) <= 1e-2
+    assert _rel_norm(hg.grad[..., Di:].float().cpu(), ref[3]) <= 1e-2
