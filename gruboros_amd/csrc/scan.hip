@@ -146,42 +146,54 @@ __device__ __forceinline__ bool take_tile(const Geometry& g, WsHeader* hdr, uint
   return true;
 }
 
-// Walk from tile k + step in direction `step` (-1: earlier tiles, forward
-// scan; +1: later tiles, backward scan) until an inclusive prefix is found,
-// folding aggregates on the way. Returns the state entering tile k of
-// channel c (one channel per lane). `last` is the chain's end tile in that
-// direction (0 or ntiles - 1), which only ever publishes an inclusive
-// prefix: the walk never steps past it. A word that stays not-ready for
-// max_polls polls ends the wait: the error bit is set and the prefix folded
-// so far is returned (the results are then wrong, and the caller learns it
-// from mg_scan_workspace_check).
+// The state entering tile k of channel c (one channel per lane), from the
+// look-back words of the tiles before it in scan order (step -1: earlier
+// tiles, forward scan; +1: later tiles, backward scan). `last` is the chain's
+// end tile in that direction (0 or ntiles - 1); it only ever publishes an
+// inclusive prefix, and the walk never steps past it.
+//   1. Walk back until an inclusive prefix I_j is found (aggregates on the
+//      way are passed over).
+//   2. Compose forward from it: c = A_i c + V_i for each tile i between j and
+//      k, re-reading each word. A word that has meanwhile become inclusive
+//      holds exactly that value (tile i computed it as A_i c + V_i from the
+//      same c), so the carry is the one a strictly sequential chain computes,
+//      bit for bit, whatever the timing (folding the aggregates during the
+//      walk would round (A_1 A_2) I instead of A_1 (A_2 I)).
+// A word that stays not-ready for max_polls polls ends the wait: the error
+// bit is set and 0 is returned (the results are then wrong, and the caller
+// learns it from mg_scan_workspace_check).
 __device__ __forceinline__ float look_back1(const uint64_t* status, int64_t BD, int64_t c, int k, int step, int last,
                                             uint32_t parity, uint32_t max_polls, uint32_t* err) {
-  float accA = 1.0f, accV = 0.0f;
-  int j = k + step;
-  const uint64_t* w = status + static_cast<int64_t>(j) * BD + c;
-  const int64_t dw = step * BD;
+  const uint64_t* base = status + c;
   const uint32_t par = parity ? kTagParity : 0u;
+  int j = k + step;
   uint32_t polls = 0;
+  float carry;
   while (true) {
-    const uint64_t x = poll_word(w);
+    const uint64_t x = poll_word(base + static_cast<int64_t>(j) * BD);
     const uint32_t tag = static_cast<uint32_t>(x);
-    const float val = __uint_as_float(static_cast<uint32_t>(x >> 32));
-    if (tag == (kTagIncl | par)) return accA * val + accV;
+    if (tag == (kTagIncl | par)) {
+      carry = __uint_as_float(static_cast<uint32_t>(x >> 32));
+      break;
+    }
     if (j != last && (tag & (kTagAggBit | kTagParity)) == (kTagAggBit | par)) {
-      accV = accA * val + accV;
-      accA = accA * __uint_as_float(tag & ~(kTagAggBit | kTagParity));
-      w += dw;
       j += step;
       polls = 0;
     } else {
       if (++polls > max_polls) {
         atomicOr(err, kErrStall);
-        return accV;
+        return 0.0f;
       }
       __builtin_amdgcn_s_sleep(2);
     }
   }
+  for (int i = j - step; i != k; i -= step) {  // every word here was seen ready (an aggregate)
+    const uint64_t x = poll_word(base + static_cast<int64_t>(i) * BD);
+    const uint32_t tag = static_cast<uint32_t>(x);
+    const float v = __uint_as_float(static_cast<uint32_t>(x >> 32));
+    carry = tag == (kTagIncl | par) ? v : __builtin_fmaf(__uint_as_float(tag & ~(kTagAggBit | kTagParity)), carry, v);
+  }
+  return carry;
 }
 
 // Load one run of rows. hb/gb are tile base pointers (wave-uniform), off is
@@ -316,7 +328,7 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
       publish_agg(st, TA, TV, parity);
       carry = look_back1(status, g.BD, c + s, k, -1, 0, parity, max_polls, &hdr->err);
     }
-    if (k + 1 < g.ntiles) publish_incl(st, TA * carry + TV, parity);
+    if (k + 1 < g.ntiles) publish_incl(st, __builtin_fmaf(TA, carry, TV), parity);  // as look_back1 composes
     reinterpret_cast<float*>(&s_carry[cl])[s] = carry;
   }
   __syncthreads();
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
       publish_agg(st, TA, TM, parity);
       carry = look_back1(status, g.BD, c + q, k, +1, g.ntiles - 1, parity, max_polls, &hdr->err);
     }
-    if (k > 0) publish_incl(st, TA * carry + TM, parity);
+    if (k > 0) publish_incl(st, __builtin_fmaf(TA, carry, TM), parity);  // as look_back1 composes
     reinterpret_cast<float*>(&s_carry[cl])[q] = carry;
   }
   __syncthreads();
