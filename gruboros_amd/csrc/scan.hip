@@ -44,6 +44,7 @@
 //     g(hidden) - h_{t-1}, a difference of two nearly equal numbers.)
 
 #include <algorithm>
+#include <mutex>
 
 #include "mg_common.h"
 
@@ -601,14 +602,15 @@ inline size_t ws_bytes_any(int B, int T, int Di) {
   return ws_header_bytes(f.ncb) + static_cast<size_t>(f.ntiles + b.ntiles) * f.BD * sizeof(uint64_t);
 }
 
+// `need`: the workspace bytes the call requires (0: both directions' size)
 inline int check_common(const char* fn, int B, int T, int Di, int tile_rows, void* ws, size_t ws_size,
-                        Geometry& g) {
+                        Geometry& g, size_t need = 0) {
   if (B < 1 || T < 1 || Di < 4) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
   if (Di % kVec) return fail(MG_ERR_ARG, "%s: Di=%d must be a multiple of 4", fn, Di);
   make_geometry(B, T, Di, tile_rows, g);
   const int64_t nblocks = static_cast<int64_t>(g.ncb) * g.ntiles;
   if (nblocks > 0x7fffffff) return fail(MG_ERR_ARG, "%s: problem too large (%lld tiles)", fn, (long long)nblocks);
-  const size_t need = ws_bytes_any(B, T, Di);
+  if (!need) need = ws_bytes_any(B, T, Di);
   if (!ws || ws_size < need)
     return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn, ws_size, need);
   if (!aligned(ws, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
@@ -665,6 +667,46 @@ void launch_bwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_
                      static_cast<const Th*>(h), out_sb, out_ld, ckpt, static_cast<const Th*>(dh), g_sb, g_ld, dh_last,
                      static_cast<Tin*>(dhidden), static_cast<Tin*>(dgate), d_sb, d_ld, dh0, g, ws_header(ws),
                      ws_counters(ws, g, true), ws_status(ws, g, true));
+}
+
+// ------------------------------------------------------------------ allocation-free forward
+//
+// mg_scan_fwd_noalloc keeps its look-back workspace in this file-scope device
+// array instead of a caller's workspace. Each device holds its own copy (at
+// its own address, found once per device with hipGetSymbolAddress); every
+// call re-initialises the part it uses with the init kernel (a kernel, not a
+// memset: callers may capture the call into a graph). Calls on one device
+// share the array, so calls that may overlap on one device race.
+constexpr size_t kNoAllocBytes = (size_t(16) << 20) + (size_t(64) << 10);  // 16 MiB + 64 KiB
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call per device).
+inline int scratch_ptr(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MG_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MG_ERR_ARG, "%s: device %d beyond %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MG_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MG_OK;
+}
+
+// Bytes of a forward-only workspace (header, counters, forward look-back words).
+inline size_t fwd_ws_bytes(int B, int T, int Di) {
+  Geometry f;
+  make_geometry(B, T, Di, kFwdTileRows, f);
+  return ws_header_bytes(f.ncb) + static_cast<size_t>(f.ntiles) * f.BD * sizeof(uint64_t);
 }
 
 }  // namespace scan
@@ -727,14 +769,16 @@ extern "C" int mg_scan_workspace_check(const void* workspace, void* stream) {
   return MG_OK;
 }
 
-extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
-                           const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
-                           float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
-                           size_t workspace_bytes, void* stream) {
-  const char* fn = "mg_scan_fwd";
+namespace mg {
+namespace scan {
+// Checks and launches the forward; need: the workspace bytes required (see check_common).
+static int fwd_impl(const char* fn, int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
+                    const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld, float* h_last,
+                    float* ckpt, int B, int T, int Di, void* workspace, size_t workspace_bytes, size_t need,
+                    void* stream) {
   scan::Geometry g;
   int rc;
-  if ((rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, workspace, workspace_bytes, g))) return rc;
+  if ((rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, workspace, workspace_bytes, g, need))) return rc;
   if ((rc = scan::check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
@@ -751,6 +795,42 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
   else
     return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
   return check_launch(fn);
+}
+}  // namespace scan
+}  // namespace mg
+
+extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
+                           const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
+                           float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return scan::fwd_impl("mg_scan_fwd", in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last,
+                        ckpt, B, T, Di, workspace, workspace_bytes, 0, stream);
+}
+
+extern "C" size_t mg_scan_fwd_noalloc_max_bytes(void) { return scan::kNoAllocBytes; }
+
+extern "C" int mg_scan_fwd_noalloc(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
+                                   const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
+                                   float* h_last, float* ckpt, int B, int T, int Di, void* stream) {
+  const char* fn = "mg_scan_fwd_noalloc";
+  if (B < 1 || T < 1 || Di < 4 || Di % scan::kVec) return fail(MG_ERR_ARG, "%s: bad shape B=%d T=%d Di=%d", fn, B, T, Di);
+  const size_t need = scan::fwd_ws_bytes(B, T, Di);
+  if (need > scan::kNoAllocBytes)
+    return fail(MG_ERR_ARG, "%s: B=%d T=%d Di=%d needs %zu bytes of look-back scratch, above the allocation-free "
+                "maximum of %zu (use mg_scan_fwd with a workspace)", fn, B, T, Di, need, scan::kNoAllocBytes);
+  void* ws = nullptr;
+  if (int rc = scan::scratch_ptr(fn, &ws)) return rc;
+  // validate the arguments before anything is enqueued (a NULL workspace skips the launch)
+  scan::Geometry g;
+  if (int rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, ws, scan::kNoAllocBytes, g, need)) return rc;
+  // initialise the part this call uses (zeros + header), then the forward on it
+  const int64_t n16 = static_cast<int64_t>((need + 15) / 16);
+  const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
+  hipLaunchKernelGGL(scan::init_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint4*>(ws), n16, B, T, Di, scan::kDefaultPolls);
+  if (int rc = check_launch(fn)) return rc;
+  return scan::fwd_impl(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last, ckpt, B,
+                        T, Di, ws, scan::kNoAllocBytes, need, stream);
 }
 
 extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,

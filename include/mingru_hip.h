@@ -114,6 +114,26 @@ int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free mg_scan_fwd. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * results as mg_scan_fwd without the workspace: the look-back scratch is a
+ * file-scope device array of mg_scan_fwd_noalloc_max_bytes() bytes (16 MiB +
+ * 64 KiB; each device the library runs on holds its own copy until the
+ * process ends), re-initialised on `stream` by a kernel at every call (no
+ * memset). Shapes needing more look-back scratch than that (more than ~2 M
+ * channel-tiles: B * Di * ceil(T / 128) > 2^21, e.g. cfg2's B16 T8192 Di2048
+ * fits exactly) are refused with MG_ERR_ARG. It calls no hipMalloc, hipFree
+ * or allocating library routine. All calls on one device share the array:
+ * calls that may overlap on one device race. */
+size_t mg_scan_fwd_noalloc_max_bytes(void);
+int mg_scan_fwd_noalloc(int in_dtype, const void* hidden, const void* gate,
+                        int64_t in_sb, int64_t in_ld,
+                        const float* h0,
+                        int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
+                        float* h_last, float* ckpt,
+                        int B, int T, int Di, void* stream);
+
 /* Backward of mg_scan_fwd: autograd of reference mingru/minGRU.py:16-20,
  * :53-69 through gate, hidden and prev_hidden, in closed form:
  *   lambda_t  = dh_t + a_{t+1} lambda_{t+1},
