@@ -15,16 +15,14 @@ activations over fp32 master weights):
   FinalNormCE   embed = RMSNorm(x + pending); mean cross-entropy of
                 embed W_out^T (streaming loss kernel).
 
-Why blocks rather than one Function per op: inside a block the gradients
-of the normalized inputs and of the GELU input are kept in fp32 (the
-input-gradient products write fp32, which the norm and GELU backward
-kernels read), and every gradient stored in bf16 (dlogits, the FeedForward
-output's gradient, dgate/dhidden, dpre) is rounded stochastically by the
-kernel that writes it. An autograd boundary at a bf16 tensor would cast its
+Why blocks rather than one Function per op: every gradient a block stores
+in bf16 (dlogits, the input-gradient products, dgate/dhidden, dpre, the
+FeedForward output's gradient) is rounded stochastically by the kernel that
+writes it. An autograd boundary at a bf16 tensor would instead cast its
 incoming gradient to bf16 with round-to-nearest, whose errors at a near-
 uniform softmax repeat across the rows of a label and add up in the weight
 gradients (measured on the fp64 restatement: 4-7% at the cfg3 row count
-against 0.5% for this arrangement). The gradients crossing block boundaries
+against 0.5% with stochastic rounding). The gradients crossing block boundaries
 are the fp32 residual stream's, the fp32 minGRU output's, and the bf16
 FeedForward output's (stochastically rounded by the next block's norm).
 """
@@ -108,7 +106,7 @@ class MinGRUBlock(torch.autograd.Function):
         else:
             dh0 = _scan_bwd(hg3[..., :Di], hg3[..., Di:], h0, h, None, dh, dh_last, dhg3[..., :Di], dhg3[..., Di:],
                             want_dh0)
-        dn = gemm.linear_dx(dhg, whb, out_dtype=torch.float32)     # fp32: no rounding of n's gradient
+        dn = gemm.linear_dx(dhg, whb, stochastic=True)             # bf16, stochastically rounded
         dW_hg = gemm.linear_dw(dhg, pair[:, :D]) if ctx.needs_input_grad[3] else None
         dres = dx1.reshape(N, D) if dx1 is not None else None
         dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, dn, dres, True, BF16, ctx.has_pending)
@@ -151,11 +149,11 @@ class FFBlock(torch.autograd.Function):
             dp = dpend.reshape(N, D)
             if dp.dtype != BF16 or not dp.is_contiguous():
                 dp = dp.to(BF16).contiguous()
-            dact = gemm.linear_dx(dp, w2b, out_dtype=torch.float32)    # fp32 into the GELU backward
+            dact = gemm.linear_dx(dp, w2b, stochastic=True)            # bf16, stochastically rounded
             dpre, db1 = gelu_backward(dact, pre)                        # bf16, stochastically rounded
             dW2 = gemm.linear_dw(dp, act)
             db2 = column_sum(dp)
-            dn2 = gemm.linear_dx(dpre, w1b, out_dtype=torch.float32)   # fp32 into the norm backward
+            dn2 = gemm.linear_dx(dpre, w1b, stochastic=True)           # bf16, stochastically rounded
             dW1 = gemm.linear_dw(dpre, n2)
         dx1, dout, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, True)
         return dx1.view(B, T, D), dout.view(B, T, D), dw_norm, dW1, db1, dW2, db2
@@ -191,7 +189,7 @@ class FinalNormCE(torch.autograd.Function):
     def backward(ctx, g):
         B, T, D = ctx.dims
         xn, w_norm, rstd, embed, dl, wob = ctx.saved_tensors
-        de = gemm.linear_dx(dl, wob, out_dtype=torch.float32)         # fp32 into the norm backward
+        de = gemm.linear_dx(dl, wob, out_dtype=torch.float32)         # fp32 (scaled by g below)
         dW = gemm.linear_dw(dl, embed) if ctx.needs_input_grad[3] else None
         de.mul_(g)  # upstream scale (1 / grad_accum in the reference loop), in fp32; no host sync
         if dW is not None:

@@ -219,7 +219,8 @@ __device__ __forceinline__ bf16x8 read_frag(const uint4* tile, int row, int s, i
   }
 }
 
-enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_GELU_GRAD = 3 };
+// EPI_SR (internal; MG_GEMM_STOCHASTIC): C = acc rounded stochastically to bf16 (a gradient).
+enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_GELU = 2, EPI_GELU_GRAD = 3, EPI_SR = 4 };
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
@@ -408,6 +409,227 @@ __device__ __forceinline__ void mainloop(const Params& p, uint4* smem, uint4* s1
   __syncthreads();
 }
 
+// Four-wave main loop for 256 x 256 tiles, any operand layouts: waves in
+// 2 x 2, each 128 x 128 as 4 x 4 MFMA blocks, accumulators in AGPRs, one wave
+// per SIMD. With one wave per SIMD nothing hides a stall of the wave's own
+// instruction stream, so the k-tile is software-pipelined by hand:
+//   * the two LDS stages are distinct __shared__ objects and the k-loop runs
+//     tiles in pairs, so each stage is static (an LDS read is then not made
+//     to wait for loads into the other stage);
+//   * the next tile's loads (8 instructions per operand and wave) are spread
+//     over the MFMAs of the tile's first two k-steps (A, then B: a burst
+//     stalls the MFMA stream), and waited for before the last k-step;
+//   * the next k-step's fragment reads are spread over the current k-step's
+//     MFMAs; at the last k-step, after the tile's barrier, they are the next
+//     tile's first fragments;
+//   * load addresses are per-lane offsets computed once, a k-tile adds one
+//     scalar; fragment addresses are computed once, k-steps are immediates.
+// No load is masked: K-contiguous operands need K % 64 == 0, MN-contiguous
+// ones a row count (M or N) that is a multiple of 256 (their k-rows past K lie
+// past the end of the buffer and read as zero), and the prefetch after a
+// split's last tile reloads that tile.
+
+// Scheduler hints for one k-step: ND fragment reads spread over the first
+// MFMAs (MD of them; early, so each read has many MFMAs to land before the
+// next k-step needs it) and NV loads over the last ones.
+#ifndef MG_W4_READ_SPAN
+#define MG_W4_READ_SPAN 8
+#endif
+template <int NM, int ND, int NV, int m = 0>
+__device__ __forceinline__ void interleave() {
+  if constexpr (m < NM) {
+    constexpr int MD = ND > MG_W4_READ_SPAN ? NM : MG_W4_READ_SPAN;  // MFMAs carrying reads
+    constexpr int MV = NM / 2;                                          // MFMAs carrying loads (the last)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    constexpr int d = m < MD ? (m + 1) * ND / MD - m * ND / MD : 0;
+    constexpr int mv = m - (NM - MV);
+    constexpr int v = mv >= 0 ? (mv + 1) * NV / MV - mv * NV / MV : 0;
+    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  // DS read
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);  // VMEM read
+    interleave<NM, ND, NV, m + 1>();
+  }
+}
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+constexpr int kW4Rows = 256;                         // tile rows per operand
+constexpr int kW4Loads = kW4Rows * 8 / 64 / 4;       // load instructions per operand and wave (8)
+
+template <bool KMAJ>
+struct W4Operand;
+
+// K-contiguous operand: tiles [256 rows][64 k] (Loader<256, true, 256>), one
+// 16-byte read per fragment.
+template <>
+struct W4Operand<true> {
+  static constexpr int kReads = 4;  // fragment reads per k-step (4 blocks of 32 rows)
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t v[kW4Loads];
+  uint32_t p0, p1;  // fragment addresses of even / odd 32-row blocks
+  // r0: first matrix row of the tile; wr: first tile row of this wave's 128
+  __device__ __forceinline__ void init(const Operand& o, int r0, int wr, int wave, int lane) {
+    rsrc = o.rsrc;
+#pragma unroll
+    for (int i = 0; i < kW4Loads; ++i) {
+      const int r = (wave * kW4Loads + i) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
+      v[i] = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(c) * 16u;
+    }
+    // row wr + 32 i + L, chunk (2 s + half) ^ f(row), f(r) = (r ^ (r >> 3)) & 7;
+    // f(wr + 32 i + L) = f(wr + L) ^ 4 (i & 1) for wr a multiple of 128
+    const int L = lane & 31, half = lane >> 5, r = wr + L;
+    p0 = static_cast<uint32_t>(r * 128 + ((half ^ ((r ^ (r >> 3)) & 7)) << 4));
+    p1 = p0 ^ 64u;
+  }
+  __device__ __forceinline__ uint32_t koff(int k0, int kofs, uint32_t) const {
+    return static_cast<uint32_t>(k0 + kofs) * 2u;
+  }
+  __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * kW4Loads + i) * 64),
+                                             16, v[i] + ko, 0, 0, 0);
+  }
+  __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int i) const {
+    const uint32_t a = (((i & 1) ? p1 : p0) ^ (32u * s)) + 4096u * i;
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(st) + a));
+  }
+};
+
+// MN-contiguous operand: tiles [64 k-rows][256] (Loader<256, false, 256>),
+// fragments through the LDS transpose read (two 8-byte reads each).
+template <>
+struct W4Operand<false> {
+  static constexpr int kReads = 8;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t v[kW4Loads];
+  uint32_t fb[4];  // byte address of block i's first read at k-step 0
+  __device__ __forceinline__ void init(const Operand& o, int r0, int wr, int wave, int lane) {
+    rsrc = o.rsrc;
+#pragma unroll
+    for (int i = 0; i < kW4Loads; ++i) {
+      const int chunk = (wave * kW4Loads + i) * 64 + lane;
+      const int kr = chunk >> 5, cpos = chunk & 31;
+      const int m = (((cpos >> 1) ^ tr_swz(kr)) << 4) + ((cpos & 1) << 3);
+      v[i] = static_cast<uint32_t>(kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
+    }
+    // read_frag<256, false>: k-row 16 s + 8 (g >> 1) + j, column wr + 32 i + 16 (g & 1) + 4 q;
+    // tr_swz of that k-row is tr_swz(j), and the xor only touches the low 3 bits of
+    // (column >> 4) since wr is a multiple of 128
+    const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int colblk = (wr >> 4) + 2 * i + (g & 1);
+      fb[i] = static_cast<uint32_t>((8 * (g >> 1) + j) * (kW4Rows * 2) + ((colblk ^ tr_swz(j)) << 5) + 8 * q);
+    }
+  }
+  __device__ __forceinline__ uint32_t koff(int k0, int, uint32_t ld2) const { return static_cast<uint32_t>(k0) * ld2; }
+  __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * kW4Loads + i) * 64),
+                                             16, v[i] + ko, 0, 0, 0);
+  }
+  __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int i) const {
+    const char* base = reinterpret_cast<const char*>(st) + fb[i] + 16 * s * (kW4Rows * 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 4 * kW4Rows * 2));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+template <bool AK, bool BKM>
+__device__ __forceinline__ void mainloop_w4(const Params& p, uint4* sa, uint4* sb, int m0, int n0, int kt0, int kt1,
+                                            f32x16 (&acc)[4][4]) {
+  constexpr int S = BK / 16;
+  constexpr int kStageA = kW4Rows * 8;  // uint4 of the A tile (B follows)
+  // the wave index in a scalar register: the loads' LDS destinations (M0) are then scalar arithmetic
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  W4Operand<AK> A;
+  W4Operand<BKM> B;
+  A.init(oa, m0, wm * 128, wave, lane);
+  B.init(ob, n0, wn * 128, wave, lane);
+  // byte offsets of k-tile t (relative to kt0); tiles past kt1 reload tile kt1 - 1
+  auto koffs = [&](int t, uint32_t& ao, uint32_t& bo) {
+    const int tg = min(kt0 + t, kt1 - 1);
+    int seg = 0, k0 = tg * BK;
+    if (p.hilo) {  // K-contiguous only (checked by the host)
+      seg = tg / p.nkt_seg;
+      k0 = (tg - seg * p.nkt_seg) * BK;
+    }
+    ao = A.koff(k0, seg == 1 ? p.K : 0, oa.ld2);
+    bo = B.koff(k0, seg == 2 ? p.K : 0, ob.ld2);
+  };
+  bf16x8 af[2][4], bfr[2][4];
+  // in the order the MFMAs need them: (i, j) loops i outer, so A_0 and all of B first
+  auto read_step = [&](const uint4* st, int s, int buf) {
+    af[buf][0] = A.frag(st, s, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[buf][j] = B.frag(st + kStageA, s, j);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) af[buf][i] = A.frag(st, s, i);
+  };
+  auto mfma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NR = W4Operand<AK>::kReads + W4Operand<BKM>::kReads;  // fragment reads per k-step
+  const int n = kt1 - kt0;
+  {
+    uint32_t ao, bo;
+    koffs(0, ao, bo);
+#pragma unroll
+    for (int i = 0; i < kW4Loads; ++i) A.load(sa, wave, i, ao);
+#pragma unroll
+    for (int i = 0; i < kW4Loads; ++i) B.load(sa + kStageA, wave, i, bo);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  read_step(sa, 0, 0);
+  // one k-tile from `cur`, loading tile t + 1 into `nxt`
+  auto tile = [&](int t, const uint4* cur, uint4* nxt) __attribute__((always_inline)) {
+    uint32_t ao, bo;
+    koffs(t + 1, ao, bo);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int c = s & 1;
+      if (s == 0) {
+#pragma unroll
+        for (int i = 0; i < kW4Loads; ++i) A.load(nxt, wave, i, ao);
+      } else if (s == 1) {
+#pragma unroll
+        for (int i = 0; i < kW4Loads; ++i) B.load(nxt + kStageA, wave, i, bo);
+      }
+      if (s + 1 < S) {
+        read_step(cur, s + 1, c ^ 1);
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // tile t + 1 is in `nxt` for every wave; every wave is done with `cur`
+        read_step(nxt, 0, c ^ 1);
+      }
+      mfma_step(c);
+      if (s < 2) interleave<16, NR, kW4Loads>();
+      else interleave<16, NR, 0>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  int t = 0;
+  for (; t + 1 < n; t += 2) {
+    tile(t, sa, sb);
+    tile(t + 1, sb, sa);
+  }
+  if (t < n) tile(t, sa, sb);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // Ping-pong main loop, 256 x 256 tiles, 8 waves in two groups of four (one
 // wave of each group per SIMD; group g owns tile rows 128 g .. 128 g + 127,
 // each wave 128 x 64). The groups alternate, a workgroup barrier between
@@ -543,7 +765,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
   // 128 x 128 tiles keep their stages as two distinct objects (the
   // interleaved schedule needs that); 256 x 256 tiles one array of two.
-  constexpr bool kSplit = BM != 256;
+  constexpr bool kSplit = BM != 256 || WM * WN == 4;
   __shared__ uint4 smem[kSplit ? kStage : 2 * kStage];
   __shared__ uint4 smem_b[kSplit ? kStage : 1];
   uint4* const stage1 = kSplit ? smem_b : smem + kStage;
@@ -560,6 +782,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   f32x16 acc[MB][NB];
   if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
     mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);  // both stages in smem (kSplit is false)
+  else if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 2)
+    mainloop_w4<AK, BKM>(p, smem, stage1, m0, n0, kt0, kt1, acc);
   else
     mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256), kSplit>(p, smem, stage1, m0, n0, kt0, kt1, acc);
 
@@ -666,7 +890,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x.v[e] = old.v[e] + x.v[e];
           }
-          if constexpr (EPI == EPI_GELU_GRAD)  // a gradient: stochastic rounding (mg_common.h)
+          if constexpr (EPI == EPI_GELU_GRAD || EPI == EPI_SR)  // gradients: stochastic rounding (mg_common.h)
             io4<TC>::store_grad(cp, x, static_cast<uint32_t>(static_cast<int64_t>(m) * p.N + n), 0x9e5bu);
           else
             io4<TC>::store(cp, x);
@@ -816,11 +1040,19 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   const int64_t t256 = int64_t((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
   const bool wgrad = !ak && !bk;
-  pl.big = !wgrad && t256 >= kCUs;
+  // weight gradients whose output dimensions are multiples of 256 run 256 x 256
+  // four-wave tiles (half the L2 traffic per flop of 128 x 128), split along K
+  // to about one workgroup per CU
+#ifndef MG_GEMM_WGRAD128
+  const bool wgrad_big = wgrad && M % 256 == 0 && N % 256 == 0;
+#else
+  const bool wgrad_big = false;
+#endif
+  pl.big = (!wgrad && t256 >= kCUs) || wgrad_big;
   const int64_t tiles = pl.big ? t256 : t128;
   pl.tiles = static_cast<int>(tiles);
   const int nkt = (hilo ? 3 : 1) * ((K + BK - 1) / BK);
-  const int64_t want_wgs = wgrad ? 2 * kCUs : kCUs;
+  const int64_t want_wgs = wgrad && !wgrad_big ? 2 * kCUs : kCUs;
   int splits = 1;
   if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
     splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
@@ -858,14 +1090,35 @@ int dispatch_epi(const Params& p, const Plan& pl, int epi, int c_dtype, hipStrea
     if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, C_STORE>(p, pl, s);
+    if (epi == EPI_SR) return launch<BM, BN, WM, WN, AK, BKM, EPI_SR, bf16_t, C_STORE>(p, pl, s);
   }
   return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
 }
 
 // 256 x 256 tiles run 8 waves (two per SIMD), 128 x 128 tiles 4.
+// Whether a product meets the four-wave loop's no-mask conditions.
+inline bool w4_ok(const Params& p, bool ak, bool bk) {
+  if ((ak || bk) && p.K % BK) return false;
+  if (!ak && p.M % kW4Rows) return false;
+  if (!bk && p.N % kW4Rows) return false;
+  return true;
+}
+
+// 256 x 256 tiles run the four-wave pipelined loop (mainloop_w4) when the
+// product meets its conditions (w4_ok), else 8 waves.
 template <int BM, int BN>
 int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, int c_dtype, hipStream_t s) {
   constexpr int WN = BM * BN >= 256 * 256 ? 4 : 2;
+#ifndef MG_GEMM_NO_W4
+  if constexpr (BM == 256 && BN == 256) {
+    if (w4_ok(p, ak, bk)) {
+      if (ak && bk) return dispatch_epi<256, 256, 2, 2, true, true>(p, pl, epi, c_dtype, s);
+      if (ak && !bk) return dispatch_epi<256, 256, 2, 2, true, false>(p, pl, epi, c_dtype, s);
+      if (!ak && !bk) return dispatch_epi<256, 256, 2, 2, false, false>(p, pl, epi, c_dtype, s);
+      return dispatch_epi<256, 256, 2, 2, false, true>(p, pl, epi, c_dtype, s);
+    }
+  }
+#endif
   if (ak && bk) return dispatch_epi<BM, BN, 2, WN, true, true>(p, pl, epi, c_dtype, s);
   if (ak && !bk) return dispatch_epi<BM, BN, 2, WN, true, false>(p, pl, epi, c_dtype, s);
   if (!ak && !bk) return dispatch_epi<BM, BN, 2, WN, false, false>(p, pl, epi, c_dtype, s);
@@ -882,8 +1135,10 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
                        int N, int K, int epilogue, const float* bias, void* aux, int64_t ldaux, int c_dtype, void* C,
                        int64_t ldc, int flags, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "mg_gemm";
-  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC | MG_GEMM_HILO))
+  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC | MG_GEMM_HILO | MG_GEMM_STOCHASTIC))
     return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
+  if ((flags & MG_GEMM_STOCHASTIC) && (c_dtype != MG_BF16 || (epilogue != MG_EPI_NONE && epilogue != MG_EPI_GELU_GRAD)))
+    return fail(MG_ERR_ARG, "%s: stochastic rounding needs a bf16 C and no epilogue (or the GELU gradient's)", fn);
   const bool accumulate = flags & MG_GEMM_ACCUMULATE;
   const bool deterministic = flags & MG_GEMM_DETERMINISTIC;
   const bool hilo = flags & MG_GEMM_HILO;
@@ -951,8 +1206,9 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
     p.part = static_cast<float*>(workspace);
   }
   p.accumulate = accumulate ? 1 : 0;
-  const int rc = pl.big ? gemm::dispatch_layout<256, 256>(p, pl, ak, bk, epilogue, c_dtype, s)
-                        : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epilogue, c_dtype, s);
+  const int epi = (flags & MG_GEMM_STOCHASTIC) && epilogue == MG_EPI_NONE ? gemm::EPI_SR : epilogue;
+  const int rc = pl.big ? gemm::dispatch_layout<256, 256>(p, pl, ak, bk, epi, c_dtype, s)
+                        : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epi, c_dtype, s);
   if (rc || pl.ysplits <= 1) return rc;
   const int64_t n4 = int64_t(M) * (N / 4);
   hipLaunchKernelGGL(gemm::split_reduce_kernel, dim3(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048))),

@@ -59,9 +59,14 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 // cancelling: on the fp64 restatement at the cfg3 model size they moved the
 // FeedForward and norm weight gradients by 4-7% at 8-16 k rows, growing with
 // the row count; with stochastic rounding by 0.5%, independent of it.
-// The 16 random bits are a hash of the element's index, its value and a salt
-// per call site, so the result is a deterministic function of the inputs (no
-// generator state: replays and resumed runs repeat bit for bit).
+// The random bits are a hash of the element pair's index, its values and a
+// salt per call site, so the result is a deterministic function of the inputs
+// (no generator state: replays and resumed runs repeat bit for bit). One
+// 32-bit hash serves two elements (16 bits each), and the rounding itself is
+// gfx950's v_cvt_sr_bf16_f32, which adds the HIGH 16 bits of its random
+// operand below the bf16 mantissa and truncates, i.e. for finite x
+// bf16(x) = (bits(x) + (r >> 16)) >> 16, and keeps Inf and NaN (checked
+// against that rule on the device for 2^20 random operands).
 
 // MurmurHash3's 32-bit finaliser (fmix32, A. Appleby, public domain).
 __device__ __forceinline__ uint32_t hash32(uint32_t h) {
@@ -73,18 +78,16 @@ __device__ __forceinline__ uint32_t hash32(uint32_t h) {
   return h;
 }
 
-// fp32 -> bf16, rounded stochastically (non-finite values pass through
-// round-to-nearest). idx: the element's index in its tensor.
-__device__ __forceinline__ bf16_t f32_to_bf16_sr(float f, uint32_t idx, uint32_t salt) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u) return f32_to_bf16(f);
-  const uint32_t r = hash32(idx * 0x9e3779b9u ^ u ^ salt) & 0xffffu;
-  return static_cast<bf16_t>((u + r) >> 16);
-}
+typedef __bf16 __attribute__((ext_vector_type(2))) bf16x2_t;
 
+// (lo, hi) fp32 -> packed bf16 pair (lo in the low half), each rounded
+// stochastically. idx: lo's index in its tensor (hi is idx + 1).
 __device__ __forceinline__ uint32_t pack_bf16x2_sr(float lo, float hi, uint32_t idx, uint32_t salt) {
-  return static_cast<uint32_t>(f32_to_bf16_sr(lo, idx, salt)) |
-         (static_cast<uint32_t>(f32_to_bf16_sr(hi, idx + 1, salt)) << 16);
+  const uint32_t r = hash32(idx ^ salt ^ __float_as_uint(lo) ^ __builtin_rotateleft32(__float_as_uint(hi), 16));
+  bf16x2_t v = {};
+  v = __builtin_amdgcn_cvt_sr_bf16_f32(v, lo, r, false);
+  v = __builtin_amdgcn_cvt_sr_bf16_f32(v, hi, r << 16, true);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // N consecutive channels of one row, loaded/stored as one vector access
@@ -168,7 +171,7 @@ template <int N> struct iov<bf16_t, N> {
     for (int q = 0; q < N / 2; ++q)
       __builtin_nontemporal_store(pack_bf16x2(a.v[2 * q], a.v[2 * q + 1]), reinterpret_cast<uint32_t*>(p) + q);
   }
-  // Gradient stores: stochastic rounding (f32_to_bf16_sr); idx = index of element 0.
+  // Gradient stores: stochastic rounding (pack_bf16x2_sr); idx = index of element 0.
   __device__ __forceinline__ static void store_grad(bf16_t* p, const fv<N>& a, uint32_t idx, uint32_t salt) {
     raw x;
     uint32_t* w = reinterpret_cast<uint32_t*>(&x);

@@ -12,7 +12,7 @@ from . import _lib
 
 KCONTIG, MNCONTIG = 0, 1
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD = 0, 1, 2, 3
-FLAG_ACCUMULATE, FLAG_DETERMINISTIC, FLAG_HILO = 1, 2, 4
+FLAG_ACCUMULATE, FLAG_DETERMINISTIC, FLAG_HILO, FLAG_STOCHASTIC = 1, 2, 4, 8
 
 
 def _rows(t, name):
@@ -54,15 +54,16 @@ def _workspace(device, nbytes):
 
 
 def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None, aux=None, accumulate=False,
-         deterministic=None, hilo=False):
+         deterministic=None, hilo=False, stochastic=False):
     """out[M, N] (=|+=) epilogue(sum_k A(m, k) B(k, n)); see include/mingru_hip.h (mg_gemm).
     Results repeat bit for bit. deterministic (default: torch.are_deterministic_algorithms_enabled())
     also rules out the split along K, so the sum order depends only on K. hilo: A and B rows are
-    [hi (K) | lo (K)] bf16 pairs and the product is fp32-accurate (three MFMA passes)."""
+    [hi (K) | lo (K)] bf16 pairs and the product is fp32-accurate (three MFMA passes). stochastic: a bf16
+    out is rounded stochastically (a gradient)."""
     if deterministic is None:
         deterministic = torch.are_deterministic_algorithms_enabled()
     flags = (FLAG_ACCUMULATE if accumulate else 0) | (FLAG_DETERMINISTIC if deterministic else 0) | \
-        (FLAG_HILO if hilo else 0)
+        (FLAG_HILO if hilo else 0) | (FLAG_STOCHASTIC if stochastic else 0)
     _lib.require_cuda(a, b, out)
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise _lib.MingruHipError(f"mg_gemm operands must be bfloat16 (got {a.dtype}, {b.dtype})")
@@ -122,13 +123,15 @@ def linear_fwd_hilo(x_pair, w_pair, out, K):
     return gemm(x_pair, KCONTIG, w_pair, KCONTIG, n, o, K, out, hilo=True)
 
 
-def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16):
-    """dy [N, out] bf16, w [out, in] bf16 -> dy w [N, in] (bf16 or fp32); times gelu'(gelu_pre) when given."""
+def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16, stochastic=False):
+    """dy [N, out] bf16, w [out, in] bf16 -> dy w [N, in] (bf16 or fp32); times gelu'(gelu_pre) when given
+    (then rounded stochastically); stochastic: a plain bf16 result rounded stochastically."""
     n, o = dy.shape
     k = w.shape[1]
     dx = torch.empty(n, k, device=dy.device, dtype=out_dtype)
     return gemm(dy, KCONTIG, w, MNCONTIG, n, k, o, dx,
-                epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre)
+                epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre,
+                stochastic=stochastic and gelu_pre is None and out_dtype == torch.bfloat16)
 
 
 def linear_dw(dy, x, out=None, accumulate=False, deterministic=None):

@@ -274,6 +274,9 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  * flags (bit set):
  *   MG_GEMM_ACCUMULATE (fp32 C, no epilogue): C += A B.
  *   MG_GEMM_DETERMINISTIC: never split along K.
+ *   MG_GEMM_STOCHASTIC: a bf16 C (epilogue NONE) is rounded stochastically,
+ *     as gradients are (see the conventions above); the GELU-gradient
+ *     epilogue always is.
  *   MG_GEMM_HILO: fp32-accurate product of operands stored as bf16 hi/lo
  *     pairs. A and B must both be K-contiguous; each row holds K hi values
  *     followed by K lo values (x = hi + lo; lda, ldb >= 2K), as written by
@@ -304,6 +307,7 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
 #define MG_GEMM_ACCUMULATE 1
 #define MG_GEMM_DETERMINISTIC 2
 #define MG_GEMM_HILO 4
+#define MG_GEMM_STOCHASTIC 8
 
 int mg_gemm(int a_layout, const void* A, int64_t lda,
             int b_layout, const void* B, int64_t ldb,

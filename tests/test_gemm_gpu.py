@@ -273,3 +273,85 @@ def test_hilo_product_is_fp32_accurate(M, N, K, out_dtype):
         got = out.double().cpu()
         assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
     assert bool((buf[:, N:] == 3.0).all())  # the other half of the packed buffer is untouched
+
+
+def _dev_operand(rows, k, layout, g, scale=1.0):
+    """bf16 operand [rows, k] (logical) stored K-contiguous ([rows, k]) or MN-contiguous ([k, rows])."""
+    logical = (torch.randn(rows, k, device=DEV, generator=g) * scale).to(torch.bfloat16)
+    return logical, (logical if layout == 0 else logical.t().contiguous())
+
+
+@pytest.mark.parametrize("al,bl,M,N,K", [
+    (0, 0, 16376, 1024, 1024),   # forward products: ragged M (rows past M read zero)
+    (0, 1, 16376, 1024, 2048),   # input gradients (B read through the transposed LDS read)
+    (1, 0, 4096, 4096, 1024),    # MN-contiguous A
+    (1, 1, 2048, 1024, 16376),   # weight gradients: ragged K tail, split along K
+    (1, 1, 4096, 1024, 1000),    # short ragged K
+])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_gemm_four_wave_tiles(al, bl, M, N, K, out_dtype):
+    """The four-wave 256 x 256 loop (mainloop_w4: every operand layout, no masked
+    loads) against fp64 products of the same bf16 operands."""
+    from gruboros_amd.gemm import gemm
+
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + al + 2 * bl)
+    a, ad = _dev_operand(M, K, al, g)
+    b, bd = _dev_operand(N, K, bl, g)
+    ref = a.double() @ b.double().t()
+    out = torch.full((M, N + 8), 5.0, device=DEV, dtype=out_dtype)[:, :N]
+    gemm(ad, al, bd, bl, M, N, K, out)
+    torch.cuda.synchronize()
+    if out_dtype == torch.float32:
+        assert _rel(out, ref) < 1e-5
+    else:
+        err = (out.double() - ref).abs()
+        assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+    if out_dtype == torch.float32 and al == 1 and bl == 1:
+        # deterministic (unsplit) and accumulating forms of the weight gradient
+        det = torch.empty(M, N, device=DEV)
+        gemm(ad, al, bd, bl, M, N, K, det, deterministic=True)
+        assert _rel(det, ref) < 1e-5
+        acc = torch.ones(M, N, device=DEV)
+        gemm(ad, al, bd, bl, M, N, K, acc, accumulate=True)
+        assert _rel(acc - 1.0, ref) < 1e-5
+
+
+def test_gemm_four_wave_epilogues():
+    """Epilogues on the four-wave tiles: bias, bias + GELU (pre-activation kept),
+    the GELU gradient on an input-gradient product, and the stochastic rounding
+    of a bf16 gradient (unbiased: the mean error of 16 M elements is ~0)."""
+    import torch.nn.functional as F
+
+    from gruboros_amd.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_GELU_GRAD, KCONTIG, MNCONTIG, gemm
+
+    g = torch.Generator(device=DEV).manual_seed(9)
+    M, N, K = 16376, 1024, 1024
+    a, _ = _dev_operand(M, K, 0, g)
+    b, _ = _dev_operand(N, K, 0, g, scale=0.05)
+    bias = torch.randn(N, device=DEV, generator=g)
+    acc64 = a.double() @ b.double().t()
+    y = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(a, KCONTIG, b, KCONTIG, M, N, K, y, epilogue=EPI_BIAS, bias=bias)
+    ref = acc64 + bias.double()
+    assert bool(((y.double() - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+    pre = torch.empty_like(y)
+    gemm(a, KCONTIG, b, KCONTIG, M, N, K, y, epilogue=EPI_BIAS_GELU, bias=bias, aux=pre)
+    assert bool(((pre.double() - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+    assert _rel(y, F.gelu(pre.double())) < 4e-3
+    # input-gradient layout with the GELU gradient: C = (dY W) * gelu'(pre)
+    wt, wt_mn = _dev_operand(N, K, 1, g, scale=0.05)  # B(k, n) stored [K, N]
+    dx = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(a, KCONTIG, wt_mn, MNCONTIG, M, N, K, dx, epilogue=EPI_GELU_GRAD, aux=pre)
+    p64 = pre.double().requires_grad_(True)
+    F.gelu(p64).backward(a.double() @ wt.double().t())
+    assert _rel(dx, p64.grad) < 4e-3
+    # stochastic rounding of a plain bf16 result: unbiased against the fp32 value
+    c32 = torch.empty(M, N, device=DEV)
+    gemm(a, KCONTIG, wt_mn, MNCONTIG, M, N, K, c32)
+    sr = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    gemm(a, KCONTIG, wt_mn, MNCONTIG, M, N, K, sr, stochastic=True)
+    rel_err = (sr.double() - c32.double()) / c32.double().abs().clamp_min(1e-3)
+    assert float(rel_err.abs().max()) <= 2.0 ** -7 * 1.01   # within one bf16 spacing
+    assert abs(float(rel_err.mean())) < 2e-5                # unbiased (round-to-nearest: also ~0, but
+    ne = (sr != c32.to(torch.bfloat16)).float().mean()       # it differs from round-to-nearest often)
+    assert float(ne) > 0.2
