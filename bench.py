@@ -5,12 +5,16 @@
                ff_mult 4, expansion 1.0, batch 8, seq 2048, bf16 activations,
                fp32 master weights, Schedule-Free AdamW step), counted as
                train.py:745 does (batch * chunk tokens per step).
-  roofline   = the scan backward kernel on cfg2 (B16 T8192 H2048 bf16, the
+  reference_loop = the same step in train.py:795-809's form (return_prev_hiddens,
+               loss.detach().item() after the forward, loss / grad_accum).
+  roofline   = the scan forward + backward on cfg2 (B16 T8192 H2048 bf16, the
                scan microbenchmark BASELINE.json names), HBM-bound; achieved =
-               12 B/element (algorithmic bytes) * 2^28 / its average launch time.
+               (6 + 12) B/element (algorithmic bytes) * 2^28 / the summed average
+               launch times of the two kernels; forward and backward beside it.
   scan       = cfg2 forward, backward and forward+backward figures.
-  cpu_baseline = the oracle's fp32 restatement of the reference path on the
-               host's cores, on a bounded sample of the cfg3 step.
+  cpu_baseline = the oracle's fp32 restatement of the reference step on the
+               host's cores at the cfg3 shape (forward, backward, SF-AdamW step);
+               cpu_baseline_scan = the oracle's cfg2 scan at batch 1, scaled x16.
 Inputs are synthetic and already resident in HBM when the timed region starts.
 """
 import argparse
@@ -47,9 +51,12 @@ def cfg3_matmul_params(dim=1024, depth=8, ff_mult=4, vocab=256, expansion=1.0):
     return depth * per_layer + vocab * dim
 
 
-def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8, accum=1):
+def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8, accum=1, ref_loop=False):
     """One optimizer step = `accum` forward+backward micro-steps on [B, S] ids (the loss
-    scaled by 1/accum as in train.py:798-800), then the Schedule-Free AdamW step."""
+    scaled by 1/accum as in train.py:798-800), then the Schedule-Free AdamW step.
+    ref_loop: each micro-step as train.py:795-801 writes it: the model called with
+    return_prev_hiddens=True, the loss read to the host (loss.detach().item(), one
+    device sync per micro-step) before loss / grad_accum is backpropagated."""
     import torch
 
     from gruboros_amd.mingru.minLM import minLM
@@ -70,6 +77,16 @@ def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8, accum=1):
         opt.step()
         opt.zero_grad(set_to_none=True)
         return loss
+
+    if ref_loop:
+        def step():  # noqa: F811
+            for i in range(accum):
+                loss, _hiddens = model(ids[i], return_loss=True, return_prev_hiddens=True, prev_hiddens=None)
+                step.chunk_loss = loss.detach().item()
+                (loss / accum).backward()
+            opt.step()
+            opt.zero_grad()
+            return loss
 
     for _ in range(warmup):
         step()
@@ -295,47 +312,95 @@ def bench_kernels(reps=20, N=8 * 2047, D=1024, F=4096, V=256):
     return out
 
 
-def cpu_baseline(seconds_budget=20.0, B=1, S=512, dim=1024, depth=8):
-    """The oracle's fp32 restatement of the reference step (mingru/minLM.py:86-155
-    forward + autograd backward) on the host's cores, on a bounded sample of cfg3:
-    one sequence of S tokens per step, same model shape."""
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_baseline(B=2, S=2048, dim=1024, depth=8, max_steps=2, seconds_budget=30.0):
+    """The oracle's fp32 restatement of the reference step at the cfg3 model shape and
+    sequence length on the host's cores: forward and autograd backward of
+    mingru/minLM.py:86-155 (conv and dropout off), then the Schedule-Free AdamW step
+    (oracle.sf_adamw, the package's update; train.py:808). One untimed warm-up step
+    on a [1, 256] batch, then [B, S] steps (at least one, at most `max_steps`, while
+    under `seconds_budget`); the median step time gives tokens/s. The default batch
+    is 2 of cfg3's 8 sequences, which keeps the sample near 10-30 s of CPU work:
+    every op but the optimizer step is linear in the batch, so tokens/s carries over
+    (the full batch-8 step takes ~2 min on 8 cores)."""
+    import torch
+
+    from oracle import mingru_oracle as O
+    from oracle.sf_adamw import RefAdamWScheduleFree
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=1.0, seed=0)
+    params = {k: v.clone().requires_grad_(True) for k, v in sd.items()}
+    opt = RefAdamWScheduleFree(list(params.values()), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01)
+    gen = torch.Generator().manual_seed(0)
+
+    def one(ids):
+        loss, _ = O.minlm_forward(params, ids, depth, return_loss=True, dtype=torch.float32)
+        loss.backward()
+        opt.step([p.grad for p in params.values()])
+        for p in params.values():
+            p.grad = None
+
+    one(torch.randint(0, 256, (1, 256), generator=gen))  # warm-up
+    ids = torch.randint(0, 256, (B, S), generator=gen)
+    times = []
+    t_start = time.perf_counter()
+    while not times or (len(times) < max_steps and time.perf_counter() - t_start + times[-1] < seconds_budget):
+        t0 = time.perf_counter()
+        one(ids)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": B * (S - 1) / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "s_per_step": med,
+            "sample": f"cfg3 model and sequence length (d{dim} L{depth} ff4 vocab 256), batch {B} x seq {S} "
+                      f"(cfg3: batch 8): fp32 forward + backward + "
+                      f"SF-AdamW step of the oracle restatement, median of {len(times)} full steps after a "
+                      f"[1, 256] warm-up; torch CPU with {cores} threads on {_cpu_name()}"}
+
+
+def cpu_baseline_scan(T=8192, Di=2048, B_full=16):
+    """The oracle's restatement of the reference scan (mingru/minGRU.py:53-69, log-space
+    Heinsen scan) forward + autograd backward in fp32 on the host's cores, at cfg2's
+    shape with batch 1; the cfg2 figure (batch 16) is 16x its time."""
     import torch
 
     from oracle import mingru_oracle as O
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=1.0, seed=0)
-    params = {k: v.clone().requires_grad_(True) for k, v in sd.items()}
     gen = torch.Generator().manual_seed(0)
-    ids = torch.randint(0, 256, (B, S), generator=gen)
+    hidden = torch.randn(1, T, Di, generator=gen).requires_grad_(True)
+    gate = torch.randn(1, T, Di, generator=gen).requires_grad_(True)
+    h0 = O.g(torch.randn(1, 1, Di, generator=gen))
+    dh = torch.randn(1, T, Di, generator=gen)
 
     def one():
-        loss, _ = O.minlm_forward(params, ids, depth, return_loss=True, dtype=torch.float32)
-        loss.backward()
+        out, _ = O.mingru_scan(hidden, gate, h0)
+        out.backward(dh)
+        hidden.grad = gate.grad = None
 
     one()  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < seconds_budget and len(times) < 10):
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > seconds_budget:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": B * S / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"cfg3 model shape (d{dim} L{depth}), batch {B} x seq {S}, fp32 forward+backward "
-                      f"(no optimizer), median of {len(times)} steps; {cpu}"}
+    t0 = time.perf_counter()
+    one()
+    dt = time.perf_counter() - t0
+    n_full = B_full * T * Di
+    t_full = dt * B_full
+    return {"value": 18.0 * n_full / t_full / 1e9, "unit": "GB/s (cfg2 algorithmic bytes, 18 B/element)",
+            "cores": cores, "kind": "port", "s_cfg2_fwd_bwd": t_full,
+            "sample": f"oracle log-space scan fp32 forward + autograd backward at batch 1 x T {T} x H {Di} "
+                      f"({dt:.2f} s), scaled x{B_full} to cfg2's batch; torch CPU with {cores} threads "
+                      f"on {_cpu_name()}"}
 
 
 def main():
@@ -376,7 +441,7 @@ def main():
         print("[bench] copy calibration: 3 x 1 GiB device copies (1073741824 B read + written each)",
               file=sys.stderr, flush=True)
 
-    train = scan = kern = dec = ceil = None
+    train = ref = scan = kern = dec = ceil = None
     # The training step (`value`) runs first: after the decode phase's ~0.6 s
     # of light, latency-bound work the first training steps run ~25% slower
     # (measured: 14.9 vs 11.9 ms/step, back to 11.9 on a second run).
@@ -386,6 +451,14 @@ def main():
         else:
             train = bench_train(args.steps, args.warmup)
         print(f"[bench] train {json.dumps(train)}", file=sys.stderr, flush=True)
+        if args.workload == "cfg3":
+            r = bench_train(args.steps, args.warmup, ref_loop=True)
+            ref = {"ms_per_step": r["ms_per_step"], "value": r["tokens_per_step"] / (r["ms_per_step"] * 1e-3),
+                   "unit": "tokens/s",
+                   "form": "train.py:795-809: model(chunk, return_loss=True, return_prev_hiddens=True, "
+                           "prev_hiddens=None); loss.detach().item(); (loss / grad_accum).backward(); "
+                           "optimizer.step(); optimizer.zero_grad() (grad_accum 1)"}
+            print(f"[bench] reference loop {json.dumps(ref)}", file=sys.stderr, flush=True)
     if args.only in (None, "ceilings"):
         ceil = bench_ceilings()
         print(f"[bench] ceilings {json.dumps(ceil)}", file=sys.stderr, flush=True)
@@ -398,10 +471,12 @@ def main():
     if args.only in (None, "decode"):
         dec = bench_decode()
         print(f"[bench] decode {json.dumps(dec)}", file=sys.stderr, flush=True)
-    cpu = None
+    cpu = cpu_scan = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
         print(f"[bench] cpu {json.dumps(cpu)}", file=sys.stderr, flush=True)
+        cpu_scan = cpu_baseline_scan()
+        print(f"[bench] cpu scan {json.dumps(cpu_scan)}", file=sys.stderr, flush=True)
 
     out = {
         "metric": METRIC,
@@ -417,7 +492,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (uniform random byte ids; random-init weights; scan inputs N(0,1))",
         "config": ({"workload": "cfg3 minLM train step (vocab 256, d1024, L8, ff4, exp1.0, B8, seq2048, "
-                                "SF-AdamW) for value; cfg2 scan B16 T8192 H2048 bf16 for roofline",
+                                "SF-AdamW) for value; cfg2 scan B16 T8192 H2048 bf16 forward+backward for roofline",
                     "global_batch": 8, "seq_len": 2048, "parallelism": "single GPU"}
                    if args.workload == "cfg3" else
                    {"workload": "cfg5 minLM train step (vocab 256, d2048, L24, ff4, exp1.0, B4, seq4096, "
@@ -425,14 +500,21 @@ def main():
                     "global_batch": 16, "seq_len": 4096, "parallelism": "single GPU"}),
     }
     if scan:
-        bwd_gbs = scan["bwd_GBs"]
-        out["roofline"] = {"kernel": "scan_bwd_kernel<bf16,bf16> (cfg2)", "bound": "hbm", "achieved": bwd_gbs,
-                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bwd_gbs / HBM_PEAK_GBS,
-                           "traffic": measured_traffic("scan_bwd_kernel"),
-                           "algorithmic_bytes": 12 * scan["elements"],
-                           "note": "achieved = 12 B/element x 2^28 / mean launch time of the timed launches "
-                                   "(HIP events on the launch stream, after ~30 ms of warm-up); traffic = "
-                                   "calibrated FETCH_SIZE+WRITE_SIZE bytes per launch "
+        fb_gbs = scan["fwd_bwd_GBs"]
+        tf, tb = measured_traffic("scan_fwd_kernel"), measured_traffic("scan_bwd_kernel")
+        out["roofline"] = {"kernel": "scan_fwd_kernel + scan_bwd_kernel <bf16,bf16> (cfg2)", "bound": "hbm",
+                           "achieved": fb_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": fb_gbs / HBM_PEAK_GBS,
+                           "traffic": (tf + tb) if tf is not None and tb is not None else None,
+                           "algorithmic_bytes": 18 * scan["elements"],
+                           "forward": {"achieved": scan["fwd_GBs"], "frac": scan["fwd_GBs"] / HBM_PEAK_GBS,
+                                       "us": scan["fwd_ms"] * 1e3, "algorithmic_bytes": 6 * scan["elements"],
+                                       "traffic": tf},
+                           "backward": {"achieved": scan["bwd_GBs"], "frac": scan["bwd_GBs"] / HBM_PEAK_GBS,
+                                        "us": scan["bwd_ms"] * 1e3, "algorithmic_bytes": 12 * scan["elements"],
+                                        "traffic": tb},
+                           "note": "achieved = (6 + 12) B/element x 2^28 / (forward + backward mean launch time "
+                                   "of the timed launches; HIP events on the launch stream, after ~30 ms of "
+                                   "warm-up); traffic = calibrated FETCH_SIZE+WRITE_SIZE bytes per launch pair "
                                    "(profiles/scan_cfg2_traffic.md)"}
         out["scan"] = scan
     if train:
@@ -447,8 +529,12 @@ def main():
         out["kernels"] = kern
     if dec:
         out["decode"] = dec
+    if ref:
+        out["reference_loop"] = ref
     if cpu:
         out["cpu_baseline"] = cpu
+    if cpu_scan:
+        out["cpu_baseline_scan"] = cpu_scan
     print(json.dumps(out), flush=True)
 
 

@@ -19,12 +19,19 @@
 // at chunk c ^ ((r ^ (r >> 3)) & 7)) and a fragment is one 16-byte LDS
 // read; MN-contiguous tiles stay [64 k][rows] and their fragments come
 // through the LDS transpose read (two 8-byte reads).
-// Two main loops (measured on MI355X, the faster one per layout):
-//   mainloop     one barrier per k-tile, the fragments of the next k-step
-//                (also across tiles) read under the MFMAs of the current one;
-//   mainloop_pp  256 x 256 with an MN-contiguous B (the input gradient):
-//                two wave groups alternate between reading a whole k-tile of
-//                fragments and multiplying it, a barrier between phases.
+// Main loops (measured on MI355X):
+//   mainloop_w8  256 x 256, eight waves (two per SIMD, 64 x 128 each), any
+//                layout without masking (K % 64 == 0 for a K-contiguous
+//                operand, a multiple of 256 rows for an MN-contiguous one):
+//                every product of the cfg3 step, except the GELU-gradient
+//                epilogue, which runs
+//   mainloop_w4  the same pipeline with four waves of 128 x 128;
+//   mainloop     masked tiles of other shapes, one barrier per k-tile, the
+//                fragments of the next k-step read under the MFMAs of the
+//                current one;
+//   mainloop_pp  masked 256 x 256 with an MN-contiguous B: two wave groups
+//                alternate between reading a whole k-tile of fragments and
+//                multiplying it, a barrier between phases.
 //
 // The MFMA is fed the B fragment as its first operand and the A fragment as
 // its second, so a lane's accumulator holds C[m][n..n+3] (4 consecutive
@@ -454,6 +461,8 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 constexpr int kW4Rows = 256;                         // tile rows per operand
 constexpr int kW4Loads = kW4Rows * 8 / 64 / 4;       // load instructions per operand and wave (8)
 
+// init<NL> / load<NL>: NL load instructions per operand and wave (the tile's
+// 2048 16-byte chunks over the workgroup's waves: 8 for four waves, 4 for eight).
 template <bool KMAJ>
 struct W4Operand;
 
@@ -461,21 +470,22 @@ struct W4Operand;
 // 16-byte read per fragment.
 template <>
 struct W4Operand<true> {
-  static constexpr int kReads = 4;  // fragment reads per k-step (4 blocks of 32 rows)
+  static constexpr int kReadsPerBlock = 1;  // fragment reads per 32-row block and k-step
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t v[kW4Loads];
   uint32_t p0, p1;  // fragment addresses of even / odd 32-row blocks
   // r0: first matrix row of the tile; wr: first tile row of this wave's 128
+  template <int NL = kW4Loads>
   __device__ __forceinline__ void init(const Operand& o, int r0, int wr, int wave, int lane) {
     rsrc = o.rsrc;
 #pragma unroll
-    for (int i = 0; i < kW4Loads; ++i) {
-      const int r = (wave * kW4Loads + i) * 8 + (lane >> 3);
+    for (int i = 0; i < NL; ++i) {
+      const int r = (wave * NL + i) * 8 + (lane >> 3);
       const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
       v[i] = static_cast<uint32_t>(r0 + r) * o.ld2 + static_cast<uint32_t>(c) * 16u;
     }
     // row wr + 32 i + L, chunk (2 s + half) ^ f(row), f(r) = (r ^ (r >> 3)) & 7;
-    // f(wr + 32 i + L) = f(wr + L) ^ 4 (i & 1) for wr a multiple of 128
+    // f(wr + 32 i + L) = f(wr + L) ^ 4 (i & 1) for wr a multiple of 64
     const int L = lane & 31, half = lane >> 5, r = wr + L;
     p0 = static_cast<uint32_t>(r * 128 + ((half ^ ((r ^ (r >> 3)) & 7)) << 4));
     p1 = p0 ^ 64u;
@@ -483,8 +493,9 @@ struct W4Operand<true> {
   __device__ __forceinline__ uint32_t koff(int k0, int kofs, uint32_t) const {
     return static_cast<uint32_t>(k0 + kofs) * 2u;
   }
+  template <int NL = kW4Loads>
   __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko) const {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * kW4Loads + i) * 64),
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * NL + i) * 64),
                                              16, v[i] + ko, 0, 0, 0);
   }
   __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int i) const {
@@ -497,22 +508,23 @@ struct W4Operand<true> {
 // fragments through the LDS transpose read (two 8-byte reads each).
 template <>
 struct W4Operand<false> {
-  static constexpr int kReads = 8;
+  static constexpr int kReadsPerBlock = 2;
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t v[kW4Loads];
   uint32_t fb[4];  // byte address of block i's first read at k-step 0
+  template <int NL = kW4Loads>
   __device__ __forceinline__ void init(const Operand& o, int r0, int wr, int wave, int lane) {
     rsrc = o.rsrc;
 #pragma unroll
-    for (int i = 0; i < kW4Loads; ++i) {
-      const int chunk = (wave * kW4Loads + i) * 64 + lane;
+    for (int i = 0; i < NL; ++i) {
+      const int chunk = (wave * NL + i) * 64 + lane;
       const int kr = chunk >> 5, cpos = chunk & 31;
       const int m = (((cpos >> 1) ^ tr_swz(kr)) << 4) + ((cpos & 1) << 3);
       v[i] = static_cast<uint32_t>(kr) * o.ld2 + static_cast<uint32_t>(r0 + m) * 2u;
     }
     // read_frag<256, false>: k-row 16 s + 8 (g >> 1) + j, column wr + 32 i + 16 (g & 1) + 4 q;
-    // tr_swz of that k-row is tr_swz(j), and the xor only touches the low 3 bits of
-    // (column >> 4) since wr is a multiple of 128
+    // tr_swz of that k-row is tr_swz(j) (the xor is applied to the absolute
+    // 16-column block index, which the loader swizzled the same way)
     const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -521,8 +533,9 @@ struct W4Operand<false> {
     }
   }
   __device__ __forceinline__ uint32_t koff(int k0, int, uint32_t ld2) const { return static_cast<uint32_t>(k0) * ld2; }
+  template <int NL = kW4Loads>
   __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko) const {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * kW4Loads + i) * 64),
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * NL + i) * 64),
                                              16, v[i] + ko, 0, 0, 0);
   }
   __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int i) const {
@@ -580,7 +593,7 @@ __device__ __forceinline__ void mainloop_w4(const Params& p, uint4* sa, uint4* s
       for (int j = 0; j < 4; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
   };
-  constexpr int NR = W4Operand<AK>::kReads + W4Operand<BKM>::kReads;  // fragment reads per k-step
+  constexpr int NR = 4 * (W4Operand<AK>::kReadsPerBlock + W4Operand<BKM>::kReadsPerBlock);  // reads per k-step
   const int n = kt1 - kt0;
   {
     uint32_t ao, bo;
@@ -626,6 +639,118 @@ __device__ __forceinline__ void mainloop_w4(const Params& p, uint4* sa, uint4* s
     tile(t + 1, sb, sa);
   }
   if (t < n) tile(t, sa, sb);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// Eight-wave pipelined main loop, 256 x 256 tiles: mainloop_w4's stage
+// pipeline with two waves per SIMD, each owning 64 x 128 of the tile (2 x 4
+// blocks, 128 accumulator registers), all eight multiplying at once. A second
+// wave per SIMD keeps the matrix core busier than one wave issuing back to
+// back (measured on random operands: about 1.8-2.0 against 1.7 PFLOP/s for
+// 32x32x16 bf16), at 1.5x the fragment reads per MFMA of the 128 x 128 wave
+// tile. Waves 0-3 (one per SIMD) also issue the tile loads, 16 per k-tile
+// each, so every SIMD has one wave whose MFMA stream no load interrupts
+// (measured 4-6% faster than all eight waves loading).
+template <bool AK, bool BKM>
+__device__ __forceinline__ void mainloop_w8(const Params& p, uint4* sa, uint4* sb, int m0, int n0, int kt0, int kt1,
+                                            f32x16 (&acc)[2][4]) {
+  constexpr int S = BK / 16;
+  constexpr int kLoaders = 4;                  // waves 0..3 load
+  constexpr int NL = kW4Loads * 4 / kLoaders;  // load instructions per operand and loading wave
+  constexpr int kStageA = kW4Rows * 8;         // uint4 of the A tile (B follows)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // tile rows 64 wm .., columns 128 wn ..
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  W4Operand<AK> A;
+  W4Operand<BKM> B;
+  A.template init<NL>(oa, m0, wm * 64, wave % kLoaders, lane);
+  B.template init<NL>(ob, n0, wn * 128, wave % kLoaders, lane);
+  auto koffs = [&](int t, uint32_t& ao, uint32_t& bo) {
+    const int tg = min(kt0 + t, kt1 - 1);
+    int seg = 0, k0 = tg * BK;
+    if (p.hilo) {
+      seg = tg / p.nkt_seg;
+      k0 = (tg - seg * p.nkt_seg) * BK;
+    }
+    ao = A.koff(k0, seg == 1 ? p.K : 0, oa.ld2);
+    bo = B.koff(k0, seg == 2 ? p.K : 0, ob.ld2);
+  };
+  bf16x8 af[2][2], bfr[2][4];
+  auto read_step = [&](const uint4* st, int s, int buf) {
+    af[buf][0] = A.frag(st, s, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[buf][j] = B.frag(st + kStageA, s, j);
+    af[buf][1] = A.frag(st, s, 1);
+  };
+  auto mfma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NR = 2 * W4Operand<AK>::kReadsPerBlock + 4 * W4Operand<BKM>::kReadsPerBlock;
+  const int n = kt1 - kt0;
+  // The whole loop once per role, so a loading wave's loads and MFMAs share
+  // one instruction block (and one schedule).
+  auto run = [&](auto role) __attribute__((always_inline)) {
+    constexpr bool kLoad = decltype(role)::value;
+    if constexpr (kLoad) {
+      uint32_t ao, bo;
+      koffs(0, ao, bo);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) A.template load<NL>(sa, wave, i, ao);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) B.template load<NL>(sa + kStageA, wave, i, bo);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    read_step(sa, 0, 0);
+    auto tile = [&](int t, const uint4* cur, uint4* nxt) __attribute__((always_inline)) {
+      uint32_t ao = 0, bo = 0;
+      if constexpr (kLoad) koffs(t + 1, ao, bo);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int c = s & 1;
+        if constexpr (kLoad) {
+          if (s == 0) {
+#pragma unroll
+            for (int i = 0; i < NL; ++i) A.template load<NL>(nxt, wave, i, ao);
+          } else if (s == 1) {
+#pragma unroll
+            for (int i = 0; i < NL; ++i) B.template load<NL>(nxt + kStageA, wave, i, bo);
+          }
+        }
+        if (s + 1 < S) {
+          read_step(cur, s + 1, c ^ 1);
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();  // tile t + 1 is in `nxt` for every wave; every wave is done with `cur`
+          read_step(nxt, 0, c ^ 1);
+        }
+        mfma_step(c);
+        if (kLoad && s < 2) interleave<8, NR, NL>();
+        else interleave<8, NR, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    int t = 0;
+    for (; t + 1 < n; t += 2) {
+      tile(t, sa, sb);
+      tile(t + 1, sb, sa);
+    }
+    if (t < n) tile(t, sa, sb);
+  };
+  if (wave < kLoaders) run(std::true_type{});
+  else run(std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 }
@@ -765,7 +890,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
   // 128 x 128 tiles keep their stages as two distinct objects (the
   // interleaved schedule needs that); 256 x 256 tiles one array of two.
-  constexpr bool kSplit = BM != 256 || WM * WN == 4;
+  constexpr bool kW8 = BM == 256 && BN == 256 && WM == 4 && WN == 2;  // mainloop_w8
+  constexpr bool kSplit = BM != 256 || WM * WN == 4 || kW8;
   __shared__ uint4 smem[kSplit ? kStage : 2 * kStage];
   __shared__ uint4 smem_b[kSplit ? kStage : 1];
   uint4* const stage1 = kSplit ? smem_b : smem + kStage;
@@ -784,6 +910,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);  // both stages in smem (kSplit is false)
   else if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 2)
     mainloop_w4<AK, BKM>(p, smem, stage1, m0, n0, kt0, kt1, acc);
+  else if constexpr (kW8)
+    mainloop_w8<AK, BKM>(p, smem, stage1, m0, n0, kt0, kt1, acc);
   else
     mainloop<BM, BN, WM, WN, AK, BKM, (BM == 256), kSplit>(p, smem, stage1, m0, n0, kt0, kt1, acc);
 
@@ -799,8 +927,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   constexpr int CQ = RB / 16;                // 16-byte chunks per row
   constexpr int EPC = 16 / int(sizeof(S));   // elements per chunk
   constexpr int RPI = 64 / CQ;               // rows per read instruction
-  static_assert(32 * RB * WM * WN <= int(sizeof(smem)), "staging fits in the first operand stage");
-  unsigned char* stage = reinterpret_cast<unsigned char*>(smem) + wave * 32 * RB;
+  // (eight-wave 256 x 256 tiles: waves 0-3 stage in the first operand stage, 4-7 in the second)
+  constexpr int kStWaves = kW8 ? 4 : WM * WN;
+  static_assert(32 * RB * kStWaves <= int(sizeof(smem)), "staging fits in the operand stages");
+  unsigned char* stage = reinterpret_cast<unsigned char*>(kW8 && wave >= 4 ? stage1 : smem) + (wave % kStWaves) * 32 * RB;
   const int row0 = m0 + wm * (BM / WM), col0 = n0 + wn * NW;
   // A lane reads back the same columns for every row: col0 + (lane % CQ) * EPC.
   const int qc = lane % CQ;
@@ -812,7 +942,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   // The GELU gradient's pre-activations (bf16) of block i+1 stream straight
   // into LDS (unswizzled [32 rows][NW]) while block i is written out.
   constexpr int PB = 32 * NW * 2;  // bytes per pre-activation block and wave
-  static_assert(EPI != EPI_GELU_GRAD || 2 * PB * WM * WN <= kStage * 16, "aux staging");
+  static_assert(EPI != EPI_GELU_GRAD || (!kW8 && 2 * PB * WM * WN <= kStage * 16), "aux staging");
   unsigned char* pstage = reinterpret_cast<unsigned char*>(stage1) + wave * 2 * PB;
   Operand oaux;
   if constexpr (EPI == EPI_GELU_GRAD) oaux = make_operand(p.aux, p.ldaux, p.aux_span);
@@ -1089,14 +1219,14 @@ int dispatch_epi(const Params& p, const Plan& pl, int epi, int c_dtype, hipStrea
     if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, C_STORE>(p, pl, s);
-    if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, C_STORE>(p, pl, s);
+    if constexpr (!(WM == 4 && WN == 2))  // (no room for the pre-activation staging next to eight waves)
+      if (epi == EPI_GELU_GRAD) return launch<BM, BN, WM, WN, AK, BKM, EPI_GELU_GRAD, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_SR) return launch<BM, BN, WM, WN, AK, BKM, EPI_SR, bf16_t, C_STORE>(p, pl, s);
   }
   return fail(MG_ERR_ARG, "mg_gemm: epilogue %d not available for this output dtype", epi);
 }
 
-// 256 x 256 tiles run 8 waves (two per SIMD), 128 x 128 tiles 4.
-// Whether a product meets the four-wave loop's no-mask conditions.
+// Whether a product meets the pipelined loops' no-mask conditions.
 inline bool w4_ok(const Params& p, bool ak, bool bk) {
   if ((ak || bk) && p.K % BK) return false;
   if (!ak && p.M % kW4Rows) return false;
@@ -1104,13 +1234,23 @@ inline bool w4_ok(const Params& p, bool ak, bool bk) {
   return true;
 }
 
-// 256 x 256 tiles run the four-wave pipelined loop (mainloop_w4) when the
-// product meets its conditions (w4_ok), else 8 waves.
+// 256 x 256 tiles run the eight-wave pipelined loop (mainloop_w8) when the
+// product meets the no-mask conditions (w4_ok); the GELU-gradient epilogue
+// (whose pre-activation staging needs the second operand stage) runs the
+// four-wave one (mainloop_w4); other products the masked 8-wave loops.
 template <int BM, int BN>
 int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, int c_dtype, hipStream_t s) {
   constexpr int WN = BM * BN >= 256 * 256 ? 4 : 2;
 #ifndef MG_GEMM_NO_W4
   if constexpr (BM == 256 && BN == 256) {
+#ifndef MG_GEMM_NO_W8
+    if (w4_ok(p, ak, bk) && epi != EPI_GELU_GRAD) {
+      if (ak && bk) return dispatch_epi<256, 256, 4, 2, true, true>(p, pl, epi, c_dtype, s);
+      if (ak && !bk) return dispatch_epi<256, 256, 4, 2, true, false>(p, pl, epi, c_dtype, s);
+      if (!ak && !bk) return dispatch_epi<256, 256, 4, 2, false, false>(p, pl, epi, c_dtype, s);
+      return dispatch_epi<256, 256, 4, 2, false, true>(p, pl, epi, c_dtype, s);
+    }
+#endif
     if (w4_ok(p, ak, bk)) {
       if (ak && bk) return dispatch_epi<256, 256, 2, 2, true, true>(p, pl, epi, c_dtype, s);
       if (ak && !bk) return dispatch_epi<256, 256, 2, 2, true, false>(p, pl, epi, c_dtype, s);
