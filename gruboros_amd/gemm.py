@@ -28,6 +28,15 @@ def spans_ok(rows, ld):
     return (rows + 256) * ld * 2 < (1 << 31)
 
 
+def _row_step(n, *row_bytes):
+    """Rows per launch for a row-parallel product over n rows: every operand
+    (row_bytes: its bytes per row) then spans under 2 GiB, mg_gemm's buffer
+    range (with its 256 rows of slack); a multiple of 256 rows."""
+    r = ((1 << 31) - 1) // max(max(row_bytes), 1) - 257
+    r = max(256, r // 256 * 256)
+    return n if n <= r else r
+
+
 def fits(a, w):
     """Whether linear_fwd(a, w) and linear_dx(a, w) (with a GELU pre-activation
     of a's rows) meet mg_gemm's rules: bf16 2-D tensors with unit inner
@@ -93,7 +102,12 @@ def linear_fwd(x, w, bias=None, *, gelu_pre=None, out_dtype=torch.bfloat16):
         epi = EPI_BIAS_GELU
     else:
         epi = EPI_BIAS if bias is not None else EPI_NONE
-    return gemm(x, KCONTIG, w, KCONTIG, n, o, k, y, epilogue=epi, bias=bias, aux=gelu_pre)
+    step = _row_step(n, 2 * x.stride(0), o * y.element_size(), 2 * o if gelu_pre is not None else 0)
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        gemm(x[r0:r1], KCONTIG, w, KCONTIG, r1 - r0, o, k, y[r0:r1], epilogue=epi, bias=bias,
+             aux=gelu_pre[r0:r1] if gelu_pre is not None else None)
+    return y
 
 
 def split_hilo(x, out=None):
@@ -120,7 +134,11 @@ def linear_fwd_hilo(x_pair, w_pair, out, K):
     """out[N, O] = x w^T to fp32 accuracy from hi/lo pairs: x_pair [N, 2K], w_pair [O, 2K] (bf16);
     out bf16 or fp32, any row stride."""
     n, o = x_pair.shape[0], w_pair.shape[0]
-    return gemm(x_pair, KCONTIG, w_pair, KCONTIG, n, o, K, out, hilo=True)
+    step = _row_step(n, 2 * x_pair.stride(0), out.stride(0) * out.element_size())
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        gemm(x_pair[r0:r1], KCONTIG, w_pair, KCONTIG, r1 - r0, o, K, out[r0:r1], hilo=True)
+    return out
 
 
 def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16, stochastic=False):
@@ -129,9 +147,14 @@ def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16, stochastic=Fals
     n, o = dy.shape
     k = w.shape[1]
     dx = torch.empty(n, k, device=dy.device, dtype=out_dtype)
-    return gemm(dy, KCONTIG, w, MNCONTIG, n, k, o, dx,
-                epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE, aux=gelu_pre,
-                stochastic=stochastic and gelu_pre is None and out_dtype == torch.bfloat16)
+    step = _row_step(n, 2 * dy.stride(0), k * dx.element_size(), 2 * k if gelu_pre is not None else 0)
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        gemm(dy[r0:r1], KCONTIG, w, MNCONTIG, r1 - r0, k, o, dx[r0:r1],
+             epilogue=EPI_GELU_GRAD if gelu_pre is not None else EPI_NONE,
+             aux=gelu_pre[r0:r1] if gelu_pre is not None else None,
+             stochastic=stochastic and gelu_pre is None and out_dtype == torch.bfloat16)
+    return dx
 
 
 def linear_dw(dy, x, out=None, accumulate=False, deterministic=None):
@@ -140,4 +163,10 @@ def linear_dw(dy, x, out=None, accumulate=False, deterministic=None):
     k = x.shape[1]
     if out is None:
         out = torch.empty(o, k, device=dy.device, dtype=torch.float32)
-    return gemm(dy, MNCONTIG, x, MNCONTIG, o, k, n, out, accumulate=accumulate, deterministic=deterministic)
+    # over 2 GiB of rows: the sum along rows in blocks, each added to the last
+    step = _row_step(n, 2 * dy.stride(0), 2 * x.stride(0))
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        gemm(dy[r0:r1], MNCONTIG, x[r0:r1], MNCONTIG, o, k, r1 - r0, out, accumulate=accumulate or r0 > 0,
+             deterministic=deterministic)
+    return out

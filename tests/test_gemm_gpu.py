@@ -355,3 +355,31 @@ def test_gemm_four_wave_epilogues():
     assert abs(float(rel_err.mean())) < 2e-5                # unbiased (round-to-nearest: also ~0, but
     ne = (sr != c32.to(torch.bfloat16)).float().mean()       # it differs from round-to-nearest often)
     assert float(ne) > 0.2
+
+
+def test_products_over_2gib_run_in_row_blocks():
+    """Operands spanning more than mg_gemm's 2 GiB buffer range (the cfg4
+    full-length FeedForward: 262,144 rows x 4096) run as row blocks: the
+    forward and input-gradient products block by row, the weight gradient by
+    K, each block added to the last. Checked around the block boundary and at
+    the end against fp32 products of the same bf16 operands."""
+    from gruboros_amd.gemm import _row_step, linear_dw, linear_fwd
+
+    N, K, O = 1_100_000, 1024, 256
+    step = _row_step(N, 2 * K, 2 * O)
+    assert step < N  # the product is split
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(N, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn(O, K, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    y = linear_fwd(x, w)
+    for r0, r1 in ((0, 256), (step - 512, step + 512), (N - 300, N)):
+        ref = x[r0:r1].float() @ w.float().t()
+        err = (y[r0:r1].float() - ref).abs().max() / ref.abs().max()
+        assert float(err) < 8e-3, (r0, float(err))
+    dy = torch.randn(N, O, device=DEV, generator=g).to(torch.bfloat16)
+    dw = linear_dw(dy, x)
+    ref = torch.zeros(O, K, device=DEV, dtype=torch.float64)
+    for r0 in range(0, N, 1 << 18):
+        ref += (dy[r0:r0 + (1 << 18)].float().t() @ x[r0:r0 + (1 << 18)].float()).double()
+    err = (dw.double() - ref).abs().max() / ref.abs().max()
+    assert float(err) < 1e-4, float(err)

@@ -95,6 +95,25 @@ def test_minlm_loss_and_grads(dtype, expansion):
         assert e_loss <= 2e-2 and e_hid <= 2e-2 and worst[0] <= 2e-2
 
 
+def test_minlm_bf16_feed_forward_forward_on_mg_gemm(monkeypatch):
+    """The FeedForward forward on mg_gemm's bias + GELU and bias epilogues
+    (blocks.FF_FORWARD_MG_GEMM) keeps the bf16 step within 2e-2 of fp64."""
+    from gruboros_amd import blocks
+
+    monkeypatch.setattr(blocks, "FF_FORWARD_MG_GEMM", True)
+    dim, depth, B, S = 64, 2, 2, 130
+    m, sd = _model(dim, depth, 1.0, torch.bfloat16)
+    ids = torch.randint(0, 256, (B, S), generator=torch.Generator().manual_seed(7))
+    loss = m(ids.to(DEV), return_loss=True)
+    loss.backward()
+    p = {k: v.double().requires_grad_(True) for k, v in sd.items()}
+    ref, _ = O.minlm_forward(p, ids, depth, return_loss=True, dtype=torch.float64)
+    ref.backward()
+    assert abs(float(loss) - float(ref)) / abs(float(ref)) <= 2e-2
+    worst = max((_rel(prm.grad, p[n].grad), n) for n, prm in m.named_parameters())
+    assert worst[0] <= 2e-2, worst
+
+
 def test_mingru_module_cfg1_fp32():
     """cfg1: one minGRU layer, dim 512, expansion 1.0, B4 T1024, fp32, x ~ N(0,1), no prev_hidden."""
     from gruboros_amd.mingru.minGRU import minGRU
