@@ -1069,6 +1069,13 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   const int m0 = blockIdx.x * BM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int L = lane & 31, half = lane >> 5;
+  // this wave's 16 labels, one per lane, loaded before the product so their
+  // latency hides under it (read per row, each would be a dependent load)
+  int64_t my_lab = 0;
+  {
+    const int64_t row = static_cast<int64_t>(m0) + wave * (BM / 4) + lane;
+    if (lane < BM / 4 && row < p.M) my_lab = labels[row];
+  }
   f32x16 acc[MB][NB];
   mainloop<BM, BN, WM, WN, true, true, false>(p, smem, smem + kStage, m0, 0, 0, (p.K + BK - 1) / BK, acc);
 
@@ -1089,45 +1096,65 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
       }
   __syncthreads();
 
-  float lsum = 0.0f;
+  // Softmax tail, all 16 rows of the wave at once: lane 4 rl + q holds classes
+  // 64 q .. 64 q + 63 of the wave's row rl (register x[4 k + e] is class
+  // 64 q + 4 kk(k) + e, kk(k) = (k + 2 q + 4 (r & 1)) & 15: staggered so the 8
+  // lanes of each LDS read phase, two rows by four quarters, hit distinct banks);
+  // the row's max and sum combine over its four lanes.
   const int V = p.N;
-  const int col = 4 * lane;
-  for (int rr = 0; rr < BM / 4; ++rr) {
-    const int r = wave * (BM / 4) + rr;
-    const int64_t row = static_cast<int64_t>(m0) + r;
-    if (row >= p.M) break;
-    const int64_t lab = labels[row];
-    f4 x = io4<float>::load(tile + r * BN + ((lane ^ (r & 63)) * 4));
-    float m = -INFINITY, picked = 0.0f;
+  const int rl = lane >> 2, q = lane & 3;
+  const int r = wave * (BM / 4) + rl;
+  const int64_t row = static_cast<int64_t>(m0) + r;
+  const int64_t lab = __shfl(my_lab, rl, 64);
+  const int stag = 2 * q + 4 * (r & 1);
+  float x[64];
+  float m = -INFINITY, picked = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = q * 16 + ((k + stag) & 15);  // this lane's chunk k: classes 4c .. 4c + 3
+    const f4 v = io4<float>::load(tile + r * BN + ((c ^ (r & 63)) * 4));
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (col + e >= V) x.v[e] = -INFINITY;
-      m = fmaxf(m, x.v[e]);
-      if (col + e == lab) picked = x.v[e];
-    }
-    m = wave_max(m);
-    picked = wave_sum(picked);
-    float sum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x.v[e] = expf(x.v[e] - m);
-      sum += x.v[e];
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      lsum += logf(sum) + m - picked;
-      if ((lab < 0 || lab >= V) && bad_label) atomicOr(bad_label, 1);
-    }
-    const float inv = 1.0f / sum;
-    if (col < V) {
-      f4 d;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) d.v[e] = (x.v[e] * inv - (col + e == lab ? 1.0f : 0.0f)) * scale;
-      // stochastic rounding of the bf16 gradient (mg_common.h): round-to-nearest errors of
-      // this near-uniform softmax repeat across the rows of a label
-      io4<bf16_t>::store_grad(dlogits + row * ldd + col, d, static_cast<uint32_t>(row * V + col), 0x8d4au);
+      const int cls = 4 * c + e;
+      const float l = cls < V ? v.v[e] : -INFINITY;
+      x[4 * k + e] = l;
+      m = fmaxf(m, l);
+      if (cls == lab) picked = l;
     }
   }
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    x[i] = expf(x[i] - m);
+    sum += x[i];
+  }
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  picked += __shfl_xor(picked, 1, 64);
+  picked += __shfl_xor(picked, 2, 64);
+  const bool live = row < p.M;
+  float lsum = 0.0f;
+  if (live && q == 0) {
+    lsum = logf(sum) + m - picked;
+    if ((lab < 0 || lab >= V) && bad_label) atomicOr(bad_label, 1);
+  }
+  if (live) {
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // chunks 2u, 2u + 1 are classes 8 consecutive from 4 c0 (stag is even)
+      const int c0 = q * 16 + ((2 * u + stag) & 15);
+      if (4 * c0 >= V) continue;
+      fv<8> d;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d.v[e] = (x[8 * u + e] * inv - (4 * c0 + e == lab ? 1.0f : 0.0f)) * scale;
+      // stochastic rounding of the bf16 gradient (mg_common.h): round-to-nearest errors of
+      // this near-uniform softmax repeat across the rows of a label
+      iov<bf16_t, 8>::store_grad(dlogits + row * ldd + 4 * c0, d, static_cast<uint32_t>(row * V + 4 * c0), 0x8d4au);
+    }
+  }
+  lsum = wave_sum(lsum);
   if (lane == 0) s_loss[wave] = lsum;
   __syncthreads();
   if (threadIdx.x == 0) loss_part[blockIdx.x] = s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3];
