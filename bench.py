@@ -322,16 +322,15 @@ def _cpu_name():
     return "unknown CPU"
 
 
-def cpu_baseline(B=2, S=2048, dim=1024, depth=8, max_steps=2, seconds_budget=30.0):
-    """The oracle's fp32 restatement of the reference step at the cfg3 model shape and
-    sequence length on the host's cores: forward and autograd backward of
-    mingru/minLM.py:86-155 (conv and dropout off), then the Schedule-Free AdamW step
-    (oracle.sf_adamw, the package's update; train.py:808). One untimed warm-up step
-    on a [1, 256] batch, then [B, S] steps (at least one, at most `max_steps`, while
-    under `seconds_budget`); the median step time gives tokens/s. The default batch
-    is 2 of cfg3's 8 sequences, which keeps the sample near 10-30 s of CPU work:
-    every op but the optimizer step is linear in the batch, so tokens/s carries over
-    (the full batch-8 step takes ~2 min on 8 cores)."""
+def cpu_baseline(B=8, S=2048, dim=1024, depth=8, max_steps=2, seconds_budget=30.0):
+    """The oracle's fp32 restatement of the reference step at the cfg3 shape on the
+    host's cores: forward and autograd backward of mingru/minLM.py:86-155 (conv and
+    dropout off), then the Schedule-Free AdamW step (oracle.sf_adamw, the package's
+    update; train.py:808). One untimed warm-up step on a [1, 256] batch, then [B, S]
+    steps (at least one, at most `max_steps`, and a second only when the first leaves
+    room under `seconds_budget`); the median step time gives tokens/s. On the GPU
+    box's 16 host cores a cfg3 step takes ~7.5 s (on an 8-core host ~2 min: pass a
+    smaller B there; every op but the optimizer step is linear in the batch)."""
     import torch
 
     from oracle import mingru_oracle as O
@@ -363,8 +362,7 @@ def cpu_baseline(B=2, S=2048, dim=1024, depth=8, max_steps=2, seconds_budget=30.
     med = times[len(times) // 2]
     return {"value": B * (S - 1) / med, "unit": "tokens/s", "cores": cores, "kind": "port",
             "s_per_step": med,
-            "sample": f"cfg3 model and sequence length (d{dim} L{depth} ff4 vocab 256), batch {B} x seq {S} "
-                      f"(cfg3: batch 8): fp32 forward + backward + "
+            "sample": f"cfg3 step (d{dim} L{depth} ff4 vocab 256), batch {B} x seq {S}: fp32 forward + backward + "
                       f"SF-AdamW step of the oracle restatement, median of {len(times)} full steps after a "
                       f"[1, 256] warm-up; torch CPU with {cores} threads on {_cpu_name()}"}
 
