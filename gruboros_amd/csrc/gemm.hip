@@ -1055,6 +1055,87 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Three-stage k-loop of the loss head's product (64 x 256 tile, four waves of
+// 64 x 64): the loads of k-tile t + 2 go out while tile t is multiplied, so
+// two tiles' loads are in flight. With K = 1024 the product has only 16 short
+// k-tiles (16 MFMAs per wave each), shorter than a load's latency, and with
+// two stages every tile waited for the next one's loads. The stages are three
+// distinct __shared__ arrays, run in turns of three so each is static (an LDS
+// read then waits only for the loads into its own stage).
+__device__ __forceinline__ void ce_mainloop3(const Params& p, uint4* s0, uint4* s1, uint4* s2, int m0, int n,
+                                             f32x16 (&acc)[2][2]) {
+  constexpr int BM = kCeRows, BN = 256, MB = 2, NB = 2, T = 256, S = BK / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  Loader<BM, true, T> la;
+  Loader<BN, true, T> lb;
+  constexpr int kLoads = decltype(la)::kPerWave + decltype(lb)::kPerWave;  // load instructions per tile and wave
+  auto issue_to = [&](int t, uint4* st) {  // tiles past n read as zero
+    const KTile kt = ktile(p, t, n);
+    la.load(oa, st, m0, p.M, kt.k0, kt.kmax, kt.aofs);
+    lb.load(ob, st + BM * 8, 0, p.N, kt.k0, kt.kmax, kt.bofs);
+  };
+  int arow[MB], brow[NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) arow[i] = i * 32;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) brow[j] = wave * 64 + j * 32;
+  issue_to(0, s0);
+  issue_to(1, s1);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");  // tile 0 has landed
+  __builtin_amdgcn_s_barrier();
+  bf16x8 af[2][MB], bfr[2][NB];
+  auto tile = [&](int t, const uint4* cur, uint4* fill) __attribute__((always_inline)) {
+    issue_to(t + 2, fill);  // fill held tile t - 1, which every wave finished before the last barrier
+    const uint4* Bs = cur + BM * 8;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, true>(cur, arow[i], 0, lane);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bfr[0][j] = read_frag<BN, true>(Bs, brow[j], 0, lane);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int c = s & 1;
+      if (s + 1 < S) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) af[c ^ 1][i] = read_frag<BM, true>(cur, arow[i], s + 1, lane);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bfr[c ^ 1][j] = read_frag<BN, true>(Bs, brow[j], s + 1, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[c][j], af[c][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Tile t + 1 has landed (t + 2 may still fly). A bare s_barrier, not
+    // __syncthreads(), whose fence would wait for every load in flight: this
+    // wave's loads into t + 1's stage are complete by the vmcnt wait, every
+    // wave's reads of tile t were consumed by its MFMAs, and the barrier
+    // makes both hold for the whole workgroup.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+  int t = 0;
+  for (; t + 2 < n; t += 3) {
+    tile(t, s0, s2);
+    tile(t + 1, s1, s0);
+    tile(t + 2, s2, s1);
+  }
+  if (t < n) tile(t, s0, s2);
+  if (t + 1 < n) tile(t + 1, s1, s0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-reading loads past n
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t* __restrict__ labels,
                                                         bf16_t* __restrict__ dlogits, int64_t ldd,
                                                         float* __restrict__ loss_part, int* __restrict__ bad_label,
@@ -1062,9 +1143,14 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   constexpr int BM = kCeRows, BN = 256, WM = 1, WN = 4;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;
   constexpr int kStage = (BM + BN) * 8;
-  __shared__ uint4 smem[2 * kStage];
+  __shared__ uint4 st0[kStage], st1[kStage], st2[kStage];
   __shared__ float s_loss[4];
-  static_assert(BM * BN * 4 <= int(sizeof(smem)), "logits tile fits");
+  // the fp32 logits tile after the product: rows [0, kRows0) in st0, the rest in st1
+  constexpr int kRows0 = kStage * 16 / (BN * 4);
+  static_assert(BM - kRows0 <= kRows0, "logits tile fits in two stages");
+  auto tile_row = [&](int r) -> float* {
+    return r < kRows0 ? reinterpret_cast<float*>(st0) + r * BN : reinterpret_cast<float*>(st1) + (r - kRows0) * BN;
+  };
 
   const int m0 = blockIdx.x * BM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1077,10 +1163,10 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
     if (lane < BM / 4 && row < p.M) my_lab = labels[row];
   }
   f32x16 acc[MB][NB];
-  mainloop<BM, BN, WM, WN, true, true, false>(p, smem, smem + kStage, m0, 0, 0, (p.K + BK - 1) / BK, acc);
+  static_assert(MB == 2 && NB == 2 && WM == 1 && WN == 4, "ce_mainloop3's tile");
+  ce_mainloop3(p, st0, st1, st2, m0, (p.K + BK - 1) / BK, acc);
 
   // logits tile [64][256] fp32 in LDS, 16-byte chunk c of row r at c ^ (r & 63)
-  float* tile = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1092,7 +1178,7 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
         f4 x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x.v[e] = acc[i][j][4 * g + e];
-        io4<float>::store(tile + r * BN + ((c ^ (r & 63)) * 4), x);
+        io4<float>::store(tile_row(r) + ((c ^ (r & 63)) * 4), x);
       }
   __syncthreads();
 
@@ -1112,7 +1198,7 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const int c = q * 16 + ((k + stag) & 15);  // this lane's chunk k: classes 4c .. 4c + 3
-    const f4 v = io4<float>::load(tile + r * BN + ((c ^ (r & 63)) * 4));
+    const f4 v = io4<float>::load(tile_row(r) + ((c ^ (r & 63)) * 4));
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int cls = 4 * c + e;
