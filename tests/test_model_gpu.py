@@ -345,6 +345,29 @@ def test_cfg3_training_step_matches_fp64_oracle():
     assert worst <= 2e-4 and worst_v <= 1e-6
 
 
+def test_expansion_15_step_at_cfg3_width_matches_fp64_oracle():
+    """The to_out path (reference mingru/minGRU.py:38,41,71: expansion != 1,
+    Linear(Di, D) after the scan) at the cfg3 model width: minLM d1024 L2
+    expansion 1.5 (Di 1536), batch 4 x 2048, bf16 activations. Loss,
+    next_prev_hiddens and every parameter gradient (to_out's included) within
+    2e-2 of the fp64 restatement on the device."""
+    torch.cuda.empty_cache()
+    m, sd = _model(1024, 2, 1.5, torch.bfloat16, seed=3)
+    ids = torch.randint(0, 256, (4, 2048), device=DEV, generator=torch.Generator(device=DEV).manual_seed(3))
+    loss, hid = m(ids, return_loss=True, return_prev_hiddens=True)
+    loss.backward()
+    torch.cuda.synchronize()
+    ref_loss, ref_hid, ref_grad = _oracle_fp64_on_device(sd, ids, 2, expansion=1.5)
+    e_loss = abs(float(loss.detach()) - ref_loss) / abs(ref_loss)
+    e_hid = max(_rel(a, b) for a, b in zip(hid, ref_hid))
+    errs = sorted(((_rel(p.grad, ref_grad[n]), n) for n, p in m.named_parameters()), reverse=True)
+    print(f"expansion 1.5 d1024 vs fp64: loss {e_loss:.2e}, hiddens {e_hid:.2e}, "
+          f"worst grads {[(f'{e:.2e}', n) for e, n in errs[:3]]}", flush=True)
+    assert any("to_out" in n for _, n in errs)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2
+    assert errs[0][0] <= 2e-2, errs[:3]
+
+
 def test_cfg5_micro_steps_and_accumulation():
     """cfg5: minLM d2048 L24 ff4 expansion 1.0 (1.008 B
     parameters), bf16, batch 4 x 4096, gradient accumulation 4
