@@ -174,8 +174,10 @@ class FFBlock(torch.autograd.Function):
             db2 = column_sum(dp)
             dn2 = gemm.linear_dx(dpre, w1b, stochastic=True)           # bf16, stochastically rounded
             dW1 = gemm.linear_dw(dpre, n2)
-        dx1, dout, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, True)
-        return dx1.view(B, T, D), dout.view(B, T, D), dw_norm, dW1, db1, dW2, db2
+        # x2 = x1 + out: both inputs get the same gradient, written once and returned for both
+        # (the consumer, MinGRUBlock.backward, only reads them)
+        dx1, _, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, False)
+        return dx1.view(B, T, D), dx1.view(B, T, D), dw_norm, dW1, db1, dW2, db2
 
 
 class FinalNormCE(torch.autograd.Function):
