@@ -33,6 +33,7 @@ struct Tensor {
   bf16_t* p_bf16;
   int64_t n;
   int64_t chunk_start;  // first chunk index of this tensor
+  int64_t pair_cols;    // > 0: p_bf16 is the hi/lo pair of p viewed as [n / pair_cols, pair_cols]
 };
 
 struct Hyper {
@@ -69,7 +70,20 @@ __global__ __launch_bounds__(kThreads) void sf_adamw_kernel(const Tensor* __rest
       io4<float>::store(t.p + i, y);
       io4<float>::store(t.z + i, z);
       io4<float>::store(t.v + i, v);
-      if (t.p_bf16) io4<bf16_t>::store(t.p_bf16 + i, y);
+      if (t.p_bf16) {
+        if (t.pair_cols > 0) {  // row r = i / C: hi at r * 2C + c, lo at r * 2C + C + c (4 | C)
+          const uint32_t C = static_cast<uint32_t>(t.pair_cols);
+          const int64_t r = static_cast<int64_t>(static_cast<uint32_t>(i) / C);
+          const int64_t c = i - r * C;
+          f4 lo;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lo.v[j] = y.v[j] - bf16_to_f32(f32_to_bf16(y.v[j]));
+          io4<bf16_t>::store(t.p_bf16 + r * 2 * C + c, y);
+          io4<bf16_t>::store(t.p_bf16 + r * 2 * C + C + c, lo);
+        } else {
+          io4<bf16_t>::store(t.p_bf16 + i, y);
+        }
+      }
     } else {
       for (int64_t k = i; k < std::min<int64_t>(i + 4, t.n); ++k) {
         float y = t.p[k], z = t.z[k], v = t.v[k];
@@ -77,7 +91,16 @@ __global__ __launch_bounds__(kThreads) void sf_adamw_kernel(const Tensor* __rest
         t.p[k] = y;
         t.z[k] = z;
         t.v[k] = v;
-        if (t.p_bf16) t.p_bf16[k] = f32_to_bf16(y);
+        if (t.p_bf16) {
+          if (t.pair_cols > 0) {
+            const int64_t r = k / t.pair_cols, c = k - r * t.pair_cols;
+            const bf16_t hi = f32_to_bf16(y);
+            t.p_bf16[r * 2 * t.pair_cols + c] = hi;
+            t.p_bf16[r * 2 * t.pair_cols + t.pair_cols + c] = f32_to_bf16(y - bf16_to_f32(hi));
+          } else {
+            t.p_bf16[k] = f32_to_bf16(y);
+          }
+        }
       }
     }
   }

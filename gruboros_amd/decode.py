@@ -55,9 +55,10 @@ class Decoder:
         m = self.model
         ws = []
         for _, _, gru, _, ff, _ in m.layers:
-            ws += [bf16_copy(gru.to_hidden_and_gate.weight), bf16_copy(ff[0].weight), bf16_copy(ff[0].bias),
-                   bf16_copy(ff[2].weight), bf16_copy(ff[2].bias)]
-        ws.append(bf16_copy(m.to_logits.weight))
+            ws += [bf16_copy(gru.to_hidden_and_gate.weight, dense=True), bf16_copy(ff[0].weight, dense=True),
+                   bf16_copy(ff[0].bias, dense=True), bf16_copy(ff[2].weight, dense=True),
+                   bf16_copy(ff[2].bias, dense=True)]
+        ws.append(bf16_copy(m.to_logits.weight, dense=True))
         return ws
 
     def _launch(self, weights):

@@ -81,8 +81,15 @@ def gelu_backward(dh, pre, want_bias_grad=True):
     return dpre, db
 
 
-def bf16_copy(w):
-    """The bf16 copy of fp32 parameter w, re-made if w changed in place."""
+def bf16_copy(w, dense=False):
+    """The bf16 copy of fp32 parameter w, re-made if w changed in place. Where w has a current
+    hi/lo pair (bf16_pair) and `dense` is false, its hi half (a [rows, cols] view with row
+    stride 2 cols); dense: a contiguous copy (the fused optimizer step keeps the pair current
+    and drops this copy, which is then re-made from w on its next use)."""
+    pair = getattr(w, "_mg_pair", None)
+    if not dense and pair is not None and pair[0] == w._version and pair[1].device == w.device and \
+            pair[1].shape == (w.shape[0], 2 * w.shape[1]):
+        return pair[1][:, :w.shape[1]]
     cache = getattr(w, "_mg_bf16", None)
     if cache is None or cache[0] != w._version or cache[1].device != w.device or cache[1].shape != w.shape:
         cache = (w._version, w.detach().to(torch.bfloat16))
@@ -92,8 +99,9 @@ def bf16_copy(w):
 
 def bf16_pair(w):
     """The hi/lo pair [rows, 2 cols] of fp32 parameter w (gemm.split_hilo), re-made if w
-    changed in place. The fused optimizer step drops it (it rewrites w through a raw
-    pointer, which torch's version counter does not see)."""
+    changed in place. The fused optimizer step rewrites it together with w (it changes w
+    through a raw pointer, which torch's version counter does not see), or drops it where it
+    cannot."""
     cache = getattr(w, "_mg_pair", None)
     if cache is None or cache[0] != w._version or cache[1].device != w.device or \
             cache[1].shape != (w.shape[0], 2 * w.shape[1]):

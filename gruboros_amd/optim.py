@@ -38,9 +38,9 @@ class _TableBuffers:
     a buffer is rewritten only after the copy that last read it has run."""
 
     def __init__(self, rows, device):
-        self.host = [torch.empty((rows, 7), dtype=torch.int64).pin_memory() for _ in range(2)]
+        self.host = [torch.empty((rows, 8), dtype=torch.int64).pin_memory() for _ in range(2)]
         self.done = [None, None]
-        self.dev = torch.empty((rows, 7), dtype=torch.int64, device=device)
+        self.dev = torch.empty((rows, 8), dtype=torch.int64, device=device)
         self.turn = 0
 
     def upload(self, rows, stream):
@@ -129,13 +129,20 @@ class AdamWScheduleFree(torch.optim.Optimizer):
                 g = p.grad if (p.grad.is_contiguous() and p.grad.dtype == torch.float32) else \
                     p.grad.float().contiguous()
                 keep.append(g)  # a converted copy must outlive the enqueue below
-                pb = 0
+                pb, pair_cols = 0, 0
+                pair = getattr(p, "_mg_pair", None)
                 cache = getattr(p, "_mg_bf16", None)
-                if cache is not None and cache[0] == p._version and cache[1].shape == p.shape:
+                if pair is not None and pair[0] == p._version and p.dim() == 2 and p.shape[1] % 4 == 0 \
+                        and p.numel() < (1 << 31) and pair[1].shape == (p.shape[0], 2 * p.shape[1]) \
+                        and pair[1].is_contiguous():
+                    # the kernel keeps the hi/lo pair (and with it the bf16 copy, its hi half) current
+                    pb, pair_cols = pair[1].data_ptr(), p.shape[1]
+                elif cache is not None and cache[0] == p._version and cache[1].shape == p.shape \
+                        and cache[1].is_contiguous():
                     pb = cache[1].data_ptr()
                 n = p.numel()
                 rows.append([p.data_ptr(), g.data_ptr(), st["z"].data_ptr(), st["exp_avg_sq"].data_ptr(), pb, n,
-                             nchunks])
+                             nchunks, pair_cols])
                 nchunks += (n + chunk - 1) // chunk
             if rows:
                 dev = group["params"][0].device
@@ -148,9 +155,11 @@ class AdamWScheduleFree(torch.optim.Optimizer):
                                             group["weight_decay"], ckp1, y_lr, lr,
                                             stream_of(group["params"][0]))
                 check(rc, "mg_sf_adamw_step")
-                for p in group["params"]:
-                    if hasattr(p, "_mg_pair"):  # hi/lo pairs follow the new weights on next use
+                for p, row in zip([q for q in group["params"] if q.grad is not None], rows):
+                    if row[7] == 0 and hasattr(p, "_mg_pair"):  # a pair the kernel did not update is re-made
                         del p._mg_pair
+                    if row[7] != 0 and hasattr(p, "_mg_bf16"):  # and so is a dense copy beside a pair it did
+                        del p._mg_bf16
             del keep
             group["k"] = k + 1
         return loss

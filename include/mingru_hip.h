@@ -238,9 +238,14 @@ typedef struct mg_sf_tensor {
   const float* g;
   float* z;
   float* v;
-  uint16_t* p_bf16; /* nullable */
+  uint16_t* p_bf16; /* nullable: bf16 copy of p, written with it */
   int64_t n;
   int64_t chunk_start;
+  /* 0: p_bf16 is a dense bf16 copy [n]. C > 0 (C % 4 == 0, n % C == 0, n < 2^31): p
+   * viewed as [n / C, C] and p_bf16 its hi/lo pair [n / C, 2 C] (row r:
+   * hi = bf16(p[r, :]) then lo = bf16(p[r, :] - hi), as mg_split_hilo
+   * writes it), the operand form of the fp32-accurate products. */
+  int64_t pair_cols;
 } mg_sf_tensor;
 
 int64_t mg_sf_adamw_chunk_elems(void);

@@ -80,6 +80,40 @@ def test_cross_entropy_flags_bad_labels():
     assert int(bad) == 1
 
 
+def test_sf_step_keeps_the_hi_lo_pair_current():
+    """For a weight with a hi/lo pair (the fp32-accurate products' operand),
+    the fused step writes the pair of the updated weight itself: bit for bit
+    what mg_split_hilo makes from the new fp32 master, its hi half is the bf16
+    copy the other products read, and a dense bf16 copy (the decoder's) is
+    re-made from the new master. Weights without a pair keep their dense copy
+    updated in place."""
+    from gruboros_amd.gemm import split_hilo
+    from gruboros_amd.linear import bf16_copy, bf16_pair
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    g = torch.Generator(device=DEV).manual_seed(11)
+    w = torch.nn.Parameter(torch.randn(256, 128, device=DEV, generator=g) * 0.05)
+    v = torch.nn.Parameter(torch.randn(64, 96, device=DEV, generator=g) * 0.05)
+    opt = AdamWScheduleFree([w, v], lr=1e-2, weight_decay=0.01)
+    opt.train()
+    pair0 = bf16_pair(w)
+    dense0 = bf16_copy(w, dense=True)
+    vb0 = bf16_copy(v)
+    for _ in range(3):
+        w.grad = torch.randn(w.shape, device=DEV, generator=g)
+        v.grad = torch.randn(v.shape, device=DEV, generator=g)
+        opt.step()
+    torch.cuda.synchronize()
+    pair = bf16_pair(w)
+    assert pair is pair0  # the cached pair, rewritten in place by the step
+    assert torch.equal(pair.view(torch.int16), split_hilo(w.detach()).view(torch.int16))
+    assert torch.equal(bf16_copy(w).float(), w.detach().bfloat16().float())
+    dense = bf16_copy(w, dense=True)
+    assert dense is not dense0 and dense.is_contiguous()
+    assert torch.equal(dense, w.detach().bfloat16())
+    assert bf16_copy(v) is vb0 and torch.equal(vb0, v.detach().bfloat16())
+
+
 @pytest.mark.parametrize("form", ["denominator", "lr"])
 @pytest.mark.parametrize("wd", [0.0, 0.01])
 def test_sf_adamw_fused_matches_restatement(wd, form):
