@@ -90,6 +90,26 @@ __device__ __forceinline__ uint32_t pack_bf16x2_sr(float lo, float hi, uint32_t 
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Two pairs that belong together (the scan backward's dgate and dhidden of
+// the same two elements) from ONE hash: the first pair takes the 16-bit
+// windows r[31:16] and r[15:0], the second the windows of r rotated by 8
+// bits (r[7:0]r[31:24] and r[23:8]). Each window is uniform on its own, and
+// the leading byte of every window is a distinct byte of r, so the four
+// roundings are unbiased and nearly independent, at half the hashes.
+// idx: the first pair's index (its lo element) with the call site's salt added.
+__device__ __forceinline__ void pack2_bf16x2_sr(float a0, float a1, float b0, float b1, uint32_t idx,
+                                                uint32_t& pa, uint32_t& pb) {
+  const uint32_t r = sr_hash(idx ^ __float_as_uint(a0));
+  const uint32_t r2 = __builtin_rotateright32(r, 8);
+  bf16x2_t va = __builtin_nondeterministic_value(va), vb = __builtin_nondeterministic_value(vb);
+  va = __builtin_amdgcn_cvt_sr_bf16_f32(va, a0, r, false);
+  va = __builtin_amdgcn_cvt_sr_bf16_f32(va, a1, r << 16, true);
+  vb = __builtin_amdgcn_cvt_sr_bf16_f32(vb, b0, r2, false);
+  vb = __builtin_amdgcn_cvt_sr_bf16_f32(vb, b1, r2 << 16, true);
+  pa = __builtin_bit_cast(uint32_t, va);
+  pb = __builtin_bit_cast(uint32_t, vb);
+}
+
 // N consecutive channels of one row, loaded/stored as one vector access
 // (N = 4: 8-byte bf16 / 16-byte fp32; N = 8: 16-byte bf16 / 2 x 16-byte fp32).
 template <int N>
@@ -131,6 +151,11 @@ template <int N> struct iov<float, N> {
   __device__ __forceinline__ static void store_grad(float* p, const fv<N>& a, uint32_t, uint32_t) { store(p, a); }
   __device__ __forceinline__ static void store_grad_nt(float* p, const fv<N>& a, uint32_t, uint32_t) {
     store_nt(p, a);
+  }
+  __device__ __forceinline__ static void store_grad2_nt(float* pa, const fv<N>& a, float* pb, const fv<N>& b,
+                                                        uint32_t) {
+    store_nt(pa, a);
+    store_nt(pb, b);
   }
 };
 
@@ -184,6 +209,18 @@ template <int N> struct iov<bf16_t, N> {
     for (int q = 0; q < N / 2; ++q)
       __builtin_nontemporal_store(pack_bf16x2_sr(a.v[2 * q], a.v[2 * q + 1], idx + 2 * q, salt),
                                   reinterpret_cast<uint32_t*>(p) + q);
+  }
+  // Two gradients of the same elements, rounded with one hash per element pair
+  // (pack2_bf16x2_sr); idx = index of element 0 plus the call site's salt.
+  __device__ __forceinline__ static void store_grad2_nt(bf16_t* pa, const fv<N>& a, bf16_t* pb, const fv<N>& b,
+                                                        uint32_t idx) {
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) {
+      uint32_t wa, wb;
+      pack2_bf16x2_sr(a.v[2 * q], a.v[2 * q + 1], b.v[2 * q], b.v[2 * q + 1], idx + 2 * q, wa, wb);
+      __builtin_nontemporal_store(wa, reinterpret_cast<uint32_t*>(pa) + q);
+      __builtin_nontemporal_store(wb, reinterpret_cast<uint32_t*>(pb) + q);
+    }
   }
 };
 

@@ -365,17 +365,26 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
 #pragma unroll
     for (int j = 0; j < kVec; ++j) h.v[j] = pa.v[j] * h.v[j] + pv.v[j];
   }
-  Tout* ob = hout + (b * out_sb + static_cast<int64_t>(k) * kFwdTileRows * out_ld + d0);
-  const int out_off = s * kRows * old + cl * kVec;
+  Tout* ob = hout + (b * out_sb + static_cast<int64_t>(k) * kFwdTileRows * out_ld + d0) + (s * kRows * old + cl * kVec);
+  // kFull: every row of the run is inside the sequence (all runs but the
+  // tail's), so the stores need no per-row test.
+  auto outputs = [&](auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
+    for (int i = 0; i < kRows; ++i) {
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) h.v[j] = a[i][j] * h.v[j] + v[i][j];
-    if (t0 + i < g.T) io4<Tout>::store_nt(ob + (out_off + i * old), h);
-    if (h_last && t0 + i == g.T - 1) io4<float>::store(h_last + c, h);
-    if (ckpt && (i + 1) % kCkptRows == 0 && t0 + i < g.T)
-      io4<float>::store(ckpt + static_cast<int64_t>((t0 + i) / kCkptRows) * g.BD + c, h);
-  }
+      for (int j = 0; j < kVec; ++j) h.v[j] = a[i][j] * h.v[j] + v[i][j];
+      if (kFull || t0 + i < g.T) io4<Tout>::store_nt(ob + i * old, h);
+      if (!kFull && h_last && t0 + i == g.T - 1) io4<float>::store(h_last + c, h);
+      if (ckpt && (i + 1) % kCkptRows == 0 && (kFull || t0 + i < g.T))
+        io4<float>::store(ckpt + static_cast<int64_t>((t0 + i) / kCkptRows) * g.BD + c, h);
+    }
+    if (kFull && h_last && t0 + kRows == g.T) io4<float>::store(h_last + c, h);
+  };
+  if (t0 + kRows <= g.T)
+    outputs(std::true_type{});
+  else
+    outputs(std::false_type{});
 }
 
 // ------------------------------------------------------------------ backward
@@ -474,14 +483,6 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     else if (h0)
       hc = io4<float>::load(h0 + c);
   }
-  // gradient arriving at h_last joins dh of the last row
-  f4 dl = io4<float>::fill(0.0f);
-  int il = -1;
-  if (ok && dh_last && t0 <= g.T - 1 && g.T - 1 < t0 + kRows) {
-    dl = io4<float>::load(dh_last + c);
-    il = g.T - 1 - t0;
-  }
-
   float a[kRows][kVec], z[kRows][kVec];
   f4 A, M;
 #pragma unroll
@@ -515,8 +516,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   for (int i = kRows - 1; i >= 0; --i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float dv = dr[i].get(j) + (i == il ? dl.v[j] : 0.0f);
-      M.v[j] = a[i][j] * (dv + M.v[j]);
+      M.v[j] = a[i][j] * (dr[i].get(j) + M.v[j]);
       A.v[j] = A.v[j] * a[i][j];
     }
   }
@@ -529,8 +529,13 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
     const float TA = reinterpret_cast<const float*>(&s_maps.A[buf][0][cl])[q];
     const float TM = reinterpret_cast<const float*>(&s_maps.V[buf][0][cl])[q];
     uint64_t* st = status + static_cast<int64_t>(k) * g.BD + c + q;
+    // The gradient arriving at h_last enters as the carry into the chain's
+    // last tile: every row past T - 1 is an identity step (a = 1, dh = 0), so
+    // it reaches row T - 1 unchanged and joins dh there, as it should.
     float carry = 0.0f;
-    if (k != g.ntiles - 1) {
+    if (k == g.ntiles - 1) {
+      if (dh_last) carry = dh_last[c + q];
+    } else {
       publish_agg(st, TA, TM, parity);
       carry = look_back1(status, g.BD, c + q, k, +1, g.ntiles - 1, parity, max_polls, &hdr->err);
     }
@@ -552,7 +557,7 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   for (int i = kRows - 1; i >= 0; --i) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      lam[i][j] = dr[i].get(j) + (i == il ? dl.v[j] : 0.0f) + mu.v[j];
+      lam[i][j] = dr[i].get(j) + mu.v[j];
       mu.v[j] = a[i][j] * lam[i][j];
     }
   }
@@ -561,32 +566,41 @@ __global__ __launch_bounds__(kChLanes * kBwdSubs) void scan_bwd_kernel(
   const int dld = static_cast<int>(d_ld);
   const int64_t d_tile = b * d_sb + static_cast<int64_t>(k) * kBwdTileRows * d_ld + d0;
   const int d_off = s * kRows * dld + cl * kVec;
-  Tin* dhb = dhidden + d_tile;
-  Tin* dgb = dgate + d_tile;
+  Tin* dhb = dhidden + d_tile + d_off;
+  Tin* dgb = dgate + d_tile + d_off;
+  // bf16 gradients round stochastically (mg_common.h), keyed by the element's
+  // (b, t, d) index (mod 2^32) plus a salt for this call site
+  const uint32_t idx0 = (static_cast<uint32_t>(b) * static_cast<uint32_t>(g.T) + static_cast<uint32_t>(t0)) *
+                            static_cast<uint32_t>(g.Di) + static_cast<uint32_t>(d) + 0x5a17u;
+  // kFull: every row of the run is inside the sequence (all runs but the
+  // tail's), so the stores need no per-row test.
+  auto outputs = [&](auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    f4 og, oh;
+    for (int i = 0; i < kRows; ++i) {
+      f4 og, oh;
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      // g~ = g(hidden), gp = g'(hidden) (0 at hidden = 0, as autograd of relu gives)
-      const float x = hr[i].get(j);
-      const float e2 = exp2_raw(fabsf(x) * -kLog2e);
-      const float r2 = __builtin_amdgcn_rcpf(1.0f + e2);
-      const float sig = e2 * r2;  // sigmoid(x) for x < 0
-      const float gt = x >= 0.0f ? x + 0.5f : sig;
-      const float gp = x > 0.0f ? 1.0f : (x < 0.0f ? sig * r2 : 0.0f);
-      const float vv = z[i][j] * gt;
-      og.v[j] = lam[i][j] * (a[i][j] * (vv - z[i][j] * hc.v[j]));
-      oh.v[j] = lam[i][j] * (z[i][j] * gp);
-      hc.v[j] = a[i][j] * hc.v[j] + vv;
+      for (int j = 0; j < kVec; ++j) {
+        // g~ = g(hidden), gp = g'(hidden) (0 at hidden = 0, as autograd of relu gives)
+        const float x = hr[i].get(j);
+        const float e2 = exp2_raw(fabsf(x) * -kLog2e);
+        const float r2 = __builtin_amdgcn_rcpf(1.0f + e2);
+        const float sig = e2 * r2;  // sigmoid(x) for x < 0
+        const float gt = x >= 0.0f ? x + 0.5f : sig;
+        const float gp = x > 0.0f ? 1.0f : (x < 0.0f ? sig * r2 : 0.0f);
+        const float vv = z[i][j] * gt;
+        og.v[j] = lam[i][j] * (a[i][j] * (vv - z[i][j] * hc.v[j]));
+        oh.v[j] = lam[i][j] * (z[i][j] * gp);
+        hc.v[j] = a[i][j] * hc.v[j] + vv;
+      }
+      if (kFull || t0 + i < g.T)
+        io4<Tin>::store_grad2_nt(dgb + i * dld, og, dhb + i * dld, oh, idx0 + static_cast<uint32_t>(i * g.Di));
     }
-    if (t0 + i < g.T) {
-      // bf16 gradients round stochastically (mg_common.h), keyed by the element's (b, t, d) index
-      const uint32_t idx = static_cast<uint32_t>((static_cast<int64_t>(b) * g.T + t0 + i) * g.Di + d);
-      io4<Tin>::store_grad_nt(dgb + (d_off + i * dld), og, idx, 0x5a17u);
-      io4<Tin>::store_grad_nt(dhb + (d_off + i * dld), oh, idx, 0x6b28u);
-    }
-  }
+  };
+  if (t0 + kRows <= g.T)
+    outputs(std::true_type{});
+  else
+    outputs(std::false_type{});
 }
 
 // ------------------------------------------------------------------ host
