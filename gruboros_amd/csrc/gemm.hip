@@ -1033,6 +1033,263 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   }
 }
 
+// ---------------------------------------------------------------- persistent products
+//
+// Products with more 256 x 256 tiles than CUs and a bf16 output run one
+// workgroup per CU that walks its tiles (pid = blockIdx.x, + gridDim.x, ...).
+// A workgroup per tile ends each tile exposed: the epilogue, the workgroup's
+// exit and the next workgroup's first k-tile load all run with the matrix
+// cores idle (measured: the 1024-tile FeedForward product runs its MFMAs 53%
+// of the time against 68% for the 256-tile product of equal flops). Here the
+// last k-tile of a tile prefetches the next tile's first k-tile into the
+// other stage as the k-loop prefetches any k-tile, the epilogue stages its
+// bf16 rows in the stage the last k-tile was read from, and its global stores
+// drain while the next tile multiplies.
+// The main loop is mainloop_w8's (eight waves, 64 x 128 each, waves 0-3 load),
+// with the operand offsets taken relative to the tile origin (a scalar per
+// tile). It needs an even k-tile count, so that every tile starts from stage
+// `sa` and ends in `sb`.
+// Epilogue math (bias, GELU, stochastic rounding) is done in registers on the
+// lane's own 4 consecutive columns of a row, so the staging is bf16: 8 KB per
+// wave, one stage for all eight waves.
+template <bool AK, bool BKM, int EPI>
+__global__ __launch_bounds__(512) void gemm_persist_kernel(Params p) {
+  constexpr int S = BK / 16;
+  constexpr int kLoaders = 4;
+  constexpr int NL = kW4Loads * 4 / kLoaders;
+  constexpr int kStageA = kW4Rows * 8;  // uint4 of the A tile (B follows)
+  constexpr int kStage = 2 * kStageA;
+  __shared__ uint4 sa[kStage];
+  __shared__ uint4 sb[kStage];
+  // the bias of a tile's 256 columns, double-buffered by tile parity: wave 0
+  // loads the next tile's into LDS during the current epilogue, and its wait
+  // for the next k-tile's loads covers that load too
+  constexpr bool kBias = EPI == EPI_BIAS || EPI == EPI_BIAS_GELU;
+  __shared__ float4 s_bias[kBias ? 2 : 1][64];
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int n = total_ktiles(p);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const Operand oa = make_operand(p.A, p.lda, p.a_span);
+  const Operand ob = make_operand(p.B, p.ldb, p.b_span);
+  W4Operand<AK> A;
+  W4Operand<BKM> B;
+  A.template init<NL>(oa, 0, wm * 64, wave % kLoaders, lane);
+  B.template init<NL>(ob, 0, wn * 128, wave % kLoaders, lane);
+  // byte shift of tile pid's operand blocks against the tile at the origin
+  auto origin = [&](int pid, int& m0, int& n0, uint32_t& ash, uint32_t& bsh) {
+    int tm, tn;
+    tile_of(pid, p.tiles_m, p.tiles_n, tm, tn);
+    m0 = tm * 256;
+    n0 = tn * 256;
+    ash = AK ? static_cast<uint32_t>(m0) * oa.ld2 : static_cast<uint32_t>(m0) * 2u;
+    bsh = BKM ? static_cast<uint32_t>(n0) * ob.ld2 : static_cast<uint32_t>(n0) * 2u;
+  };
+  // offsets of k-tile t of a tile with shifts (ash, bsh)
+  auto koffs = [&](int t, uint32_t ash, uint32_t bsh, uint32_t& ao, uint32_t& bo) {
+    int seg = 0, k0 = t * BK;
+    if (p.hilo) {
+      seg = t / p.nkt_seg;
+      k0 = (t - seg * p.nkt_seg) * BK;
+    }
+    ao = A.koff(k0, seg == 1 ? p.K : 0, oa.ld2) + ash;
+    bo = B.koff(k0, seg == 2 ? p.K : 0, ob.ld2) + bsh;
+  };
+  bf16x8 af[2][2], bfr[2][4];
+  auto read_step = [&](const uint4* st, int s, int buf) {
+    af[buf][0] = A.frag(st, s, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[buf][j] = B.frag(st + kStageA, s, j);
+    af[buf][1] = A.frag(st, s, 1);
+  };
+  f32x16 acc[2][4];
+  auto mfma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NR = 2 * W4Operand<AK>::kReadsPerBlock + 4 * W4Operand<BKM>::kReadsPerBlock;
+
+  int pid = blockIdx.x;
+  int m0, n0;
+  uint32_t ash, bsh;
+  origin(pid, m0, n0, ash, bsh);
+  __amdgpu_buffer_rsrc_t bias_rsrc;
+  if constexpr (kBias)
+    bias_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.bias), static_cast<short>(0), p.N * 4, 0x00020000);
+  auto load_bias = [&](int par, int col0) {  // wave 0; columns past N read as zero
+    if constexpr (kBias)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bias_rsrc, (__attribute__((address_space(3))) void*)(&s_bias[par][0]), 16,
+                                               static_cast<uint32_t>(col0 + 4 * lane) * 4u, 0, 0, 0);
+  };
+  if (wave == 0) load_bias(0, n0);
+  if (wave < kLoaders) {  // the first tile's first k-tile
+    uint32_t ao, bo;
+    koffs(0, ash, bsh, ao, bo);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) A.template load<NL>(sa, wave, i, ao);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) B.template load<NL>(sa + kStageA, wave, i, bo);
+  }
+  for (int it = 0;; ++it) {
+    const bool first = it == 0;
+    const int next = pid + static_cast<int>(gridDim.x);
+    const bool has_next = next < ntiles;
+    int m1 = 0, n1 = 0;
+    uint32_t ash1 = 0, bsh1 = 0;
+    if (has_next) origin(next, m1, n1, ash1, bsh1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    // The loop once per role (loading waves 0-3, the others), as in mainloop_w8.
+    auto run = [&](auto role) __attribute__((always_inline)) {
+      constexpr bool kLoad = decltype(role)::value;
+      // The first tile waits for its first k-tile here; a later tile's first
+      // k-tile was waited for at the previous tile's last k-step (waiting
+      // again would also wait for the epilogue's stores).
+      if (kLoad && first) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // this tile's first k-tile is in sa; the previous epilogue is done with sb
+      read_step(sa, 0, 0);
+      auto tile = [&](int t, const uint4* cur, uint4* nxt) __attribute__((always_inline)) {
+        // prefetch k-tile t + 1 of this tile, else the next tile's first
+        // k-tile, else (the last tile) a reload of this k-tile; the loads stay
+        // unconditional so that they share one scheduled block with the MFMAs
+        uint32_t ao = 0, bo = 0;
+        if constexpr (kLoad) {
+          if (t + 1 < n) koffs(t + 1, ash, bsh, ao, bo);
+          else if (has_next) koffs(0, ash1, bsh1, ao, bo);
+          else koffs(t, ash, bsh, ao, bo);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int c = s & 1;
+          if constexpr (kLoad) {
+            if (s == 0) {
+#pragma unroll
+              for (int i = 0; i < NL; ++i) A.template load<NL>(nxt, wave, i, ao);
+            } else if (s == 1) {
+#pragma unroll
+              for (int i = 0; i < NL; ++i) B.template load<NL>(nxt + kStageA, wave, i, bo);
+            }
+          }
+          if (s + 1 < S) {
+            read_step(cur, s + 1, c ^ 1);
+          } else {
+            // only the loading waves have loads to wait for (the others' epilogue
+            // stores of the previous tile are left to drain)
+            if constexpr (kLoad) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // k-tile t + 1 is in `nxt` for every wave; every wave is done with `cur`
+            read_step(nxt, 0, c ^ 1);
+          }
+          mfma_step(c);
+          if (kLoad && s < 2) interleave<8, NR, NL>();
+          else interleave<8, NR, 0>();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      for (int t = 0; t < n; t += 2) {
+        tile(t, sa, sb);
+        tile(t + 1, sb, sa);
+      }
+    };
+    if (wave < kLoaders) run(std::true_type{});
+    else run(std::false_type{});
+
+    // Epilogue: every wave has passed the last k-tile's barrier, so sb (the
+    // last k-tile's stage) is free; sa holds the next tile's first k-tile.
+    // Rows row0 + 32 i + L, columns col0 + 32 j + 8 g + 4 half + e of the
+    // lane's accumulators go as bf16 into a per-wave 32 x 128 staging block;
+    // the non-loading waves 4-7 read back the blocks of waves w and w + 4 as
+    // 16-byte row chunks and store them. The loading waves issue no stores,
+    // so their wait for the next k-tile's loads does not wait for the stores
+    // (one vector-memory counter per wave counts both, in issue order): the
+    // output of all CUs, written at the same moment, drains while the next
+    // tile multiplies.
+    if (wave == 0 && has_next) load_bias((it + 1) & 1, n1);
+    {
+      constexpr int RB = 256, CQ = RB / 16, RPI = 64 / CQ;
+      unsigned char* stg = reinterpret_cast<unsigned char*>(sb) + wave * (32 * RB);
+      const int L = lane & 31, half = lane >> 5;
+      const int row0 = m0 + wm * 64, col0 = n0 + wn * 128;
+      const int qc = lane % CQ;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int c = j * 32 + 8 * g + 4 * half;
+            const int col = col0 + c;
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = acc[i][j][4 * g + e];
+            if constexpr (kBias) {
+              const float4 bq = s_bias[it & 1][(col - n0) / 4];
+              x[0] += bq.x; x[1] += bq.y; x[2] += bq.z; x[3] += bq.w;
+            }
+            uint2 w;
+            if constexpr (EPI == EPI_SR) {
+              const uint32_t idx = static_cast<uint32_t>(static_cast<int64_t>(row0 + i * 32 + L) * p.N + col);
+              w.x = pack_bf16x2_sr(x[0], x[1], idx, 0x9e5bu);
+              w.y = pack_bf16x2_sr(x[2], x[3], idx + 2, 0x9e5bu);
+            } else {
+              w.x = pack_bf16x2(x[0], x[1]);
+              w.y = pack_bf16x2(x[2], x[3]);
+            }
+            const int q = c / 8;
+            *reinterpret_cast<uint2*>(stg + L * RB + ((q ^ (L % CQ)) * 16) + 8 * half) = w;
+          }
+        }
+        __syncthreads();
+        if (wave >= kLoaders) {
+          // BIAS_GELU: the staged values are the pre-activation (aux); C =
+          // gelu of them, computed here (a runtime loop: unrolled, the GELU
+          // is more code than the instruction cache holds)
+#pragma unroll 1
+          for (int h = 0; h < 2; ++h) {
+            const int src = wave - kLoaders + kLoaders * h;  // waves w, w + 4
+            const unsigned char* sst = reinterpret_cast<const unsigned char*>(sb) + src * (32 * RB);
+            const int srow = m0 + (src >> 1) * 64 + i * 32, scol = n0 + (src & 1) * 128 + qc * 8;
+            constexpr int kUnroll = EPI == EPI_BIAS_GELU ? 1 : 32 / RPI;
+#pragma unroll kUnroll
+            for (int t = 0; t < 32 / RPI; ++t) {
+              const int r = t * RPI + lane / CQ;
+              const int m = srow + r;
+              const uint4 raw = *reinterpret_cast<const uint4*>(sst + r * RB + ((qc ^ (r % CQ)) * 16));
+              if (m < p.M && scol < p.N) {
+                if constexpr (EPI == EPI_BIAS_GELU) {
+                  *reinterpret_cast<uint4*>(p.aux + static_cast<int64_t>(m) * p.ldaux + scol) = raw;
+                  const uint32_t wi[4] = {raw.x, raw.y, raw.z, raw.w};
+                  uint32_t wo[4];
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    wo[e] = pack_bf16x2(gelu(__uint_as_float(wi[e] << 16)), gelu(__uint_as_float(wi[e] & 0xffff0000u)));
+                  *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + scol) =
+                      make_uint4(wo[0], wo[1], wo[2], wo[3]);
+                } else {
+                  *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + scol) = raw;
+                }
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (!has_next) break;
+    pid = next;
+    m0 = m1;
+    n0 = n1;
+    ash = ash1;
+    bsh = bsh1;
+  }
+}
+
 // ---------------------------------------------------------------- loss head
 //
 // Streaming cross-entropy head: logits = E W^T for 64 rows at a time with
@@ -1321,6 +1578,41 @@ int launch(const Params& p0, const Plan& pl, hipStream_t stream) {
   return check_launch("mg_gemm");
 }
 
+// The persistent kernel (gemm_persist_kernel): one workgroup per CU.
+template <bool AK, bool BKM, int EPI>
+int launch_persist(const Params& p0, hipStream_t stream) {
+  Params p = p0;
+  p.tiles_m = (p.M + 255) / 256;
+  p.tiles_n = (p.N + 255) / 256;
+  p.kt_per_split = total_ktiles(p);
+  const int grid = std::min(p.tiles_m * p.tiles_n, kCUs);
+  hipLaunchKernelGGL((gemm_persist_kernel<AK, BKM, EPI>), dim3(grid), dim3(512), 0, stream, p);
+  return check_launch("mg_gemm");
+}
+
+// Whether a product that meets the eight-wave loop's conditions runs
+// persistent: a bf16 output written whole (no split, no accumulation), an
+// epilogue done in registers, an even k-tile count, and more tiles than CUs.
+// MG_GEMM_PERSIST=0 in the environment turns the persistent kernel off (read
+// per call, so tests can compare both kernels in one process).
+inline bool persist_ok(const Params& p, const Plan& pl, int epi, int c_dtype) {
+  const char* e = getenv("MG_GEMM_PERSIST");
+  const int mode = e ? atoi(e) : 1;
+  if (!mode || c_dtype != MG_BF16 || pl.ysplits > 1 || p.accumulate) return false;
+  if (epi != EPI_NONE && epi != EPI_BIAS && epi != EPI_BIAS_GELU && epi != EPI_SR) return false;
+  if (total_ktiles(p) % 2) return false;
+  const int64_t tiles = int64_t((p.M + 255) / 256) * ((p.N + 255) / 256);
+  return tiles > kCUs || mode == 2;
+}
+
+template <bool AK, bool BKM>
+int dispatch_persist(const Params& p, int epi, hipStream_t s) {
+  if (epi == EPI_NONE) return launch_persist<AK, BKM, EPI_NONE>(p, s);
+  if (epi == EPI_BIAS) return launch_persist<AK, BKM, EPI_BIAS>(p, s);
+  if (epi == EPI_BIAS_GELU) return launch_persist<AK, BKM, EPI_BIAS_GELU>(p, s);
+  return launch_persist<AK, BKM, EPI_SR>(p, s);
+}
+
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
 int dispatch_epi(const Params& p, const Plan& pl, int epi, int c_dtype, hipStream_t s) {
   if (c_dtype == MG_F32) {
@@ -1358,6 +1650,12 @@ int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, 
   if constexpr (BM == 256 && BN == 256) {
 #ifndef MG_GEMM_NO_W8
     if (w4_ok(p, ak, bk) && epi != EPI_GELU_GRAD) {
+      if (persist_ok(p, pl, epi, c_dtype)) {
+        if (ak && bk) return dispatch_persist<true, true>(p, epi, s);
+        if (ak && !bk) return dispatch_persist<true, false>(p, epi, s);
+        if (!ak && !bk) return dispatch_persist<false, false>(p, epi, s);
+        return dispatch_persist<false, true>(p, epi, s);
+      }
       if (ak && bk) return dispatch_epi<256, 256, 4, 2, true, true>(p, pl, epi, c_dtype, s);
       if (ak && !bk) return dispatch_epi<256, 256, 4, 2, true, false>(p, pl, epi, c_dtype, s);
       if (!ak && !bk) return dispatch_epi<256, 256, 4, 2, false, false>(p, pl, epi, c_dtype, s);

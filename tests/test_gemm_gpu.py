@@ -383,3 +383,56 @@ def test_products_over_2gib_run_in_row_blocks():
         ref += (dy[r0:r0 + (1 << 18)].float().t() @ x[r0:r0 + (1 << 18)].float()).double()
     err = (dw.double() - ref).abs().max() / ref.abs().max()
     assert float(err) < 1e-4, float(err)
+
+
+@pytest.mark.parametrize("al,bl,M,N,K,hilo", [
+    (0, 0, 4133, 4104, 256, False),    # ragged M and N, 17 x 17 tiles: some workgroups take two
+    (0, 1, 16376, 4096, 1024, False),  # the input gradient into the FeedForward (4 tiles per workgroup)
+    (1, 0, 4352, 4096, 512, False),    # MN-contiguous A
+    (1, 1, 4352, 4096, 128, False),    # both MN-contiguous
+    (0, 0, 4133, 2048, 1024, True),    # hi/lo operands (three K segments)
+])
+def test_gemm_persistent_matches_per_tile_kernel(al, bl, M, N, K, hilo, monkeypatch):
+    """Products with more 256 x 256 tiles than CUs and a bf16 output run the
+    persistent kernel (one workgroup per CU walking its tiles, the next tile's
+    first k-tile prefetched under the last k-tile, the epilogue in registers).
+    Every epilogue must equal the per-tile kernel's result bit for bit (same
+    sums in the same order, same rounding), and the plain product must match
+    the fp64 product of the same operands."""
+    from gruboros_amd.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_NONE, gemm
+
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + 3 * al + 5 * bl)
+    kk = 2 * K if hilo else K
+    a, ad = _dev_operand(M, kk, al, g)
+    b, bd = _dev_operand(N, kk, bl, g, scale=0.05)
+    bias = torch.randn(N, device=DEV, generator=g)
+    cases = [dict(epilogue=EPI_NONE), dict(stochastic=True)]
+    if not hilo:
+        cases += [dict(epilogue=EPI_BIAS), dict(epilogue=EPI_BIAS_GELU)]
+    for kw in cases:
+        outs = []
+        for mode in ("1", "0"):
+            monkeypatch.setenv("MG_GEMM_PERSIST", mode)
+            y_full = torch.full((M, N + 8), 3.0, device=DEV, dtype=torch.bfloat16)
+            pre_full = torch.full((M, N + 8), 3.0, device=DEV, dtype=torch.bfloat16)
+            y, pre = y_full[:, :N], pre_full[:, :N]
+            extra = {}
+            if kw.get("epilogue") in (EPI_BIAS, EPI_BIAS_GELU):
+                extra["bias"] = bias
+            if kw.get("epilogue") == EPI_BIAS_GELU:
+                extra["aux"] = pre
+            gemm(ad, al, bd, bl, M, N, K, y, hilo=hilo, **kw, **extra)
+            torch.cuda.synchronize()
+            outs.append((y_full, pre_full))
+        print(f"persistent {al}{bl} {M}x{N}x{K} hilo={hilo} {kw}", flush=True)
+        assert torch.equal(outs[0][0], outs[1][0]), f"output differs from the per-tile kernel ({kw})"
+        assert torch.equal(outs[0][1], outs[1][1]), f"aux differs from the per-tile kernel ({kw})"
+        if kw == dict(epilogue=EPI_NONE):
+            if hilo:  # A_hi B_hi + A_lo B_hi + A_hi B_lo (the lo x lo term is left out by design)
+                ah, al_, bh, bl_ = a[:, :K].double(), a[:, K:].double(), b[:, :K].double(), b[:, K:].double()
+                ref = ah @ bh.t() + al_ @ bh.t() + ah @ bl_.t()
+            else:
+                ref = a.double() @ b.double().t()
+            got = outs[0][0][:, :N].double()
+            assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
+            assert bool((outs[0][0][:, N:] == 3.0).all()), "padding columns written"
