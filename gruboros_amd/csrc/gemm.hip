@@ -75,8 +75,9 @@ struct Params {
   int64_t lda, ldb, ldc, ldaux;
   int M, N, K;
   int tiles_m, tiles_n;
-  int kt_per_split;  // k-tiles per split (gridDim.y splits)
-  float* part;       // split partials: gridDim.y dense [M, N] fp32 slices
+  int kt_per_split;  // k-tiles per split
+  float* part;       // split partials: one dense [M, N] fp32 slice per split
+  int xcd_splits;    // > 0: a 1-D grid of tiles x xcd_splits workgroups, laid out by split_tile_of
   int accumulate;    // C += (fp32 outputs)
   uint32_t a_span, b_span;  // bytes from A / B to one past their last element
   uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
@@ -238,6 +239,28 @@ __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int nt = tiles_m * tiles_n;
   if ((nt & 7) == 0) pid = (pid & 7) * (nt >> 3) + (pid >> 3);
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int group = pid / per_group;
+  const int first = group * GM;
+  const int gsize = min(tiles_m - first, GM);
+  const int in_group = pid - group * per_group;
+  tm = first + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Tile and split of a workgroup of a K-split product launched as a 1-D grid
+// of T tiles x S splits. Workgroups go round robin over the 8 XCDs (each with
+// its own L2), so workgroup L runs on XCD L % 8. The linear order here puts
+// consecutive (split, tile) pairs on one XCD: the workgroups of an XCD share
+// one split's K range (and so its operand k-slices, in L2), instead of the
+// same few tiles over every split. Within a split, tiles go in groups of 8
+// tile rows (as tile_of). Needs T * S % 8 == 0.
+__device__ __forceinline__ void split_tile_of(int L, int tiles_m, int tiles_n, int S, int& tm, int& tn, int& split) {
+  const int T = tiles_m * tiles_n;
+  const int g = (L & 7) * (T * S >> 3) + (L >> 3);
+  split = g / T;
+  const int pid = g - split * T;
   constexpr int GM = 8;
   const int per_group = GM * tiles_n;
   const int group = pid / per_group;
@@ -896,11 +919,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
   __shared__ uint4 smem_b[kSplit ? kStage : 1];
   uint4* const stage1 = kSplit ? smem_b : smem + kStage;
 
-  int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  int tm, tn, split;
+  if (p.xcd_splits > 0) {
+    split_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.xcd_splits, tm, tn, split);
+  } else {
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    split = blockIdx.y;
+  }
   const int m0 = tm * BM, n0 = tn * BN;
   const int nkt = total_ktiles(p);
-  const int kt0 = blockIdx.y * p.kt_per_split;
+  const int kt0 = split * p.kt_per_split;
   const int kt1 = min(nkt, kt0 + p.kt_per_split);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -993,7 +1021,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
         const uint4 raw = *reinterpret_cast<const uint4*>(stage + r * RB + ((qc ^ (r % CQ)) * 16));
         if (m >= p.M || n >= p.N) continue;
         TC* cp = CMODE == C_SPLIT
-                     ? reinterpret_cast<TC*>(p.part + (static_cast<int64_t>(blockIdx.y) * p.M + m) * p.N + n)
+                     ? reinterpret_cast<TC*>(p.part + (static_cast<int64_t>(split) * p.M + m) * p.N + n)
                      : static_cast<TC*>(p.C) + static_cast<int64_t>(m) * p.ldc + n;
         if constexpr (sizeof(S) == 4) {
           f4 x;
@@ -1573,8 +1601,19 @@ int launch(const Params& p0, const Plan& pl, hipStream_t stream) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
   p.kt_per_split = pl.kt_per_split;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, CMODE>), dim3(p.tiles_m * p.tiles_n, pl.ysplits),
-                     dim3(64 * WM * WN), 0, stream, p);
+  const int tiles = p.tiles_m * p.tiles_n;
+  // K-split products run as a 1-D grid laid out by split_tile_of when it can
+  // (MG_GEMM_XCD_SPLIT=0 in the environment turns that off)
+  const char* e = getenv("MG_GEMM_XCD_SPLIT");
+  if (CMODE == C_SPLIT && (tiles * pl.ysplits) % 8 == 0 && !(e && atoi(e) == 0)) {
+    p.xcd_splits = pl.ysplits;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, CMODE>), dim3(tiles * pl.ysplits), dim3(64 * WM * WN),
+                       0, stream, p);
+  } else {
+    p.xcd_splits = 0;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BKM, EPI, TC, CMODE>), dim3(tiles, pl.ysplits),
+                       dim3(64 * WM * WN), 0, stream, p);
+  }
   return check_launch("mg_gemm");
 }
 

@@ -436,3 +436,30 @@ def test_gemm_persistent_matches_per_tile_kernel(al, bl, M, N, K, hilo, monkeypa
             got = outs[0][0][:, :N].double()
             assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + 1e-5 * ref.abs().max()).all())
             assert bool((outs[0][0][:, N:] == 3.0).all()), "padding columns written"
+
+
+@pytest.mark.parametrize("al,bl,M,N,K", [
+    (1, 1, 2048, 1024, 16376),   # to_hidden_and_gate weight gradient: 32 tiles x 8 splits
+    (1, 1, 4096, 1024, 16376),   # FeedForward weight gradients: 64 tiles x 4 splits
+    (1, 1, 256, 1024, 16376),    # logits weight gradient: 4 tiles, many splits
+    (0, 0, 512, 520, 4000),      # K-contiguous split product (ragged N)
+])
+def test_gemm_split_layout_matches(al, bl, M, N, K, monkeypatch):
+    """K-split fp32 products run as a 1-D grid whose workgroups on one XCD
+    share a split (split_tile_of). The partials and their in-order reduction
+    are the same as with the 2-D (tile, split) grid, so the results must be
+    equal bit for bit; and within 1e-5 of the fp64 product."""
+    from gruboros_amd.gemm import gemm
+
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + al)
+    a, ad = _dev_operand(M, K, al, g)
+    b, bd = _dev_operand(N, K, bl, g)
+    outs = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MG_GEMM_XCD_SPLIT", mode)
+        out = torch.empty(M, N, device=DEV)
+        gemm(ad, al, bd, bl, M, N, K, out)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    assert _rel(outs[0], a.double() @ b.double().t()) < 1e-5
