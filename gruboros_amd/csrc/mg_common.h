@@ -67,14 +67,16 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 // operand below the bf16 mantissa and truncates, i.e. for finite x
 // bf16(x) = (bits(x) + (r >> 16)) >> 16, and keeps Inf and NaN (checked
 // against that rule on the device for 2^20 random operands).
-// The hash is Knuth's multiplicative (Fibonacci) hash, x * 2^32/phi, with
-// one xorshift folding its high bits into the low half that the pair's second
-// element uses: consecutive indices give equidistributed (low-discrepancy)
-// thresholds along a row and down a column. One multiply per pair instead of
-// the two of a full avalanche finaliser: in the scan backward, the rounding of
-// dgate/dhidden cost 53 us of 650 at cfg2 with the finaliser, 35 with this.
+// The hash is Knuth's multiplicative (Fibonacci) hash on 24 bits, x * 2^24/phi
+// (the low 24 bits of x; bits 16-31 of the 48-bit product go to the first
+// element), with one xorshift folding those high bits into the low half that
+// the pair's second element uses: consecutive indices give equidistributed
+// (low-discrepancy) thresholds along a row and down a column. The 24-bit
+// multiply is a full-rate instruction (v_mul_u32_u24; a 32-bit multiply runs
+// at a quarter of the rate), which matters where the rounding sits in an
+// HBM-bound loop (the scan backward: two gradients per element).
 __device__ __forceinline__ uint32_t sr_hash(uint32_t x) {
-  x *= 0x9e3779b1u;
+  x = __umul24(x, 0x9e3779u);
   return x ^ (x >> 15);
 }
 
