@@ -1340,15 +1340,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Three-stage k-loop of the loss head's product (64 x 256 tile, four waves of
-// 64 x 64): the loads of k-tile t + 2 go out while tile t is multiplied, so
-// two tiles' loads are in flight. With K = 1024 the product has only 16 short
-// k-tiles (16 MFMAs per wave each), shorter than a load's latency, and with
-// two stages every tile waited for the next one's loads. The stages are three
-// distinct __shared__ arrays, run in turns of three so each is static (an LDS
-// read then waits only for the loads into its own stage).
-__device__ __forceinline__ void ce_mainloop3(const Params& p, uint4* s0, uint4* s1, uint4* s2, int m0, int n,
-                                             f32x16 (&acc)[2][2]) {
+// Four-stage k-loop of the loss head's product (64 x 256 tile, four waves of
+// 64 x 64): the loads of k-tile t + 3 go out while tile t is multiplied, so
+// three tiles' loads (120 KB) are in flight. With K = 1024 the product has
+// only 16 short k-tiles (16 MFMAs per wave each), and every workgroup reads
+// all of W from L2 (512 KB per 64 rows): the product is bound by how many
+// bytes each CU keeps in flight against the L2 latency, so the four stages
+// fill the whole 160 KB of LDS. The stages are four distinct __shared__
+// arrays, run in turns of four so each is static (an LDS read then waits only
+// for the loads into its own stage).
+__device__ __forceinline__ void ce_mainloop4(const Params& p, uint4* s0, uint4* s1, uint4* s2, uint4* s3, int m0,
+                                             int n, f32x16 (&acc)[2][2]) {
   constexpr int BM = kCeRows, BN = 256, MB = 2, NB = 2, T = 256, S = BK / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -1374,11 +1376,12 @@ __device__ __forceinline__ void ce_mainloop3(const Params& p, uint4* s0, uint4* 
   for (int j = 0; j < NB; ++j) brow[j] = wave * 64 + j * 32;
   issue_to(0, s0);
   issue_to(1, s1);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");  // tile 0 has landed
+  issue_to(2, s2);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kLoads) : "memory");  // tile 0 has landed
   __builtin_amdgcn_s_barrier();
   bf16x8 af[2][MB], bfr[2][NB];
   auto tile = [&](int t, const uint4* cur, uint4* fill) __attribute__((always_inline)) {
-    issue_to(t + 2, fill);  // fill held tile t - 1, which every wave finished before the last barrier
+    issue_to(t + 3, fill);  // fill held tile t - 1, which every wave finished before the last barrier
     const uint4* Bs = cur + BM * 8;
 #pragma unroll
     for (int i = 0; i < MB; ++i) af[0][i] = read_frag<BM, true>(cur, arow[i], 0, lane);
@@ -1401,22 +1404,24 @@ __device__ __forceinline__ void ce_mainloop3(const Params& p, uint4* s0, uint4* 
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[c][j], af[c][i], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Tile t + 1 has landed (t + 2 may still fly). A bare s_barrier, not
-    // __syncthreads(), whose fence would wait for every load in flight: this
-    // wave's loads into t + 1's stage are complete by the vmcnt wait, every
-    // wave's reads of tile t were consumed by its MFMAs, and the barrier
-    // makes both hold for the whole workgroup.
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+    // Tile t + 1 has landed (t + 2 and t + 3 may still fly). A bare
+    // s_barrier, not __syncthreads(), whose fence would wait for every load
+    // in flight: this wave's loads into t + 1's stage are complete by the
+    // vmcnt wait, every wave's reads of tile t were consumed by its MFMAs,
+    // and the barrier makes both hold for the whole workgroup.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kLoads) : "memory");
     __builtin_amdgcn_s_barrier();
   };
   int t = 0;
-  for (; t + 2 < n; t += 3) {
-    tile(t, s0, s2);
+  for (; t + 3 < n; t += 4) {
+    tile(t, s0, s3);
     tile(t + 1, s1, s0);
     tile(t + 2, s2, s1);
+    tile(t + 3, s3, s2);
   }
-  if (t < n) tile(t, s0, s2);
+  if (t < n) tile(t, s0, s3);
   if (t + 1 < n) tile(t + 1, s1, s0);
+  if (t + 2 < n) tile(t + 2, s2, s1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-reading loads past n
   __syncthreads();
 }
@@ -1428,8 +1433,8 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   constexpr int BM = kCeRows, BN = 256, WM = 1, WN = 4;
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;
   constexpr int kStage = (BM + BN) * 8;
-  __shared__ uint4 st0[kStage], st1[kStage], st2[kStage];
-  __shared__ float s_loss[4];
+  __shared__ uint4 st0[kStage], st1[kStage], st2[kStage], st3[kStage];
+  float* const s_loss = reinterpret_cast<float*>(st2);  // after the product (st2 is not part of the logits tile)
   // the fp32 logits tile after the product: rows [0, kRows0) in st0, the rest in st1
   constexpr int kRows0 = kStage * 16 / (BN * 4);
   static_assert(BM - kRows0 <= kRows0, "logits tile fits in two stages");
@@ -1448,8 +1453,8 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
     if (lane < BM / 4 && row < p.M) my_lab = labels[row];
   }
   f32x16 acc[MB][NB];
-  static_assert(MB == 2 && NB == 2 && WM == 1 && WN == 4, "ce_mainloop3's tile");
-  ce_mainloop3(p, st0, st1, st2, m0, (p.K + BK - 1) / BK, acc);
+  static_assert(MB == 2 && NB == 2 && WM == 1 && WN == 4, "ce_mainloop4's tile");
+  ce_mainloop4(p, st0, st1, st2, st3, m0, (p.K + BK - 1) / BK, acc);
 
   // logits tile [64][256] fp32 in LDS, 16-byte chunk c of row r at c ^ (r & 63)
 #pragma unroll
@@ -1478,48 +1483,60 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   const int64_t row = static_cast<int64_t>(m0) + r;
   const int64_t lab = __shfl(my_lab, rl, 64);
   const int stag = 2 * q + 4 * (r & 1);
+  const bool lab_ok = lab >= 0 && lab < V;
   float x[64];
-  float m = -INFINITY, picked = 0.0f;
+  float m = -INFINITY;
+  // kFull: V == 256, no class past V to mask
+  auto load_row = [&](auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int c = q * 16 + ((k + stag) & 15);  // this lane's chunk k: classes 4c .. 4c + 3
-    const f4 v = io4<float>::load(tile_row(r) + ((c ^ (r & 63)) * 4));
+    for (int k = 0; k < 16; ++k) {
+      const int c = q * 16 + ((k + stag) & 15);  // this lane's chunk k: classes 4c .. 4c + 3
+      const f4 v = io4<float>::load(tile_row(r) + ((c ^ (r & 63)) * 4));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int cls = 4 * c + e;
-      const float l = cls < V ? v.v[e] : -INFINITY;
-      x[4 * k + e] = l;
-      m = fmaxf(m, l);
-      if (cls == lab) picked = l;
+      for (int e = 0; e < 4; ++e) {
+        const float l = (kFull || 4 * c + e < V) ? v.v[e] : -INFINITY;
+        x[4 * k + e] = l;
+        m = fmaxf(m, l);
+      }
     }
-  }
+  };
+  if (V == 256)
+    load_row(std::true_type{});
+  else
+    load_row(std::false_type{});
+  // the label's logit, read once by each of the row's four lanes
+  const int labi = lab_ok ? static_cast<int>(lab) : 0;
+  const float picked = lab_ok ? tile_row(r)[((labi >> 2) ^ (r & 63)) * 4 + (labi & 3)] : 0.0f;
   m = fmaxf(m, __shfl_xor(m, 1, 64));
   m = fmaxf(m, __shfl_xor(m, 2, 64));
+  // e^(l - m) as 2^(l log2(e) - mc) with mc = m log2(e) rounded once: the
+  // rounding of mc scales every term of the row alike, and the log-sum-exp
+  // below adds back the same mc (classes past V: 2^-inf = 0)
+  const float mc = m * kLog2e;
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 64; ++i) {
-    x[i] = expf(x[i] - m);
+    x[i] = exp2_raw(__builtin_fmaf(x[i], kLog2e, -mc));
     sum += x[i];
   }
   sum += __shfl_xor(sum, 1, 64);
   sum += __shfl_xor(sum, 2, 64);
-  picked += __shfl_xor(picked, 1, 64);
-  picked += __shfl_xor(picked, 2, 64);
   const bool live = row < p.M;
   float lsum = 0.0f;
   if (live && q == 0) {
-    lsum = logf(sum) + m - picked;
-    if ((lab < 0 || lab >= V) && bad_label) atomicOr(bad_label, 1);
+    lsum = logf(sum) + mc * 0.69314718055994531f - picked;
+    if (!lab_ok && bad_label) atomicOr(bad_label, 1);
   }
   if (live) {
-    const float inv = 1.0f / sum;
+    const float s = scale / sum;  // dlogits = softmax * scale - onehot * scale
 #pragma unroll
     for (int u = 0; u < 8; ++u) {  // chunks 2u, 2u + 1 are classes 8 consecutive from 4 c0 (stag is even)
       const int c0 = q * 16 + ((2 * u + stag) & 15);
       if (4 * c0 >= V) continue;
       fv<8> d;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d.v[e] = (x[8 * u + e] * inv - (4 * c0 + e == lab ? 1.0f : 0.0f)) * scale;
+      for (int e = 0; e < 8; ++e) d.v[e] = __builtin_fmaf(x[8 * u + e], s, 4 * c0 + e == lab ? -scale : 0.0f);
       // stochastic rounding of the bf16 gradient (mg_common.h): round-to-nearest errors of
       // this near-uniform softmax repeat across the rows of a label
       iov<bf16_t, 8>::store_grad(dlogits + row * ldd + 4 * c0, d, static_cast<uint32_t>(row * V + 4 * c0), 0x8d4au);
