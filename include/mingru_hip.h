@@ -298,6 +298,11 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  *   workspace: mg_gemm_workspace_bytes(...) bytes (0: the product never
  *   splits), 16-byte aligned; NULL runs unsplit. Calls sharing a workspace
  *   must be ordered on one stream.
+ * Kernel choice (results do not depend on it): bf16 outputs with more
+ *   256 x 256 tiles than CUs run one persistent workgroup per CU; K-split
+ *   products lay their workgroups out so that each XCD's share one split.
+ *   MG_GEMM_PERSIST=0 / MG_GEMM_XCD_SPLIT=0 in the environment turn these
+ *   off (read per call).
  * Requirements: N % 8 == 0; K % 8 == 0 if an operand is K-contiguous;
  *   M % 8 == 0 if A is MN-contiguous; lda, ldb, ldaux % 8 == 0; ldc % 8 == 0
  *   (bf16 C) or % 4 == 0 (fp32 C); A, B, C, bias, aux 16-byte aligned; each
