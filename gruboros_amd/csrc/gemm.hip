@@ -1586,10 +1586,12 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
   const bool wgrad = !ak && !bk;
   // weight gradients whose output dimensions are multiples of 256 run 256 x 256
-  // four-wave tiles (half the L2 traffic per flop of 128 x 128), split along K
-  // to about one workgroup per CU
+  // tiles (half the L2 traffic per flop of 128 x 128), split along K to about
+  // one workgroup per CU; with fewer than 16 such tiles (the logits' 256 x 1024:
+  // 4 tiles, 64 splits of 4 k-tiles) the splits get too short and their
+  // partials too many, and 128 x 128 tiles are faster (measured 27 against 40 us)
 #ifndef MG_GEMM_WGRAD128
-  const bool wgrad_big = wgrad && M % 256 == 0 && N % 256 == 0;
+  const bool wgrad_big = wgrad && M % 256 == 0 && N % 256 == 0 && t256 >= 16;
 #else
   const bool wgrad_big = false;
 #endif
