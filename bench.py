@@ -469,6 +469,18 @@ def main():
     if args.only in (None, "decode"):
         dec = bench_decode()
         print(f"[bench] decode {json.dumps(dec)}", file=sys.stderr, flush=True)
+    cfg5 = None
+    if args.only is None and args.workload == "cfg3":
+        # the ~1B-parameter configuration beside the headline: a few optimizer
+        # steps of 4 accumulated [4, 4096] micro-batches (d2048, L24)
+        torch.cuda.empty_cache()
+        t5 = bench_train(3, 1, B=4, S=4096, dim=2048, depth=24, accum=4)
+        cfg5 = {"workload": "cfg5 minLM train step (vocab 256, d2048, L24, ff4, exp1.0, 4 x [4, 4096] micro-batches "
+                            "accumulated, SF-AdamW)", "steps": 3, "warmup": 1,
+                "ms_per_step": t5["ms_per_step"], "tokens_per_s": t5["tokens_per_step"] / (t5["ms_per_step"] * 1e-3),
+                "TFLOPs": t5["tflops"], "frac_bf16_peak": t5["tflops"] / BF16_PEAK_TFLOPS}
+        print(f"[bench] cfg5 {json.dumps(cfg5)}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     cpu = cpu_scan = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
@@ -529,6 +541,8 @@ def main():
         out["decode"] = dec
     if ref:
         out["reference_loop"] = ref
+    if cfg5:
+        out["cfg5"] = cfg5
     if cpu:
         out["cpu_baseline"] = cpu
     if cpu_scan:
