@@ -57,6 +57,8 @@ SIGNATURES = {
     "mg_column_sum_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_column_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_int, _fp, _vp, _c_size, _vp]),
     "mg_gelu_bwd": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_size, _vp]),
+    "mg_embedding_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int]),
+    "mg_embedding_bwd": (_c_int, [_vp, _fp, _c_i64, _c_i64, _c_int, _c_int, _fp, _c_i64, _vp, _c_size, _vp]),
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),

@@ -22,6 +22,7 @@ from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
 from .. import blocks
+from ..embed import embedding
 from ..linear import feed_forward
 from ..linear import linear as _linear
 from ..loss import logits_cross_entropy
@@ -169,7 +170,7 @@ class minLM(Module):
         """Embedding and the blocks (reference :97-135) as block-level autograd
         functions: returns (x, pending, next_prev_hiddens), x the fp32 residual
         stream and pending the last FeedForward output, not yet added."""
-        x = self.token_emb(ids).float()
+        x = embedding(ids, self.token_emb.weight).float()
         prev_hiddens = iter(default(prev_hiddens, []))
         next_prev_hiddens = []
         pending = None
@@ -187,7 +188,7 @@ class minLM(Module):
     def _trunk(self, ids, prev_hiddens):
         """Embedding, blocks and final norm (reference :97-137) op by op:
         (embed, next_prev_hiddens)."""
-        x = self.token_emb(ids)
+        x = embedding(ids, self.token_emb.weight)
         cd, accurate = self._dtypes()
         x = x.float()  # fp32 residual stream
 

@@ -384,6 +384,22 @@ int mg_gelu_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, in
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Token-embedding weight gradient (reference mingru/minLM.py:92,99: the
+ * backward of nn.Embedding):
+ *   dw[v, :] = sum over t with ids[t] == v of dx[t, :]
+ * (ids int64 [N]; dx fp32 [N, D], row stride ldx; dw fp32 [V, D], row stride
+ * ldw, written, zero rows for ids without tokens). Sums in a fixed order
+ * (token order within chunks of 64 positions, chunks in order), so results
+ * repeat bit for bit. No host round trip (torch's version copies a segment
+ * count to the host). Ids outside [0, V) are skipped.
+ * 1 <= V <= 512, D % 4 == 0, strides % 4 == 0, dx/dw 16-byte aligned, N < 2^31;
+ * workspace of mg_embedding_bwd_workspace_bytes(N, D, V) bytes, 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+size_t mg_embedding_bwd_workspace_bytes(int64_t N, int D, int V);
+int mg_embedding_bwd(const int64_t* ids, const float* dx, int64_t ldx, int64_t N, int D, int V,
+                     float* dw, int64_t ldw, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * One-token decode step (generation), batch 1..8, bf16 weights, fp32
  * residual stream and recurrence state; replaces the per-token call of
  * minLM.forward in reference generate.py:199-212 (mingru/minLM.py:97-138 on

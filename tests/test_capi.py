@@ -80,6 +80,19 @@ def test_argument_errors(L):
     assert L.mg_scan_bwd(*bwd.values()) == 1 and b"dhidden" in L.mg_last_error()
 
 
+def test_embedding_bwd_argument_errors(L):
+    e = dict(ids=16, dx=16, ldx=64, N=100, D=64, V=256, dw=16, ldw=64, ws=16, wsb=1 << 24, stream=None)
+    # (every call below fails its checks before any launch)
+    for bad in ({"V": 0}, {"V": 513}, {"D": 62}, {"ldx": 62}, {"ldw": 32}, {"N": 0}, {"ids": None}, {"dx": 8},
+                {"ws": None}):
+        args = {**e, **bad}
+        rc = L.mg_embedding_bwd(*args.values())
+        assert rc in (1, 3), (bad, rc)
+    assert L.mg_embedding_bwd(*{**e, "wsb": 64}.values()) == 3 and b"workspace" in L.mg_last_error()
+    assert L.mg_embedding_bwd(*{**e, "V": 513}.values()) == 1 and b"V=513" in L.mg_last_error()
+    assert L.mg_embedding_bwd_workspace_bytes(16384, 1024, 256) >= (256 + 256) * 1024 * 4 + 16384 * 4
+
+
 def test_hilo_and_norm_argument_errors(L):
     # hi/lo products need K-contiguous operands and K >= 1; rows must hold 2K values
     g = dict(al=0, A=16, lda=128, bl=0, B=16, ldb=128, M=64, N=64, K=64, epi=0, bias=None, aux=None, ldaux=0,

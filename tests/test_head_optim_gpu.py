@@ -148,6 +148,41 @@ def test_sf_adamw_fused_matches_restatement(wd, form):
     torch.testing.assert_close(ps[0], y, rtol=1e-5, atol=1e-6)
 
 
+def test_sf_adamw_table_is_resent_only_when_it_changes():
+    """The tensor table goes to the device only when its rows change: gradients
+    written in place keep it, gradients at new addresses send a new one; every
+    step matches the restatement either way."""
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    torch.manual_seed(3)
+    shapes = [(300, 17), (65,)]
+    ps = [torch.nn.Parameter(torch.randn(s, device=DEV)) for s in shapes]
+    ref = S.RefAdamWScheduleFree([p.detach().double().cpu().clone() for p in ps], lr=1e-2, betas=(0.9, 0.999),
+                                 weight_decay=0.01, warmup_steps=0)
+    opt = AdamWScheduleFree(ps, lr=1e-2, betas=(0.9, 0.999), weight_decay=0.01)
+    opt.train()
+    grads = [torch.empty(s, device=DEV) for s in shapes]
+    held = []
+    sent = []
+    for step in range(5):
+        if step == 3:  # new gradient tensors while the old ones stay alive: new addresses
+            held.append(grads)
+            grads = [torch.empty(s, device=DEV) for s in shapes]
+        for g in grads:
+            g.normal_()
+        for p, g in zip(ps, grads):
+            p.grad = g
+        opt.step()
+        ref.step([g.double().cpu() for g in grads])
+        sent.append(next(iter(opt._tables.values())).sent)
+        for i, p in enumerate(ps):
+            assert _rel(p, ref.params[i]) < 1e-6, (step, i)
+            assert _rel(opt.state[p]["z"], ref.z[i]) < 1e-6, (step, i)
+    assert sent[1] is sent[0] and sent[2] is sent[0]  # same rows: not sent again
+    assert sent[3] is not sent[2] and sent[3] != sent[2]  # new gradient addresses: sent
+    assert sent[4] is sent[3]
+
+
 def test_bf16_weight_copy_follows_the_master():
     from gruboros_amd.linear import bf16_copy, linear
     from gruboros_amd.optim import AdamWScheduleFree
