@@ -20,6 +20,7 @@ MAX_VOCAB = 512  # mg_embedding_bwd's table limit
 class EmbeddingFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, ids, weight):
+        ids = ids.contiguous()  # (a slice of the batch: one copy, shared by the gather and the backward)
         ctx.save_for_backward(ids)
         ctx.vd = tuple(weight.shape)
         return F.embedding(ids, weight)
