@@ -22,7 +22,7 @@ logaddexp.accumulate and invariants (convexity bounds, constant input,
 geometric closed form, chunked == unchunked, T one-step updates == scan);
 the backward against torch.autograd.gradcheck and the closed form; RMSNorm
 against torch.nn.functional.rms_norm; the loss against
-torch.nn.functional.cross_entropy. Parity of the seeded initialisation
+torch.nn.functional.cross_entropy; the causal convolution against torch.nn.Conv1d. Parity of the seeded initialisation
 order (mingru/minLM.py:157-206) is not pinned: tests share one state dict
 between the oracle and the product instead.
 """
@@ -208,9 +208,29 @@ class _RoundGradBF16(torch.autograd.Function):
         return g.to(torch.bfloat16).to(g.dtype)
 
 
+def causal_dwconv(x, w_dw, b_dw, w_pw, b_pw):
+    """CausalDepthWiseConv1d of mingru/minLM.py:27-39 on x [B, T, D]: a depthwise
+    convolution over time with kernel k = w_dw.shape[-1], left-padded with k - 1
+    zeros (so output t sees inputs t - k + 1 .. t), then a pointwise (1 x 1)
+    convolution across channels:
+        y[b, t, d] = b_dw[d] + sum_j w_dw[d, 0, j] x[b, t + j - (k - 1), d]
+        z[b, t, :] = W_pw y[b, t, :] + b_pw        (W_pw = w_pw[:, :, 0])."""
+    k = w_dw.shape[-1]
+    T = x.shape[1]
+    y = b_dw.expand_as(x).clone()
+    for j in range(k):
+        shift = k - 1 - j                      # input t - shift
+        if shift >= T:
+            continue
+        y[:, shift:, :] += w_dw[:, 0, j] * x[:, :T - shift, :]
+    return y @ w_pw[:, :, 0].t() + b_pw
+
+
 def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=False):
     """Body of mingru/minLM.py:97-138 (embedding -> blocks -> final norm -> logits),
-    conv and dropout disabled. p: state dict already in the working dtype.
+    dropout disabled; a layer whose state holds the conv's keys
+    (`layers.i.0.net.{0,1}.{weight,bias}`, enable_conv=True) adds
+    causal_dwconv(x) to x first (:109-112). p: state dict already in the working dtype.
     Returns (logits, next_prev_hiddens).
 
     bf16_points=True evaluates the same mathematics (in p's dtype) with every
@@ -232,6 +252,9 @@ def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=Fals
         prev = next(hiddens, None)
         if prev is not None:
             prev = prev.to(x.dtype)
+        if pre + "0.net.0.weight" in p:                                    # :109-112 (conv)
+            x = causal_dwconv(x, p[pre + "0.net.0.weight"], p[pre + "0.net.0.bias"], p[pre + "0.net.1.weight"],
+                              p[pre + "0.net.1.bias"]) + x
         n = rg(rms_norm(x, p[pre + "1.weight"]))                           # :121
         w_hg = p[pre + "2.to_hidden_and_gate.weight"]
         di = w_hg.shape[0] // 2
@@ -255,7 +278,8 @@ def minlm_core(p, ids, depth, prev_hiddens=None, expansion=1.0, bf16_points=Fals
 
 def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expansion=1.0, dtype=torch.float64,
                   bf16_points=False):
-    """mingru/minLM.py:86-155 with conv and dropout disabled (enable_conv=False, dropout=0).
+    """mingru/minLM.py:86-155 with dropout disabled (dropout=0); the conv is applied
+    where the state holds its keys (enable_conv=True).
 
     params: state dict with the reference's key names (floating tensors are
     cast to `dtype`). Returns (loss or logits, next_prev_hiddens).
@@ -271,7 +295,8 @@ def minlm_forward(params, ids, depth, return_loss=True, prev_hiddens=None, expan
     return cross_entropy_mean(logits, labels), nxt                         # :146-149
 
 
-def make_minlm_state(num_tokens, dim, depth, ff_mult=4, expansion=1.0, seed=0, dtype=torch.float32):
+def make_minlm_state(num_tokens, dim, depth, ff_mult=4, expansion=1.0, seed=0, dtype=torch.float32,
+                     conv_kernel_size=None):
     """A state dict with the reference's keys, order and shapes
     (mingru/minLM.py:58-75, minGRU.py:40-41), initialised as
     mingru/minLM.py:157-206 describes (distributionally; the RNG draw order of
@@ -283,6 +308,12 @@ def make_minlm_state(num_tokens, dim, depth, ff_mult=4, expansion=1.0, seed=0, d
     sd = {"token_emb.weight": torch.randn(num_tokens, dim, generator=gen) * std}
     for i in range(depth):
         pre = f"layers.{i}."
+        if conv_kernel_size:  # enable_conv=True (random values: the reference keeps nn.Conv1d's init)
+            k = conv_kernel_size
+            sd[pre + "0.net.0.weight"] = torch.randn(dim, 1, k, generator=gen) / math.sqrt(k)
+            sd[pre + "0.net.0.bias"] = torch.randn(dim, generator=gen) * 0.1
+            sd[pre + "0.net.1.weight"] = torch.randn(dim, dim, 1, generator=gen) / math.sqrt(dim)
+            sd[pre + "0.net.1.bias"] = torch.randn(dim, generator=gen) * 0.1
         sd[pre + "1.weight"] = torch.ones(dim)
         sd[pre + "2.to_hidden_and_gate.weight"] = torch.randn(2 * di, dim, generator=gen) * std
         if expansion != 1.0:

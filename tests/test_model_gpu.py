@@ -32,12 +32,14 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm().clamp_min(1e-300))
 
 
-def _model(dim, depth, expansion, dtype, seed=0):
+def _model(dim, depth, expansion, dtype, seed=0, conv_kernel_size=None):
     from gruboros_amd.mingru.minLM import minLM
 
     torch.manual_seed(seed)
-    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=expansion, compute_dtype=dtype)
-    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=expansion, seed=seed + 1)
+    kw = dict(enable_conv=True, conv_kernel_size=conv_kernel_size) if conv_kernel_size else {}
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=expansion, compute_dtype=dtype, **kw)
+    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=expansion, seed=seed + 1,
+                            conv_kernel_size=conv_kernel_size)
     gen = torch.Generator().manual_seed(seed + 2)
     for k in sd:
         if k.endswith("4.2.weight") or k.endswith("to_out.weight"):
@@ -93,6 +95,55 @@ def test_minlm_loss_and_grads(dtype, expansion):
         print(f"{dtype} exp={expansion} vs fp64 with bf16 rounding points: loss {e_loss:.2e}, hiddens {e_hid:.2e}, "
               f"worst grad {worst[0]:.2e} ({worst[1]})", flush=True)
         assert e_loss <= 2e-2 and e_hid <= 2e-2 and worst[0] <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_minlm_with_causal_conv_matches_fp64_oracle(dtype):
+    """enable_conv=True (reference mingru/minLM.py:27-39,109-112): each layer adds
+    a causal depthwise + pointwise convolution of the residual stream before its
+    minGRU block. The conv runs in torch (off the headline configs); the test
+    checks the plumbing around it (the pending FeedForward output added first,
+    the op-by-op trunk) against the fp64 oracle's restatement."""
+    dim, depth, B, S = 64, 2, 2, 130
+    m, sd = _model(dim, depth, 1.0, dtype, conv_kernel_size=3)
+    assert list(m.state_dict().keys()) == list(sd.keys())
+    gen = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, 256, (B, S), generator=gen)
+    loss = m(ids.to(DEV), return_loss=True)
+    loss.backward()
+    p = {k: v.double().requires_grad_(True) for k, v in sd.items()}
+    ref, _ = O.minlm_forward(p, ids, depth, return_loss=True, dtype=torch.float64)
+    ref.backward()
+    e_loss = abs(float(loss) - float(ref)) / abs(float(ref))
+    worst = max((_rel(prm.grad, p[n].grad), n) for n, prm in m.named_parameters())
+    print(f"conv {dtype}: loss {e_loss:.2e}, worst grad {worst[0]:.2e} ({worst[1]})", flush=True)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert e_loss <= tol and worst[0] <= tol
+    assert p["layers.1.0.net.0.weight"].grad.abs().sum() > 0  # the conv is in the graph
+
+
+def test_minlm_with_dropout_eval_matches_oracle_and_train_drops():
+    """dropout > 0 (reference mingru/minLM.py:72,133-135: nn.Dropout on the residual
+    stream after each layer): in eval() the model equals the dropout-free fp64
+    oracle; in train() the loss differs and its gradients stay finite."""
+    from gruboros_amd.mingru.minLM import minLM
+
+    dim, depth, B, S = 64, 2, 2, 66
+    ref_model, sd = _model(dim, depth, 1.0, torch.float32)
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0, dropout=0.1).to(DEV)
+    m.load_state_dict(sd)
+    ids = torch.randint(0, 256, (B, S), generator=torch.Generator().manual_seed(4))
+    m.eval()
+    with torch.no_grad():
+        loss_eval = m(ids.to(DEV), return_loss=True)
+    ref, _ = O.minlm_forward(sd, ids, depth, return_loss=True, dtype=torch.float64)
+    assert abs(float(loss_eval) - float(ref)) / abs(float(ref)) <= 1e-5
+    m.train()
+    torch.manual_seed(0)
+    loss_train = m(ids.to(DEV), return_loss=True)
+    loss_train.backward()
+    assert float(loss_train) != float(loss_eval)
+    assert all(torch.isfinite(q.grad).all() for q in m.parameters() if q.grad is not None)
 
 
 def test_minlm_bf16_feed_forward_forward_on_mg_gemm(monkeypatch):

@@ -255,3 +255,24 @@ def test_planted_index_shift_is_caught():
     lam_guess = dg / (z * (1 - z) * (O.np_g(hidden.numpy()) - np.concatenate([h0.numpy(), h[:, :-1]], 1)))
     wrong = lam_guess * z * (1 - z) * (O.np_g(hidden.numpy()) - h)
     assert not np.allclose(wrong, dg, rtol=1e-3)
+
+
+@pytest.mark.parametrize("T,k", [(9, 3), (9, 4), (2, 4), (1, 3)])
+def test_causal_dwconv_matches_torch_conv1d(T, k):
+    """The oracle's explicit-sum restatement of CausalDepthWiseConv1d
+    (mingru/minLM.py:27-39) against the same module built from torch's
+    nn.Conv1d (left zero padding, depthwise then pointwise), including
+    sequences shorter than the kernel."""
+    torch.manual_seed(T * 10 + k)
+    B, D = 2, 6
+    x = torch.randn(B, T, D, dtype=torch.float64)
+    net = torch.nn.Sequential(torch.nn.Conv1d(D, D, kernel_size=k, groups=D),
+                              torch.nn.Conv1d(D, D, kernel_size=1)).double()
+    want = net(F.pad(x.transpose(1, 2), (k - 1, 0), value=0.0)).transpose(1, 2)
+    got = O.causal_dwconv(x, net[0].weight, net[0].bias, net[1].weight, net[1].bias)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    # causal: output t does not depend on inputs after t
+    x2 = x.clone()
+    x2[:, T - 1, :] += 1.0
+    got2 = O.causal_dwconv(x2, net[0].weight, net[0].bias, net[1].weight, net[1].bias)
+    torch.testing.assert_close(got2[:, :T - 1], got[:, :T - 1], rtol=0, atol=0)
