@@ -46,6 +46,10 @@ BF16 = torch.bfloat16
 # below hipBLASLt's and the GELU epilogue adds ~45 us per layer to the first.
 FF_FORWARD_MG_GEMM = False
 
+# The FeedForward's two weight gradients in one K-split launch
+# (mg_gemm_wgrad_pair) instead of one launch each.
+FF_DW_PAIR = True
+
 
 def _f32(b):
     """A bias as the fp32 contiguous vector the GEMM epilogue adds."""
@@ -170,10 +174,12 @@ class FFBlock(torch.autograd.Function):
                 dp = dp.to(BF16).contiguous()
             dact = gemm.linear_dx(dp, w2b, stochastic=True)            # bf16, stochastically rounded
             dpre, db1 = gelu_backward(dact, pre)                        # bf16, stochastically rounded
-            dW2 = gemm.linear_dw(dp, act)
             db2 = column_sum(dp)
             dn2 = gemm.linear_dx(dpre, w1b, stochastic=True)           # bf16, stochastically rounded
-            dW1 = gemm.linear_dw(dpre, n2)
+            if FF_DW_PAIR:
+                dW2, dW1 = gemm.linear_dw_pair(dp, act, dpre, n2)     # one launch for both weight gradients
+            else:
+                dW2, dW1 = gemm.linear_dw(dp, act), gemm.linear_dw(dpre, n2)
         # x2 = x1 + out: both inputs get the same gradient, written once and returned for both
         # (the consumer, MinGRUBlock.backward, only reads them)
         dx1, _, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, False)

@@ -907,8 +907,9 @@ __device__ __forceinline__ void mainloop_pp(const Params& p, uint4* smem, int m0
 // then sums the partials into C).
 enum CMode { C_STORE = 0, C_ADD = 1, C_SPLIT = 2 };
 
+// One workgroup tile: bx, by stand for blockIdx.x, blockIdx.y of a one-product launch.
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
+__device__ __forceinline__ void gemm_tile(const Params& p, int bx, int by) {
   constexpr int MB = BM / WM / 32, NB = BN / WN / 32;  // 32x32 blocks per wave
   constexpr int kStage = (BM + BN) * 8;                 // uint4 per stage
   // 128 x 128 tiles keep their stages as two distinct objects (the
@@ -921,10 +922,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
 
   int tm, tn, split;
   if (p.xcd_splits > 0) {
-    split_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.xcd_splits, tm, tn, split);
+    split_tile_of(bx, p.tiles_m, p.tiles_n, p.xcd_splits, tm, tn, split);
   } else {
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    split = blockIdx.y;
+    tile_of(bx, p.tiles_m, p.tiles_n, tm, tn);
+    split = by;
   }
   const int m0 = tm * BM, n0 = tn * BN;
   const int nkt = total_ktiles(p);
@@ -1059,6 +1060,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
     }
     __syncthreads();
   }
+}
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM, int EPI, typename TC, int CMODE>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(Params p) {
+  gemm_tile<BM, BN, WM, WN, AK, BKM, EPI, TC, CMODE>(p, blockIdx.x, blockIdx.y);
+}
+
+// Two K-split products in one launch (the FeedForward's two weight
+// gradients): workgroups [0, wgs0) run p0's (tile, split) pairs, the rest
+// p1's, each laid out by split_tile_of. wgs0 is a multiple of 8, so a
+// workgroup's XCD is the same as in a launch of its product alone. One
+// launch fills the CUs with half the splits per product, so half the
+// partial tiles are written and summed.
+template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_pair_kernel(Params p0, Params p1, int wgs0) {
+  const int bx = blockIdx.x;
+  if (bx < wgs0) gemm_tile<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_SPLIT>(p0, bx, 0);
+  else gemm_tile<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_SPLIT>(p1, bx - wgs0, 0);
 }
 
 // ---------------------------------------------------------------- persistent products
@@ -1734,6 +1753,47 @@ int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, 
   return dispatch_epi<BM, BN, 2, WN, false, true>(p, pl, epi, c_dtype, s);
 }
 
+// Split plan of a weight-gradient pair (both operands MN-contiguous, fp32
+// outputs written or added, 256 x 256 tiles): the pair runs as one launch
+// when each product has at least 16 tiles (as a lone weight gradient needs
+// for 256 x 256 tiles), the two together fewer than one per CU, and a split
+// count that keeps both XCD layouts whole. Otherwise each product runs alone.
+struct PairPlan {
+  bool ok;
+  int t0, t1, kt_per_split, splits;
+};
+
+inline PairPlan pair_plan(int M0, int N0, int M1, int N1, int K, bool deterministic) {
+  PairPlan pp{};
+  if (deterministic || K < 1 || M0 % 256 || N0 % 256 || M1 % 256 || N1 % 256) return pp;
+  pp.t0 = (M0 / 256) * (N0 / 256);
+  pp.t1 = (M1 / 256) * (N1 / 256);
+  if (pp.t0 < 16 || pp.t1 < 16 || pp.t0 + pp.t1 >= kCUs) return pp;
+  const int nkt = (K + BK - 1) / BK;
+  const int want = std::min(std::max(kCUs / (pp.t0 + pp.t1), 1), std::max(nkt / 4, 1));
+  pp.kt_per_split = (nkt + want - 1) / want;
+  pp.splits = (nkt + pp.kt_per_split - 1) / pp.kt_per_split;
+  pp.ok = pp.splits >= 2 && (pp.t0 * pp.splits) % 8 == 0 && (pp.t1 * pp.splits) % 8 == 0;
+  return pp;
+}
+
+inline int launch_pair(Params p0, Params p1, const PairPlan& pp, hipStream_t s) {
+  for (Params* p : {&p0, &p1}) {
+    p->tiles_m = p->M / 256;
+    p->tiles_n = p->N / 256;
+    p->kt_per_split = pp.kt_per_split;
+    p->xcd_splits = pp.splits;
+  }
+  hipLaunchKernelGGL((gemm_pair_kernel<256, 256, 4, 2, false, false>), dim3((pp.t0 + pp.t1) * pp.splits), dim3(512), 0,
+                     s, p0, p1, pp.t0 * pp.splits);
+  if (check_launch("mg_gemm_wgrad_pair")) return MG_ERR_HIP;
+  for (const Params* p : {&p0, &p1}) {
+    const int64_t n4 = int64_t(p->M) * (p->N / 4);
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048))), dim3(256),
+                       0, s, p->part, pp.splits, p->M, p->N, static_cast<float*>(p->C), p->ldc, p->accumulate);
+  }
+  return check_launch("mg_gemm_wgrad_pair");
+}
 
 }  // namespace gemm
 }  // namespace mg
@@ -1831,6 +1891,68 @@ extern "C" size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int
   const gemm::Plan pl = gemm::plan(M, N, K, a_layout == MG_KCONTIG, b_layout == MG_KCONTIG, c_dtype, epilogue,
                                    flags & MG_GEMM_DETERMINISTIC, flags & MG_GEMM_HILO);
   return gemm::ws_bytes(pl, M, N);
+}
+
+extern "C" size_t mg_gemm_wgrad_pair_workspace_bytes(int M0, int N0, int M1, int N1, int K, int flags) {
+  if (M0 < 1 || N0 < 1 || M1 < 1 || N1 < 1 || K < 1) return 0;
+  const gemm::PairPlan pp = gemm::pair_plan(M0, N0, M1, N1, K, flags & MG_GEMM_DETERMINISTIC);
+  if (pp.ok) return static_cast<size_t>(pp.splits) * (size_t(M0) * N0 + size_t(M1) * N1) * sizeof(float);
+  return std::max(mg_gemm_workspace_bytes(MG_MNCONTIG, MG_MNCONTIG, M0, N0, K, MG_EPI_NONE, MG_F32, flags),
+                  mg_gemm_workspace_bytes(MG_MNCONTIG, MG_MNCONTIG, M1, N1, K, MG_EPI_NONE, MG_F32, flags));
+}
+
+extern "C" int mg_gemm_wgrad_pair(const void* dy0, int64_t ld_dy0, const void* x0, int64_t ld_x0, int M0, int N0,
+                                  float* dw0, int64_t ldc0, const void* dy1, int64_t ld_dy1, const void* x1,
+                                  int64_t ld_x1, int M1, int N1, float* dw1, int64_t ldc1, int K, int flags,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "mg_gemm_wgrad_pair";
+  if (flags & ~(MG_GEMM_ACCUMULATE | MG_GEMM_DETERMINISTIC)) return fail(MG_ERR_ARG, "%s: unknown flags %d", fn, flags);
+  if (!dy0 || !x0 || !dw0 || !dy1 || !x1 || !dw1) return fail(MG_ERR_ARG, "%s: null operand", fn);
+  if (M0 < 0 || N0 < 0 || M1 < 0 || N1 < 0 || K < 0) return fail(MG_ERR_ARG, "%s: negative size", fn);
+  const gemm::PairPlan pp = gemm::pair_plan(M0, N0, M1, N1, K, (flags & MG_GEMM_DETERMINISTIC) || !workspace);
+  if (!pp.ok) {  // each product alone (mg_gemm validates its arguments)
+    int rc = mg_gemm(MG_MNCONTIG, dy0, ld_dy0, MG_MNCONTIG, x0, ld_x0, M0, N0, K, MG_EPI_NONE, nullptr, nullptr, 0, MG_F32,
+                     dw0, ldc0, flags, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    return mg_gemm(MG_MNCONTIG, dy1, ld_dy1, MG_MNCONTIG, x1, ld_x1, M1, N1, K, MG_EPI_NONE, nullptr, nullptr, 0, MG_F32,
+                   dw1, ldc1, flags, workspace, workspace_bytes, stream);
+  }
+  // (pp.ok: M and N are positive multiples of 256, K >= 1)
+  const void* A[2] = {dy0, dy1};
+  const void* B[2] = {x0, x1};
+  float* C[2] = {dw0, dw1};
+  const int64_t lda[2] = {ld_dy0, ld_dy1}, ldb[2] = {ld_x0, ld_x1}, ldc[2] = {ldc0, ldc1};
+  const int Ms[2] = {M0, M1}, Ns[2] = {N0, N1};
+  gemm::Params p[2] = {};
+  const size_t need = static_cast<size_t>(pp.splits) * (size_t(M0) * N0 + size_t(M1) * N1) * sizeof(float);
+  if (workspace_bytes < need)
+    return fail(MG_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu (mg_gemm_wgrad_pair_workspace_bytes)", fn,
+                workspace_bytes, need);
+  if (!aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: workspace not 16-byte aligned", fn);
+  float* part = static_cast<float*>(workspace);
+  for (int i = 0; i < 2; ++i) {
+    const int M = Ms[i], N = Ns[i];
+    if (lda[i] % 8 || ldb[i] % 8 || ldc[i] % 4) return fail(MG_ERR_ARG, "%s: leading dimensions must span whole 16-byte chunks", fn);
+    if (lda[i] < M || ldb[i] < N || ldc[i] < N) return fail(MG_ERR_ARG, "%s: leading dimension smaller than the row", fn);
+    if (!aligned(A[i], 16) || !aligned(B[i], 16) || !aligned(C[i], 16))
+      return fail(MG_ERR_ARG, "%s: operands must be 16-byte aligned", fn);
+    const int64_t a_span = (int64_t(K - 1) * lda[i] + M) * 2, b_span = (int64_t(K - 1) * ldb[i] + N) * 2;
+    if (a_span + 256 * lda[i] * 2 >= (int64_t(1) << 31) || b_span + 256 * ldb[i] * 2 >= (int64_t(1) << 31))
+      return fail(MG_ERR_ARG, "%s: operands must span less than 2 GiB", fn);
+    gemm::Params& q = p[i];
+    q.A = static_cast<const bf16_t*>(A[i]);
+    q.B = static_cast<const bf16_t*>(B[i]);
+    q.C = C[i];
+    q.lda = lda[i]; q.ldb = ldb[i]; q.ldc = ldc[i];
+    q.M = M; q.N = N; q.K = K;
+    q.a_span = static_cast<uint32_t>(a_span);
+    q.b_span = static_cast<uint32_t>(b_span);
+    q.nkt_seg = (K + gemm::BK - 1) / gemm::BK;
+    q.accumulate = (flags & MG_GEMM_ACCUMULATE) ? 1 : 0;
+    q.part = part;
+    part += static_cast<size_t>(pp.splits) * M * N;
+  }
+  return gemm::launch_pair(p[0], p[1], pp, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mg_logits_cross_entropy_partials(int64_t N) {

@@ -157,6 +157,35 @@ def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16, stochastic=Fals
     return dx
 
 
+def linear_dw_pair(dy0, x0, dy1, x1, deterministic=None):
+    """(dy0^T x0, dy1^T x1), fp32, over the same rows: the FeedForward's two weight gradients in one
+    K-split launch (mg_gemm_wgrad_pair; each product alone where the pair does not apply). Operands
+    over 2 GiB go through linear_dw one product at a time."""
+    n = dy0.shape[0]
+    if deterministic is None:
+        deterministic = torch.are_deterministic_algorithms_enabled()
+    if dy1.shape[0] != n or x0.shape[0] != n or x1.shape[0] != n:
+        raise _lib.MingruHipError("linear_dw_pair: the four operands must have the same number of rows")
+    if _row_step(n, 2 * dy0.stride(0), 2 * x0.stride(0), 2 * dy1.stride(0), 2 * x1.stride(0)) < n:
+        return linear_dw(dy0, x0, deterministic=deterministic), linear_dw(dy1, x1, deterministic=deterministic)
+    _lib.require_cuda(dy0, x0, dy1, x1)
+    if any(t.dtype != torch.bfloat16 for t in (dy0, x0, dy1, x1)):
+        raise _lib.MingruHipError("linear_dw_pair operands must be bfloat16")
+    (m0, n0), (m1, n1) = (dy0.shape[1], x0.shape[1]), (dy1.shape[1], x1.shape[1])
+    out0 = torch.empty(m0, n0, device=dy0.device, dtype=torch.float32)
+    out1 = torch.empty(m1, n1, device=dy0.device, dtype=torch.float32)
+    flags = FLAG_DETERMINISTIC if deterministic else 0
+    L = _lib.lib()
+    wsb = L.mg_gemm_wgrad_pair_workspace_bytes(m0, n0, m1, n1, n, flags)
+    ws = _workspace(out0.device, wsb) if wsb else None
+    rc = L.mg_gemm_wgrad_pair(_lib.ptr(dy0), _rows(dy0, "dy0"), _lib.ptr(x0), _rows(x0, "x0"), m0, n0,
+                              _lib.ptr(out0), n0, _lib.ptr(dy1), _rows(dy1, "dy1"), _lib.ptr(x1), _rows(x1, "x1"),
+                              m1, n1, _lib.ptr(out1), n1, n, flags, _lib.ptr(ws), ws.numel() if ws is not None else 0,
+                              _lib.stream_of(out0))
+    _lib.check(rc, "mg_gemm_wgrad_pair")
+    return out0, out1
+
+
 def linear_dw(dy, x, out=None, accumulate=False, deterministic=None):
     """dy [N, out] bf16, x [N, in] bf16 -> dy^T x [out, in] fp32 (written, or added when accumulate)."""
     n, o = dy.shape

@@ -328,6 +328,27 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
 size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
                                int c_dtype, int flags);
 
+/* Two weight gradients over the same K rows in one launch: the autograd of
+ * the FeedForward's two nn.Linear weights (reference mingru/minLM.py:17-23,
+ * :130), dW_i = dY_i^T X_i, i.e. mg_gemm(MG_MNCONTIG, dy_i, ld_dy_i,
+ * MG_MNCONTIG, x_i, ld_x_i, M_i, N_i, K, MG_EPI_NONE, ..., MG_F32, dw_i,
+ * ldc_i, flags, ...) for i = 0, 1 (dy_i [K, M_i], x_i [K, N_i]; dw_i fp32,
+ * written, or added with MG_GEMM_ACCUMULATE). When both have at least 16
+ * 256 x 256 tiles and fewer than one per CU together, they share one K-split
+ * launch. Each product then has half the splits it would have alone, and
+ * half the partial tiles are written and summed. Otherwise each product
+ * runs alone, as mg_gemm. Results repeat bit for bit (the sum order depends
+ * on the shapes only). flags: MG_GEMM_ACCUMULATE, MG_GEMM_DETERMINISTIC
+ * (the products then run alone, unsplit). workspace:
+ * mg_gemm_wgrad_pair_workspace_bytes(...) bytes, 16-byte aligned (NULL: alone,
+ * unsplit). Requirements as mg_gemm's for these layouts. */
+int mg_gemm_wgrad_pair(const void* dy0, int64_t ld_dy0, const void* x0, int64_t ld_x0, int M0, int N0,
+                       float* dw0, int64_t ldc0,
+                       const void* dy1, int64_t ld_dy1, const void* x1, int64_t ld_x1, int M1, int N1,
+                       float* dw1, int64_t ldc1, int K, int flags,
+                       void* workspace, size_t workspace_bytes, void* stream);
+size_t mg_gemm_wgrad_pair_workspace_bytes(int M0, int N0, int M1, int N1, int K, int flags);
+
 /* fp32 -> bf16 hi/lo pairs for MG_GEMM_HILO operands: out[r, c] =
  * bf16(x[r, c]) (RNE), out[r, cols + c] = bf16(x[r, c] - out[r, c]), for
  * rows x cols (cols % 4 == 0; ldx >= cols, ldo >= 2 cols, both % 4 == 0;

@@ -93,6 +93,31 @@ def test_embedding_bwd_argument_errors(L):
     assert L.mg_embedding_bwd_workspace_bytes(16384, 1024, 256) >= (256 + 256) * 1024 * 4 + 16384 * 4
 
 
+def test_wgrad_pair_argument_errors(L):
+    """Every call here fails validation before any launch (fake, aligned pointers)."""
+    fake = ctypes.c_void_p(1 << 20)
+    ws = 1 << 30
+    ok = dict(dy0=fake, ld_dy0=1024, x0=fake, ld_x0=4096, M0=1024, N0=4096, dw0=fake, ldc0=4096,
+              dy1=fake, ld_dy1=4096, x1=fake, ld_x1=1024, M1=4096, N1=1024, dw1=fake, ldc1=1024, K=16376, flags=0,
+              ws=fake, wsb=ws, stream=None)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.mg_gemm_wgrad_pair(*a.values())
+
+    assert L.mg_gemm_wgrad_pair_workspace_bytes(1024, 4096, 4096, 1024, 16376, 0) == 2 * 2 * 1024 * 4096 * 4
+    assert call(flags=4) == 1                      # hi/lo is not a weight-gradient flag
+    assert call(dy1=None) == 1
+    assert call(M0=-256) == 1
+    assert call(ld_dy0=1000) == 1                  # below M0
+    assert call(ldc1=1020) == 1                    # below N1
+    assert call(ld_x0=4100) == 1                   # not a multiple of 8
+    assert call(x1=ctypes.c_void_p((1 << 20) + 8)) == 1   # misaligned
+    assert call(wsb=1024) == 3                     # workspace too small
+    assert call(K=1 << 20) == 1                    # operands over 2 GiB
+    assert b"mg_gemm_wgrad_pair" in L.mg_last_error()
+
+
 def test_hilo_and_norm_argument_errors(L):
     # hi/lo products need K-contiguous operands and K >= 1; rows must hold 2K values
     g = dict(al=0, A=16, lda=128, bl=0, B=16, ldb=128, M=64, N=64, K=64, epi=0, bias=None, aux=None, ldaux=0,

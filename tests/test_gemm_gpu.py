@@ -463,3 +463,54 @@ def test_gemm_split_layout_matches(al, bl, M, N, K, monkeypatch):
         outs.append(out)
     assert torch.equal(outs[0], outs[1])
     assert _rel(outs[0], a.double() @ b.double().t()) < 1e-5
+
+
+@pytest.mark.parametrize("shapes,K,paired", [
+    (((1024, 4096), (4096, 1024)), 16376, True),    # cfg3 FeedForward weight gradients: 128 tiles x 2 splits
+    (((1024, 1024), (1024, 2048)), 3000, True),     # 48 tiles x 5 splits, ragged K
+    (((264, 512), (512, 264)), 5000, False),        # not whole 256 x 256 tiles: each product alone
+    (((2048, 8192), (8192, 2048)), 1024, False),    # cfg5 widths: 512 tiles, no split
+])
+def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired):
+    """mg_gemm_wgrad_pair (the FeedForward's dW2 = dp^T act and dW1 = dpre^T n2
+    in one K-split launch) against float64 products of the same bf16 inputs
+    (1e-5 relative), against one mg_gemm per product (1e-6 when the pair runs
+    paired, which splits K in half as many parts; bit for bit when it runs
+    each product alone), repeat calls bit for bit, and accumulation."""
+    from gruboros_amd import _lib
+    from gruboros_amd.gemm import linear_dw, linear_dw_pair
+
+    L = _lib.lib()
+    (m0, n0), (m1, n1) = shapes
+    t0, t1 = (m0 // 256) * (n0 // 256), (m1 // 256) * (n1 // 256)
+    whole = m0 % 256 == 0 and n0 % 256 == 0 and m1 % 256 == 0 and n1 % 256 == 0
+    assert paired == (whole and min(t0, t1) >= 16 and t0 + t1 < 256)
+    g = torch.Generator(device=DEV).manual_seed(K + m0)
+    dy0, x0 = [torch.randn(K, c, device=DEV, generator=g).to(torch.bfloat16) for c in (m0, n0)]
+    dy1, x1 = [torch.randn(K, c, device=DEV, generator=g).to(torch.bfloat16) for c in (m1, n1)]
+    a, b = linear_dw_pair(dy0, x0, dy1, x1)
+    a2, b2 = linear_dw_pair(dy0, x0, dy1, x1)
+    assert torch.equal(a, a2) and torch.equal(b, b2)
+    for got, dy, x in ((a, dy0, x0), (b, dy1, x1)):
+        ref = dy.double().t() @ x.double()
+        assert _rel(got, ref) < 1e-5
+        single = linear_dw(dy, x)
+        if paired:
+            assert _rel(got, single) < 1e-6
+        else:
+            assert torch.equal(got, single)
+    # accumulation: dw += product, through the C ABI
+    base0 = torch.randn(m0, n0, device=DEV, generator=g)
+    base1 = torch.randn(m1, n1, device=DEV, generator=g)
+    c0, c1 = base0.clone(), base1.clone()
+    wsb = L.mg_gemm_wgrad_pair_workspace_bytes(m0, n0, m1, n1, K, 1)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=DEV)
+    P = _lib.ptr
+    _lib.check(L.mg_gemm_wgrad_pair(P(dy0), m0, P(x0), n0, m0, n0, P(c0), n0, P(dy1), m1, P(x1), n1, m1, n1, P(c1), n1,
+                                    K, 1, P(ws), ws.numel(), _lib.stream_of(c0)), "mg_gemm_wgrad_pair")
+    assert _rel(c0, base0.double() + a.double()) < 1e-6
+    assert _rel(c1, base1.double() + b.double()) < 1e-6
+    # deterministic: each product alone and unsplit, as mg_gemm's deterministic form
+    d0, d1 = linear_dw_pair(dy0, x0, dy1, x1, deterministic=True)
+    assert torch.equal(d0, linear_dw(dy0, x0, deterministic=True))
+    assert torch.equal(d1, linear_dw(dy1, x1, deterministic=True))
