@@ -47,7 +47,8 @@ BF16 = torch.bfloat16
 FF_FORWARD_MG_GEMM = False
 
 # The FeedForward's two weight gradients in one K-split launch
-# (mg_gemm_wgrad_pair) instead of one launch each.
+# (mg_gemm_wgrad_pair) instead of one launch each; likewise to_out's and
+# to_hidden_and_gate's (expansion != 1).
 FF_DW_PAIR = True
 
 
@@ -108,7 +109,7 @@ class MinGRUBlock(torch.autograd.Function):
             h_pair, wtb = saved[8:10]
             dob = gemm.round_bf16_sr(dout.reshape(N, D).contiguous().float())
             dh = gemm.linear_dx(dob, wtb, out_dtype=torch.float32).view(B, T, Di)
-            if ctx.needs_input_grad[5]:
+            if ctx.needs_input_grad[5] and not (FF_DW_PAIR and ctx.needs_input_grad[3]):
                 dW_to = gemm.linear_dw(dob, h_pair[:, :Di])
         else:
             dh = dout.float()
@@ -122,7 +123,13 @@ class MinGRUBlock(torch.autograd.Function):
             dh0 = _scan_bwd(hg3[..., :Di], hg3[..., Di:], h0, h, None, dh, dh_last, dhg3[..., :Di], dhg3[..., Di:],
                             want_dh0)
         dn = gemm.linear_dx(dhg, whb, stochastic=True)             # bf16, stochastically rounded
-        dW_hg = gemm.linear_dw(dhg, pair[:, :D]) if ctx.needs_input_grad[3] else None
+        dW_hg = None
+        if ctx.needs_input_grad[3]:
+            if ctx.has_to and dout is not None and ctx.needs_input_grad[5] and FF_DW_PAIR:
+                # to_out's and to_hidden_and_gate's weight gradients in one launch
+                dW_to, dW_hg = gemm.linear_dw_pair(dob, h_pair[:, :Di], dhg, pair[:, :D])
+            else:
+                dW_hg = gemm.linear_dw(dhg, pair[:, :D])
         dres = dx1.reshape(N, D) if dx1 is not None else None
         dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, dn, dres, True, BF16, ctx.has_pending)
         return (dx.view(B, T, D), dpend.view(B, T, D) if dpend is not None else None,
