@@ -465,13 +465,14 @@ def test_gemm_split_layout_matches(al, bl, M, N, K, monkeypatch):
     assert _rel(outs[0], a.double() @ b.double().t()) < 1e-5
 
 
-@pytest.mark.parametrize("shapes,K,paired", [
-    (((1024, 4096), (4096, 1024)), 16376, True),    # cfg3 FeedForward weight gradients: 128 tiles x 2 splits
-    (((1024, 1024), (1024, 2048)), 3000, True),     # 48 tiles x 5 splits, ragged K
-    (((264, 512), (512, 264)), 5000, False),        # not whole 256 x 256 tiles: each product alone
-    (((2048, 8192), (8192, 2048)), 1024, False),    # cfg5 widths: 512 tiles, no split
+@pytest.mark.parametrize("shapes,K,paired,strided", [
+    (((1024, 4096), (4096, 1024)), 16376, True, False),    # cfg3 FeedForward weight gradients: 128 tiles x 2 splits
+    (((1024, 1024), (1024, 2048)), 3000, True, False),     # 48 tiles x 5 splits, ragged K
+    (((1024, 1536), (3072, 1024)), 8192, True, True),      # to_out + to_hidden_and_gate at x1.5, hi halves of pairs
+    (((264, 512), (512, 264)), 5000, False, False),        # not whole 256 x 256 tiles: each product alone
+    (((2048, 8192), (8192, 2048)), 1024, False, False),    # cfg5 widths: 512 tiles, no split
 ])
-def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired):
+def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired, strided):
     """mg_gemm_wgrad_pair (the FeedForward's dW2 = dp^T act and dW1 = dpre^T n2
     in one K-split launch) against float64 products of the same bf16 inputs
     (1e-5 relative), against one mg_gemm per product (1e-6 when the pair runs
@@ -488,6 +489,9 @@ def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired):
     g = torch.Generator(device=DEV).manual_seed(K + m0)
     dy0, x0 = [torch.randn(K, c, device=DEV, generator=g).to(torch.bfloat16) for c in (m0, n0)]
     dy1, x1 = [torch.randn(K, c, device=DEV, generator=g).to(torch.bfloat16) for c in (m1, n1)]
+    if strided:  # the x operands as the first halves of [K, 2 n] rows, as the hi/lo pairs are read
+        x0 = torch.cat([x0, torch.randn_like(x0, dtype=torch.float32).to(torch.bfloat16)], 1)[:, :n0]
+        x1 = torch.cat([x1, torch.randn_like(x1, dtype=torch.float32).to(torch.bfloat16)], 1)[:, :n1]
     a, b = linear_dw_pair(dy0, x0, dy1, x1)
     a2, b2 = linear_dw_pair(dy0, x0, dy1, x1)
     assert torch.equal(a, a2) and torch.equal(b, b2)
@@ -506,8 +510,9 @@ def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired):
     wsb = L.mg_gemm_wgrad_pair_workspace_bytes(m0, n0, m1, n1, K, 1)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=DEV)
     P = _lib.ptr
-    _lib.check(L.mg_gemm_wgrad_pair(P(dy0), m0, P(x0), n0, m0, n0, P(c0), n0, P(dy1), m1, P(x1), n1, m1, n1, P(c1), n1,
-                                    K, 1, P(ws), ws.numel(), _lib.stream_of(c0)), "mg_gemm_wgrad_pair")
+    _lib.check(L.mg_gemm_wgrad_pair(P(dy0), m0, P(x0), x0.stride(0), m0, n0, P(c0), n0, P(dy1), m1, P(x1),
+                                    x1.stride(0), m1, n1, P(c1), n1, K, 1, P(ws), ws.numel(), _lib.stream_of(c0)),
+               "mg_gemm_wgrad_pair")
     assert _rel(c0, base0.double() + a.double()) < 1e-6
     assert _rel(c1, base1.double() + b.double()) < 1e-6
     # deterministic: each product alone and unsplit, as mg_gemm's deterministic form
