@@ -26,6 +26,8 @@ SIGNATURES = {
     "mg_scan_workspace_init": (_c_int, [_vp, _c_size, _c_int, _c_int, _c_int, _vp]),
     "mg_scan_workspace_set_max_polls": (_c_int, [_vp, ctypes.c_uint32, _vp]),
     "mg_scan_workspace_check": (_c_int, [_vp, _vp]),
+    "mg_scan_workspace_poll": (_c_int, [_vp, _vp, _vp]),
+    "mg_scan_fwd_noalloc_check": (_c_int, [_vp]),
     "mg_decode_mingru": (_c_int, [_c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                                   _vp]),
     "mg_decode_ff": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),

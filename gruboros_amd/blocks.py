@@ -235,8 +235,12 @@ class FinalNormCE(torch.autograd.Function):
 
 def supported(model):
     """Whether the block path applies: bf16 activations over fp32 masters, no
-    conv, no dropout, and a loss head the streaming kernel takes."""
+    conv, no dropout, a loss head the streaming kernel takes, and widths every
+    product and kernel of the blocks takes (D, Di = D * expansion and the
+    FeedForward's F multiples of 8; mg_gemm's N and K, the scan's Di % 4)."""
     D = model.dim
     V = model.to_logits.weight.shape[0]
     return (all(conv is None and dropout is None for conv, _, _, _, _, dropout in model.layers)
-            and model.token_emb.weight.dtype == torch.float32 and D % 8 == 0 and V % 8 == 0 and V <= 256)
+            and model.token_emb.weight.dtype == torch.float32 and D % 8 == 0 and V % 8 == 0 and V <= 256
+            and all(gru.to_hidden_and_gate.weight.shape[0] % 16 == 0 and ff[0].weight.shape[0] % 8 == 0
+                    for _, _, gru, _, ff, _ in model.layers))

@@ -793,6 +793,34 @@ extern "C" int mg_scan_workspace_set_max_polls(void* workspace, uint32_t max_pol
   return check_launch(fn);
 }
 
+namespace mg {
+namespace scan {
+// The error of a header read back to the host (MG_OK when it is clean).
+static int header_error(const char* fn, const WsHeader& h) {
+  if (h.magic != kWsMagic) return fail(MG_ERR_WORKSPACE, "%s: workspace was never initialised", fn);
+  if (h.err & kErrShape)
+    return fail(MG_ERR_WORKSPACE, "%s: a scan call used this workspace (initialised for B=%d T=%d Di=%d) with "
+                "another shape; its results are invalid", fn, h.B, h.T, h.Di);
+  if (h.err & kErrStall)
+    return fail(MG_ERR_STALL, "%s: a look-back wait gave up after %u polls%s (overlapping calls on one workspace, "
+                "or a corrupted workspace); results invalid, initialise it again", fn, h.max_polls,
+                (h.err & kErrTicket) ? " and a ticket past the last tile was drawn" : "");
+  if (h.err & kErrTicket)
+    return fail(MG_ERR_WORKSPACE, "%s: ticket counters corrupted (overlapping calls on one workspace?); results "
+                "invalid, initialise it again", fn);
+  return MG_OK;
+}
+
+// One thread: ORs the header's error bits (and kErrShape for a missing
+// header) into a host word. Writes only when there is something to report.
+__global__ void poll_kernel(const WsHeader* __restrict__ h, uint32_t* host_word) {
+  uint32_t e = h->err;
+  if (h->magic != kWsMagic) e |= kErrShape;
+  if (e) *host_word = *host_word | e;
+}
+}  // namespace scan
+}  // namespace mg
+
 extern "C" int mg_scan_workspace_check(const void* workspace, void* stream) {
   const char* fn = "mg_scan_workspace_check";
   if (!workspace) return fail(MG_ERR_ARG, "%s: NULL workspace", fn);
@@ -801,45 +829,55 @@ extern "C" int mg_scan_workspace_check(const void* workspace, void* stream) {
   hipError_t e = hipStreamSynchronize(st);
   if (e == hipSuccess) e = hipMemcpy(&h, workspace, sizeof(h), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return fail(MG_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
-  if (h.magic != scan::kWsMagic) return fail(MG_ERR_WORKSPACE, "%s: workspace was never initialised", fn);
-  if (h.err & scan::kErrShape)
-    return fail(MG_ERR_WORKSPACE, "%s: a scan call used this workspace (initialised for B=%d T=%d Di=%d) with "
-                "another shape; its results are invalid", fn, h.B, h.T, h.Di);
-  if (h.err & scan::kErrStall)
-    return fail(MG_ERR_STALL, "%s: a look-back wait gave up after %u polls%s (overlapping calls on one workspace, "
-                "or a corrupted workspace); results invalid, initialise it again", fn, h.max_polls,
-                (h.err & scan::kErrTicket) ? " and a ticket past the last tile was drawn" : "");
-  if (h.err & scan::kErrTicket)
-    return fail(MG_ERR_WORKSPACE, "%s: ticket counters corrupted (overlapping calls on one workspace?); results "
-                "invalid, initialise it again", fn);
-  return MG_OK;
+  return scan::header_error(fn, h);
+}
+
+extern "C" int mg_scan_workspace_poll(const void* workspace, uint32_t* host_word, void* stream) {
+  const char* fn = "mg_scan_workspace_poll";
+  if (!workspace || !aligned(workspace, 16)) return fail(MG_ERR_ARG, "%s: bad workspace pointer", fn);
+  if (!host_word || !aligned(host_word, 4)) return fail(MG_ERR_ARG, "%s: bad host word pointer", fn);
+  void* dev_word = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dev_word, host_word, 0);
+  if (e != hipSuccess || !dev_word)
+    return fail(MG_ERR_ARG, "%s: host_word is not pinned host memory (hipHostGetDevicePointer: %s)", fn,
+                hipGetErrorString(e));
+  hipLaunchKernelGGL(scan::poll_kernel, dim3(1), dim3(1), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const scan::WsHeader*>(workspace), static_cast<uint32_t*>(dev_word));
+  return check_launch(fn);
 }
 
 namespace mg {
 namespace scan {
-// Checks and launches the forward; need: the workspace bytes required (see check_common).
-static int fwd_impl(const char* fn, int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
-                    const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld, float* h_last,
-                    float* ckpt, int B, int T, int Di, void* workspace, size_t workspace_bytes, size_t need,
-                    void* stream) {
-  scan::Geometry g;
+// Checks every argument of a forward call; need: the workspace bytes required
+// (see check_common).
+static int fwd_check(const char* fn, int in_dtype, const void* hidden, const void* gate, int64_t in_sb,
+                     int64_t in_ld, const float* h0, int out_dtype, const void* h, int64_t out_sb, int64_t out_ld,
+                     const float* h_last, const float* ckpt, int B, int T, int Di, void* workspace,
+                     size_t workspace_bytes, size_t need, Geometry& g) {
   int rc;
-  if ((rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, workspace, workspace_bytes, g, need))) return rc;
-  if ((rc = scan::check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
-  if ((rc = scan::check_f32vec(fn, "h0", h0))) return rc;
-  if ((rc = scan::check_f32vec(fn, "h_last", h_last))) return rc;
-  if ((rc = scan::check_f32vec(fn, "ckpt", ckpt))) return rc;
+  if ((rc = check_common(fn, B, T, Di, kFwdTileRows, workspace, workspace_bytes, g, need))) return rc;
+  if ((rc = check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
+  if ((rc = check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
+  if ((rc = check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
+  if ((rc = check_f32vec(fn, "h0", h0))) return rc;
+  if ((rc = check_f32vec(fn, "h_last", h_last))) return rc;
+  if ((rc = check_f32vec(fn, "ckpt", ckpt))) return rc;
+  if (!(in_dtype == MG_BF16 || (in_dtype == MG_F32 && out_dtype == MG_F32)))
+    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
+  return MG_OK;
+}
+
+// Launches a forward whose arguments fwd_check accepted.
+static int fwd_launch(const char* fn, int in_dtype, const void* hidden, const void* gate, int64_t in_sb,
+                      int64_t in_ld, const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
+                      float* h_last, float* ckpt, const Geometry& g, void* workspace, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (in_dtype == MG_BF16 && out_dtype == MG_BF16)
-    scan::launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
-  else if (in_dtype == MG_F32 && out_dtype == MG_F32)
-    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
-  else if (in_dtype == MG_BF16 && out_dtype == MG_F32)
-    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
+    launch_fwd<bf16_t, bf16_t>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
+  else if (in_dtype == MG_F32)
+    launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
   else
-    return fail(MG_ERR_DTYPE, "%s: in_dtype=%d out_dtype=%d unsupported", fn, in_dtype, out_dtype);
+    launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, h, out_sb, out_ld, h_last, ckpt, g, workspace, st);
   return check_launch(fn);
 }
 }  // namespace scan
@@ -849,8 +887,13 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
                            const float* h0, int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
                            float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
                            size_t workspace_bytes, void* stream) {
-  return scan::fwd_impl("mg_scan_fwd", in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last,
-                        ckpt, B, T, Di, workspace, workspace_bytes, 0, stream);
+  const char* fn = "mg_scan_fwd";
+  scan::Geometry g;
+  if (int rc = scan::fwd_check(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last,
+                               ckpt, B, T, Di, workspace, workspace_bytes, 0, g))
+    return rc;
+  return scan::fwd_launch(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last, ckpt, g,
+                          workspace, stream);
 }
 
 extern "C" size_t mg_scan_fwd_noalloc_max_bytes(void) { return scan::kNoAllocBytes; }
@@ -866,17 +909,31 @@ extern "C" int mg_scan_fwd_noalloc(int in_dtype, const void* hidden, const void*
                 "maximum of %zu (use mg_scan_fwd with a workspace)", fn, B, T, Di, need, scan::kNoAllocBytes);
   void* ws = nullptr;
   if (int rc = scan::scratch_ptr(fn, &ws)) return rc;
-  // validate the arguments before anything is enqueued (a NULL workspace skips the launch)
+  // every argument is checked before anything is enqueued: a rejected call
+  // leaves the scratch (and any call still running on it) alone
   scan::Geometry g;
-  if (int rc = scan::check_common(fn, B, T, Di, scan::kFwdTileRows, ws, scan::kNoAllocBytes, g, need)) return rc;
+  if (int rc = scan::fwd_check(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last,
+                               ckpt, B, T, Di, ws, scan::kNoAllocBytes, need, g))
+    return rc;
   // initialise the part this call uses (zeros + header), then the forward on it
   const int64_t n16 = static_cast<int64_t>((need + 15) / 16);
   const int blocks = static_cast<int>(std::min<int64_t>((n16 + 255) / 256, 4096));
   hipLaunchKernelGGL(scan::init_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<uint4*>(ws), n16, B, T, Di, scan::kDefaultPolls);
   if (int rc = check_launch(fn)) return rc;
-  return scan::fwd_impl(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last, ckpt, B,
-                        T, Di, ws, scan::kNoAllocBytes, need, stream);
+  return scan::fwd_launch(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, out_dtype, h, out_sb, out_ld, h_last, ckpt, g,
+                          ws, stream);
+}
+
+extern "C" int mg_scan_fwd_noalloc_check(void* stream) {
+  const char* fn = "mg_scan_fwd_noalloc_check";
+  void* ws = nullptr;
+  if (int rc = scan::scratch_ptr(fn, &ws)) return rc;
+  scan::WsHeader h;
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e == hipSuccess) e = hipMemcpy(&h, ws, sizeof(h), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(MG_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+  return scan::header_error(fn, h);
 }
 
 extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,

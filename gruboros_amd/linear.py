@@ -67,10 +67,20 @@ def column_sum(x2):
     return out
 
 
+def _gelu_grad_f32(pre):
+    """gelu'(x) = Phi(x) + x phi(x) in fp32 (exact erf form of nn.GELU())."""
+    x = pre.float()
+    return 0.5 * (1.0 + torch.erf(x * 0.7071067811865476)) + x * torch.exp(-0.5 * x * x) * 0.3989422804014327
+
+
 def gelu_backward(dh, pre, want_bias_grad=True):
     """(bf16(dh * gelu'(pre)) rounded stochastically, its fp32 column sums) for a bf16 or fp32
-    dh and bf16 pre, [N, C] (mg_gelu_bwd)."""
+    dh and bf16 pre, [N, C] (mg_gelu_bwd). Widths the kernel does not take (C % 8) run as
+    torch elementwise ops in fp32, rounded to nearest."""
     N, C = pre.shape
+    if C % 8 or C < 8 or pre.stride(1) != 1 or dh.stride(1) != 1 or pre.stride(0) % 8 or dh.stride(0) % 8:
+        d = dh.float() * _gelu_grad_f32(pre)
+        return d.to(pre.dtype), (d.sum(0) if want_bias_grad else None)
     L = lib()
     dpre = torch.empty_like(pre)
     db = torch.empty(C, dtype=torch.float32, device=pre.device) if want_bias_grad else None
@@ -139,9 +149,18 @@ class HiddenGateProjection(torch.autograd.Function):
 
 
 def hidden_gate_projection(n, pair, layer):
-    """to_hidden_and_gate(n) with the accurate hidden half; n [..., D] bf16 (hi half of pair)."""
+    """to_hidden_and_gate(n) with the accurate hidden half; n [..., D] bf16 (hi half of pair).
+    Widths mg_gemm does not take (D or Di not a multiple of 8) run the hidden half as an
+    fp32 torch product of hi + lo (the same fp32-accurate value) and the gate half in bf16."""
     w = layer.weight
     shape = n.shape
+    D, Di = shape[-1], w.shape[0] // 2
+    if D % 8 or Di % 8:
+        x32 = pair[..., :D].float() + pair[..., D:].float()
+        x32 = n.float() + (x32 - n.float()).detach()  # value hi + lo, gradient to n
+        hidden = F.linear(x32, w[:Di]).to(torch.bfloat16)
+        gate = linear(n, _RowSlice(layer, Di))
+        return torch.cat([hidden, gate], dim=-1)
     hg = HiddenGateProjection.apply(n.reshape(-1, shape[-1]), pair.reshape(-1, 2 * shape[-1]), w, bf16_pair(w),
                                     bf16_copy(w))
     return hg.view(*shape[:-1], w.shape[0])
@@ -173,10 +192,21 @@ class AccurateLinearF32(torch.autograd.Function):
         return dx, dw, None, None
 
 
+class _RowSlice:
+    """rows [r0:] of a bias-free linear layer's weight, as `linear` takes a layer."""
+
+    def __init__(self, layer, r0):
+        self.weight, self.bias = layer.weight[r0:], None
+
+
 def accurate_linear_f32(x, layer):
-    """layer(x) (no bias) for an fp32 x, to fp32 accuracy on MFMA; fp32 output."""
+    """layer(x) (no bias) for an fp32 x, to fp32 accuracy on MFMA; fp32 output. Widths
+    mg_gemm does not take (either dimension of the weight not a multiple of 8) run as an
+    fp32 torch product."""
     w = layer.weight
     shape = x.shape
+    if w.shape[0] % 8 or w.shape[1] % 8:
+        return F.linear(x, w)
     y = AccurateLinearF32.apply(x.reshape(-1, shape[-1]).contiguous(), w, bf16_pair(w), bf16_copy(w))
     return y.view(*shape[:-1], w.shape[0])
 

@@ -22,6 +22,7 @@ from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
 from .. import blocks
+from .. import scan as scan_errors
 from ..embed import embedding
 from ..linear import feed_forward
 from ..linear import linear as _linear
@@ -111,6 +112,10 @@ class minLM(Module):
 
     def forward(self, x, return_loss=False, return_prev_hiddens=False, prev_hiddens=None):
         """Reference mingru/minLM.py:86-155."""
+        if x.is_cuda:
+            # a look-back error reported since the last step raises here; then
+            # the workspaces are polled again (asynchronously, no host sync)
+            scan_errors.surface_errors(x.device)
         if return_loss:
             x, labels = x[:, :-1], x[:, 1:]
         if exists(prev_hiddens) and not return_loss:

@@ -30,6 +30,7 @@ kept across steps, used in turn, so a step allocates no host memory.
 """
 import torch
 
+from . import scan as _scan
 from ._lib import check, lib, require_cuda, stream_of
 
 
@@ -104,6 +105,7 @@ class AdamWScheduleFree(torch.optim.Optimizer):
     def step(self, closure=None):
         if not self.param_groups[0]["train_mode"]:
             raise RuntimeError("AdamWScheduleFree.step() called in eval mode; call optimizer.train() first")
+        _scan.raise_pending_errors()  # a scan error reported by an earlier poll: do not apply its gradients
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -172,4 +174,6 @@ class AdamWScheduleFree(torch.optim.Optimizer):
                         del p._mg_bf16
             del keep
             group["k"] = k + 1
+        if _scan._WORKSPACES:
+            _scan.poll_workspaces()  # this step's backward scans, read at the next forward or step
         return loss

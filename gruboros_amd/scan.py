@@ -4,6 +4,8 @@ Reference semantics: mingru/minGRU.py:45-69. Given the two halves of the
 ``to_hidden_and_gate`` projection, compute the minGRU hidden sequence
 (`out` before ``to_out``) and ``next_prev_hidden``.
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -44,6 +46,64 @@ def check_workspaces():
     for (dev, sid, B, T, Di), ws in list(_WORKSPACES.items()):
         rc = L.mg_scan_workspace_check(ptr(ws), stream_of(ws))
         check(rc, f"scan workspace (device {dev}, B={B} T={T} Di={Di})")
+
+
+# Errors of the cached workspaces, surfaced without a host synchronisation per
+# step: one pinned host word per device, into which mg_scan_workspace_poll's
+# kernel ORs a workspace's error bits (it writes only when one is set).
+_ERR_WORDS = {}
+
+
+def _err_word(index):
+    w = _ERR_WORDS.get(index)
+    if w is None:
+        w = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        _ERR_WORDS[index] = w
+    return w
+
+
+def poll_workspaces(device=None):
+    """Enqueue the asynchronous error poll of every cached workspace (of
+    `device`, if given), each on the stream the workspace belongs to. Its
+    result reaches the host once that stream has passed the poll;
+    raise_pending_errors reads it there."""
+    L = lib()
+    for (dev, sid, B, T, Di), ws in list(_WORKSPACES.items()):
+        if device is not None and dev != device.index:
+            continue
+        word = _err_word(dev)
+        check(L.mg_scan_workspace_poll(ptr(ws), ctypes.c_void_p(word.data_ptr()), ctypes.c_void_p(sid)),
+              "mg_scan_workspace_poll")
+
+
+def raise_pending_errors():
+    """Raise MingruHipError if an earlier poll reported a workspace error (a
+    look-back wait that gave up, a corrupted or foreign workspace): the scan
+    results since then are invalid. Reads the pinned words only, with no
+    synchronisation. On an error it synchronises to name the workspace, drops
+    every cached workspace (the next call makes fresh ones) and raises."""
+    for dev, word in list(_ERR_WORDS.items()):
+        bits = int(word[0])
+        if bits == 0:
+            continue
+        word.zero_()
+        try:
+            check_workspaces()
+        finally:
+            release_workspaces()
+        raise _lib.MingruHipError(f"a minGRU scan on device {dev} reported workspace error bits {bits:#x} "
+                                  "(1: missing header or another shape, 2: corrupted ticket, 4: a look-back wait "
+                                  "gave up); the scan results since the last clean poll are invalid")
+
+
+def surface_errors(device):
+    """Once per training step (the model's forward and the optimizer step call
+    it): raise a pending workspace error, then poll the workspaces of `device`
+    again. An error made in step k is polled at the start of step k + 1 and
+    raised at the next call after the host has passed that point."""
+    raise_pending_errors()
+    if _WORKSPACES:
+        poll_workspaces(device)
 
 
 def _vec_ok(t: torch.Tensor) -> bool:

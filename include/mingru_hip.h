@@ -44,7 +44,8 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version (major*10000 + minor*100 + patch): 200 = 0.2.0, the ABI
+ * declared in this file. */
 int mg_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -106,6 +107,19 @@ int mg_scan_workspace_init(void* workspace, size_t workspace_bytes, int B, int T
 int mg_scan_workspace_set_max_polls(void* workspace, uint32_t max_polls, void* stream);
 int mg_scan_workspace_check(const void* workspace, void* stream);
 
+/* Asynchronous form of mg_scan_workspace_check, for a training loop that
+ * must not synchronise every step: enqueues on `stream` one single-thread
+ * kernel that ORs the workspace header's error bits (1 = missing header or
+ * another shape, 2 = a ticket past the last tile, 4 = a wait gave up) into
+ * *host_word, which must be pinned host memory (hipHostMalloc). The word is
+ * written only when a bit is set; the caller clears it and reads it at any
+ * later point (after the stream has passed the poll, e.g. at its next
+ * synchronisation), then calls mg_scan_workspace_check for the message.
+ * Same purpose as mg_scan_workspace_check (the error convention of the
+ * scan calls, which replace reference mingru/minGRU.py:16-20,53-69); no
+ * reference counterpart of its own. */
+int mg_scan_workspace_poll(const void* workspace, uint32_t* host_word, void* stream);
+
 int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int64_t in_sb, int64_t in_ld,
                 const float* h0,
@@ -133,6 +147,14 @@ int mg_scan_fwd_noalloc(int in_dtype, const void* hidden, const void* gate,
                         int out_dtype, void* h, int64_t out_sb, int64_t out_ld,
                         float* h_last, float* ckpt,
                         int B, int T, int Di, void* stream);
+
+/* The error word of the allocation-free scratch, as mg_scan_workspace_check
+ * reports a workspace's: synchronises `stream`, reads the scratch header of
+ * the current device and returns MG_OK, MG_ERR_WORKSPACE or MG_ERR_STALL for
+ * the last mg_scan_fwd_noalloc call on this device (each call re-initialises
+ * the header, so earlier calls' errors are gone). Allocates nothing. No
+ * counterpart in the reference: for the same callers as mg_scan_fwd_noalloc. */
+int mg_scan_fwd_noalloc_check(void* stream);
 
 /* Backward of mg_scan_fwd: autograd of reference mingru/minGRU.py:16-20,
  * :53-69 through gate, hidden and prev_hidden, in closed form:

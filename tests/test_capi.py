@@ -39,7 +39,7 @@ def test_every_declared_symbol_is_exported(L):
 
 
 def test_version_and_queries(L):
-    assert L.mg_version() >= 100
+    assert L.mg_version() == 200  # 0.2.0: the ABI of include/mingru_hip.h
     # a 256-byte header, ticket counters per chain and direction (rounded to
     # 256 B) + one 8-byte look-back word per (tile, channel) for the forward
     # (128-step tiles) and the backward (64-step tiles)
@@ -52,6 +52,14 @@ def _fwd(L, **kw):
                 out_ld=64, h_last=None, ckpt=None, B=2, T=8, Di=64, ws=16, wsb=1 << 20, stream=None)
     args.update(kw)
     return L.mg_scan_fwd(*args.values())
+
+
+def test_poll_and_noalloc_check_argument_errors(L):
+    # rejected before any HIP call (no GPU needed)
+    assert L.mg_scan_workspace_poll(None, None, None) == 1
+    assert "bad workspace" in L.mg_last_error().decode()
+    assert L.mg_scan_workspace_poll(16, None, None) == 1
+    assert "host word" in L.mg_last_error().decode()
 
 
 def test_argument_errors(L):

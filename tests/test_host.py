@@ -133,3 +133,21 @@ def test_alias_and_default_compute_dtype():
                 sys.modules.pop(k, None)
             else:
                 sys.modules[k] = v
+
+
+def test_block_path_width_conditions():
+    """The bf16 block path takes only widths every product and kernel of it
+    takes (D, Di = D * expansion, F = D * ff_mult multiples of 8); other
+    models go to the op-by-op path (checked on the GPU in
+    test_widths_outside_the_block_path_train_on_the_op_path)."""
+    from gruboros_amd import blocks
+    from gruboros_amd.mingru.minLM import minLM
+
+    def ok(dim, expansion, ff_mult=4):
+        return blocks.supported(minLM(num_tokens=256, dim=dim, depth=1, ff_mult=ff_mult, expansion=expansion,
+                                      compute_dtype=torch.bfloat16))
+
+    assert ok(1024, 1.0) and ok(1024, 1.5) and ok(1000, 1.0)
+    assert not ok(1000, 1.5)            # Di = 1500
+    assert not ok(1024, 1.0, 4.001)     # F = 4097
+    assert not ok(1004, 1.0)            # D = 1004

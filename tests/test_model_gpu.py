@@ -338,14 +338,167 @@ def _checkpoint_resume(config, batches, make, train):
             assert torch.equal(pb, pa), n
 
 
-def _oracle_fp64_on_device(sd, ids, depth, expansion=1.0):
+def _oracle_fp64_on_device(sd, ids, depth, expansion=1.0, prev_hiddens=None):
     """The fp64 restatement of reference mingru/minLM.py:86-155 with plain torch
     ops on the GPU (float64 everywhere, no library of this build), loss and
-    gradients by autograd."""
+    gradients by autograd; prev_hiddens (detached) seed the layers' scans."""
     p = {k: v.detach().to(DEV, torch.float64).requires_grad_(True) for k, v in sd.items()}
-    loss, hid = O.minlm_forward(p, ids, depth, return_loss=True, expansion=expansion, dtype=torch.float64)
+    prev = [h.detach().to(DEV, torch.float64) for h in prev_hiddens] if prev_hiddens is not None else None
+    loss, hid = O.minlm_forward(p, ids, depth, return_loss=True, prev_hiddens=prev, expansion=expansion,
+                                dtype=torch.float64)
     loss.backward()
     return float(loss), [h.detach() for h in hid], {k: v.grad for k, v in p.items()}
+
+
+def _tbptt_second_chunk(m, sd, ids, depth, expansion, chunk):
+    """train.py:783-804 for two consecutive chunks: the first chunk's training
+    call and backward, its hiddens detached and carried; the second chunk's
+    call model(chunk, return_loss=True, return_prev_hiddens=True,
+    prev_hiddens=hidden_state) and (loss / grad_accum).backward() with
+    grad_accum 1. Returns the errors of the second chunk's loss, next hiddens
+    and worst parameter gradient against the fp64 oracle fed the same
+    detached hiddens."""
+    c1, c2 = ids[:, :chunk], ids[:, chunk:2 * chunk]
+    loss1, hidden_state = m(c1, return_loss=True, return_prev_hiddens=True)
+    loss1.backward()
+    hidden_state = [h.detach() for h in hidden_state]
+    m.zero_grad(set_to_none=True)
+    loss2, hid2 = m(c2, return_loss=True, return_prev_hiddens=True, prev_hiddens=hidden_state)
+    (loss2 / 1).backward()
+    torch.cuda.synchronize()
+    ref_loss, ref_hid, ref_grad = _oracle_fp64_on_device(sd, c2, depth, expansion, prev_hiddens=hidden_state)
+    e_loss = abs(float(loss2.detach()) - ref_loss) / abs(ref_loss)
+    e_hid = max(_rel(a, b) for a, b in zip(hid2, ref_hid))
+    errs = sorted(((_rel(p.grad, ref_grad[n]), n) for n, p in m.named_parameters()), reverse=True)
+    # the carried state matters: the same chunk without it gives another loss
+    ref_cold, _, _ = _oracle_fp64_on_device(sd, c2, depth, expansion)
+    return e_loss, e_hid, errs, abs(ref_cold - ref_loss) / abs(ref_loss)
+
+
+@pytest.mark.parametrize("expansion", [1.0, 1.5])
+def test_tbptt_training_chunk_with_carried_state_small(expansion):
+    """The TBPTT training call with a carried state (train.py:795-804;
+    reference mingru/minLM.py:105,117) at d64 L2 bf16, expansion 1.0 and 1.5
+    (to_out in the chain): second chunk's loss, hiddens and every parameter
+    gradient within 2e-2 of fp64."""
+    m, sd = _model(64, 2, expansion, torch.bfloat16, seed=6)
+    ids = torch.randint(0, 256, (2, 260), device=DEV, generator=torch.Generator(device=DEV).manual_seed(6))
+    e_loss, e_hid, errs, cold = _tbptt_second_chunk(m, sd, ids, 2, expansion, 130)
+    print(f"tbptt small x{expansion}: loss {e_loss:.2e}, hiddens {e_hid:.2e}, worst grads "
+          f"{[(f'{e:.2e}', n) for e, n in errs[:3]]}, cold-start loss gap {cold:.2e}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2 and errs[0][0] <= 2e-2, errs[:3]
+
+
+def test_tbptt_training_chunk_with_carried_state_cfg4():
+    """Same at cfg4's shape: minLM d1024 L8 bf16, two
+    consecutive [4, 2048] chunks of one byte stream, the second seeded with
+    the first's detached hiddens; its loss, next hiddens and every parameter
+    gradient within 2e-2 of the fp64 oracle on the device."""
+    torch.cuda.empty_cache()
+    m, sd = _model(1024, 8, 1.0, torch.bfloat16, seed=4)
+    ids = torch.randint(0, 256, (4, 4096), device=DEV, generator=torch.Generator(device=DEV).manual_seed(4))
+    e_loss, e_hid, errs, cold = _tbptt_second_chunk(m, sd, ids, 8, 1.0, 2048)
+    print(f"tbptt cfg4: loss {e_loss:.2e}, hiddens {e_hid:.2e}, worst grads "
+          f"{[(f'{e:.2e}', n) for e, n in errs[:3]]}, cold-start loss gap {cold:.2e}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2 and errs[0][0] <= 2e-2, errs[:3]
+    del m
+    torch.cuda.empty_cache()
+
+
+def test_cfg5_shapes_match_fp64_oracle():
+    """cfg5's shapes against the oracle: a d2048 ff4 bf16
+    minLM slice of two layers, batch 1 x 4096 ids (a 4095-step scan, K = 2048
+    and 8192 products, a 4096-wide to_hidden_and_gate). Loss, next hiddens
+    and every parameter gradient within 2e-2 of fp64 on the device."""
+    torch.cuda.empty_cache()
+    m, sd = _model(2048, 2, 1.0, torch.bfloat16, seed=5)
+    ids = torch.randint(0, 256, (1, 4096), device=DEV, generator=torch.Generator(device=DEV).manual_seed(5))
+    loss, hid = m(ids, return_loss=True, return_prev_hiddens=True)
+    loss.backward()
+    torch.cuda.synchronize()
+    ref_loss, ref_hid, ref_grad = _oracle_fp64_on_device(sd, ids, 2)
+    e_loss = abs(float(loss.detach()) - ref_loss) / abs(ref_loss)
+    e_hid = max(_rel(a, b) for a, b in zip(hid, ref_hid))
+    errs = sorted(((_rel(p.grad, ref_grad[n]), n) for n, p in m.named_parameters()), reverse=True)
+    print(f"cfg5 shapes vs fp64: loss {e_loss:.2e}, hiddens {e_hid:.2e}, "
+          f"worst grads {[(f'{e:.2e}', n) for e, n in errs[:3]]}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2 and errs[0][0] <= 2e-2, errs[:3]
+    del m
+    torch.cuda.empty_cache()
+
+
+def test_widths_outside_the_block_path_train_on_the_op_path():
+    """dim 1000 at expansion 1.5 (Di 1500, not a multiple of 8): the block path
+    does not apply (blocks.supported is False), and the op-by-op path trains
+    it, with torch fp32 products where mg_gemm's widths do not fit: loss,
+    hiddens and every gradient within 2e-2 of fp64."""
+    from gruboros_amd import blocks
+
+    m, sd = _model(1000, 2, 1.5, torch.bfloat16, seed=8)
+    assert not blocks.supported(m)
+    ids = torch.randint(0, 256, (2, 130), generator=torch.Generator().manual_seed(8))
+    loss, hid = m(ids.to(DEV), return_loss=True, return_prev_hiddens=True)
+    loss.backward()
+    ref_loss, ref_hid, ref_grad = _oracle_fp64_on_device(sd, ids.to(DEV), 2, expansion=1.5)
+    e_loss = abs(float(loss.detach()) - ref_loss) / abs(ref_loss)
+    e_hid = max(_rel(a, b) for a, b in zip(hid, ref_hid))
+    errs = sorted(((_rel(p.grad, ref_grad[n]), n) for n, p in m.named_parameters()), reverse=True)
+    print(f"d1000 x1.5 op path vs fp64: loss {e_loss:.2e}, hiddens {e_hid:.2e}, "
+          f"worst grads {[(f'{e:.2e}', n) for e, n in errs[:3]]}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2 and errs[0][0] <= 2e-2, errs[:3]
+
+
+def test_scan_errors_surface_on_the_training_path():
+    """A look-back error inside the training step reaches the caller without a
+    per-step host synchronisation: the forward and the optimizer step poll the
+    scan workspaces asynchronously (mg_scan_workspace_poll into a pinned host
+    word) and raise at the next call. Forced from the host as the workspace
+    tests do: a 64-poll budget and corrupted forward ticket counters, so every
+    wait ends and every kernel exits normally; then the following call
+    raises, and training resumes on fresh workspaces."""
+    from gruboros_amd import _lib, scan
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    scan.release_workspaces()
+    m, _ = _model(64, 2, 1.0, torch.bfloat16, seed=9)
+    opt = AdamWScheduleFree(m.parameters(), lr=1e-3)
+    opt.train()
+    ids = torch.randint(0, 256, (2, 130), device=DEV, generator=torch.Generator(device=DEV).manual_seed(9))
+
+    def step():
+        loss = m(ids, return_loss=True)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    print("case: clean step", flush=True)
+    step()
+    torch.cuda.synchronize()
+    step()  # polls the clean first step's workspaces; nothing raised
+    torch.cuda.synchronize()
+    (key, ws), = scan._WORKSPACES.items()
+    L, P = _lib.lib(), _lib.ptr
+    B, T, Di = key[2:]
+    ncb = B * Di // 64
+    print("case: corrupted forward counters, 64 polls", flush=True)
+    assert L.mg_scan_workspace_set_max_polls(P(ws), 64, _lib.stream_of(ws)) == 0
+    ws[256:256 + 4 * ncb].view(torch.int32).fill_(1)
+    loss = m(ids, return_loss=True)  # its scans give up; the kernels exit, nothing is raised yet
+    loss.backward()
+    opt.step()  # polls the step's workspaces
+    opt.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    with pytest.raises(_lib.MingruHipError, match="gave up|ticket"):
+        m(ids, return_loss=True)
+    assert not scan._WORKSPACES  # dropped; the next call makes fresh ones
+    print("case: training resumes", flush=True)
+    loss = step()
+    torch.cuda.synchronize()
+    step()
+    torch.cuda.synchronize()
+    assert torch.isfinite(loss).all()
+    scan.check_workspaces()
 
 
 def test_cfg3_training_step_matches_fp64_oracle():
