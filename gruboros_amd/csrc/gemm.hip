@@ -63,6 +63,7 @@ namespace gemm {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;
 
@@ -778,6 +779,325 @@ __device__ __forceinline__ void mainloop_w8(const Params& p, uint4* sa, uint4* s
   __syncthreads();
 }
 
+// ---------------------------------------------------------------- 16x16x32 four-wave loop
+#ifndef MG_GEMM_W4M
+#define MG_GEMM_W4M 1
+#endif
+constexpr bool kUseW4M = MG_GEMM_W4M != 0;
+
+//
+// mainloop_w4m: 256 x 256 tiles, four waves (one per SIMD) of 128 x 128, each
+// as 8 x 8 blocks of v_mfma_f32_16x16x32_bf16 (f32x4 accumulators, 256
+// registers a lane, in AGPRs). Measured on MI355X with random operands, the
+// 16x16x32 instruction draws less energy per flop than 32x32x16 (register-only
+// microbenchmark: 2.02 against 1.75-1.79 PFLOP/s, at 2.04-2.09 against
+// 1.75-1.78 GHz), and these products are power-bound; a 128 x 128 wave tile
+// reads half the LDS fragment bytes per flop of a 64 x 128 one.
+// A k-tile (64 k) is two k-steps of 32:
+//   k-step 0: 64 MFMAs on fragments of k-step 0; k-step 1's fragments read
+//             under them;
+//   mid-tile: wait for this wave's loads of tile t + 1, then the barrier:
+//             tile t + 1 is in its stage for every wave, and every wave has
+//             read all of tile t's fragments (so its stage is free);
+//   k-step 1: 64 MFMAs; under them the loads of tile t + 2 into tile t's
+//             stage and the reads of tile t + 1's k-step 0 fragments.
+// Loads therefore have a k-tile and a half of MFMAs to land (the loop before
+// this one gave them two k-steps of 16).
+// LDS layouts (both distinct from the other loops'):
+//   K-contiguous: [256 rows][8 chunks of 16 B], chunk c of row r at
+//     c ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1). A fragment (16 rows, 8 k
+//     each for the four 16-lane groups) is one 16-byte read per lane; the 16
+//     rows of a lane group land in 16 distinct 16-byte bank groups.
+//   MN-contiguous: [64 k-rows][256], the 32-byte segment s of k-row r at
+//     s ^ t16(r), t16(r) = tr_swz(r) ^ (((r >> 3) & 1) << 2); fragments come
+//     through two LDS transpose reads (4 k-rows each).
+// Loads: every wave issues 8 per operand and k-tile.
+// Load placement in a k-step (A/B'd on MI355X at the cfg3 shapes: one load
+// every three MFMAs from MFMA 1 beat groups of 2 and 4 and a burst by 1-10%)
+#ifndef MG_W4M_LOAD_FIRST
+#define MG_W4M_LOAD_FIRST 1
+#endif
+#ifndef MG_W4M_LOAD_EVERY
+#define MG_W4M_LOAD_EVERY 3
+#endif
+#ifndef MG_W4M_LOAD_GROUP
+#define MG_W4M_LOAD_GROUP 1
+#endif
+__device__ __forceinline__ int tr_swz16(int kr) { return tr_swz(kr) ^ (((kr >> 3) & 1) << 2); }
+
+template <bool KMAJ>
+struct M16Operand;
+
+// Offsets of the loads: everything that decides whether an element lies
+// inside the operand (the row for a K-contiguous operand, the k-row for an
+// MN-contiguous one) is in the per-lane (VGPR) offset, which the buffer's
+// range check covers, so rows past M and k-rows past K read as zero; only
+// offsets that stay inside the operand for every in-range element (the
+// k-tile's columns of a K-contiguous operand, the tile's first column of an
+// MN-contiguous one, whose row count is a multiple of 256) go into the scalar
+// offset. The per-lane offsets are relative to the tile origin; load() adds
+// the origin (a scalar per tile, so a persistent kernel can load the next
+// tile's k-tiles).
+template <>
+struct M16Operand<true> {
+  static constexpr int kReads = 1;  // LDS reads per fragment
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t v[8];  // load i: byte offset of the lane's row and chunk within the tile
+  uint32_t q[2];  // byte address of block 0's fragment at k-step s
+  // wr: first tile row of this wave's 128
+  __device__ __forceinline__ void init(const Operand& o, int wr, int wave, int lane) {
+    rsrc = o.rsrc;
+    // load i of wave w fills rows (8 w + i) 8 + (lane >> 3), whose f is
+    // (lane >> 3) ^ (i & 1); lane l's LDS chunk l & 7 takes global chunk (l & 7) ^ f
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = static_cast<uint32_t>(wave * 64 + i * 8 + (lane >> 3)) * o.ld2 +
+             static_cast<uint32_t>(((lane & 7) ^ (lane >> 3) ^ (i & 1)) << 4);
+    // fragment: lane l reads row wr + 16 I + (l & 15), chunk 4 s + (l >> 4);
+    // f of that row does not depend on I
+    const int hl = lane >> 4, r = wr + (lane & 15);
+    const int f = (r & 7) ^ ((r >> 3) & 1);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) q[s] = static_cast<uint32_t>(r * 128 + ((((4 * s) | hl) ^ f) << 4));
+  }
+  // byte offset of a tile whose first row is r0
+  __device__ __forceinline__ static uint32_t origin(int r0, uint32_t ld2) { return static_cast<uint32_t>(r0) * ld2; }
+  // the k-tile's offset (scalar): k0 (+ kofs, the hi/lo segment) columns
+  __device__ __forceinline__ uint32_t koff(int k0, int kofs, uint32_t) const {
+    return static_cast<uint32_t>(k0 + kofs) * 2u;
+  }
+  __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko, uint32_t org) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * 8 + i) * 64),
+                                             16, v[i] + org, ko, 0, 0);
+  }
+  __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int I) const {
+    const uint32_t a = q[s] + 2048u * I;
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(st) + a));
+  }
+  // Hides the fragment base addresses from loop-invariant hoisting, so each
+  // read is base + immediate (else one register per fragment address).
+  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(q[0]), "+v"(q[1])); }
+};
+
+template <>
+struct M16Operand<false> {
+  static constexpr int kReads = 2;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t v[8];  // load i: k-row (of the k-tile) and column (of the tile) of the lane, in bytes
+  uint32_t z;     // byte address of the lane's first transpose read (block 0, k-step 0)
+  __device__ __forceinline__ void init(const Operand& o, int wr, int wave, int lane) {
+    rsrc = o.rsrc;
+    // load i of wave w fills k-row (8 w + i) 2 + h (h = lane >> 5), chunk
+    // c = lane & 31 of it: tile column 16 ((c >> 1) ^ t16(k-row)) + 8 (c & 1)
+    const int h = lane >> 5, cpos = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kr = (wave * 8 + i) * 2 + h;
+      const int m = (((cpos >> 1) ^ tr_swz16(kr)) << 4) + ((cpos & 1) << 3);
+      v[i] = static_cast<uint32_t>(kr) * o.ld2 + static_cast<uint32_t>(m) * 2u;
+    }
+    // fragment J: column wr + 16 J + (l & 15), k-rows 32 s + 8 g + 0..7
+    // (g = l >> 4): in each 16-lane group lane 4 j + q addresses k-row
+    // 8 g + j, columns 4 q .. 4 q + 3 of the 16-column block
+    const int g = lane >> 4, j = (lane >> 2) & 3, qq = lane & 3;
+    const int kr = 8 * g + j;
+    z = static_cast<uint32_t>(kr * (kW4Rows * 2) + (((wr >> 4) ^ tr_swz16(kr)) << 5) + 8 * qq);
+  }
+  __device__ __forceinline__ static uint32_t origin(int r0, uint32_t) { return static_cast<uint32_t>(r0) * 2u; }
+  // the k-tile's offset: k0 k-rows (added to the per-lane offset, which the range check covers)
+  __device__ __forceinline__ uint32_t koff(int k0, int, uint32_t ld2) const { return static_cast<uint32_t>(k0) * ld2; }
+  __device__ __forceinline__ void load(uint4* st, int wave, int i, uint32_t ko, uint32_t org) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(st + (wave * 8 + i) * 64),
+                                             16, v[i] + ko, org, 0, 0);
+  }
+  __device__ __forceinline__ void opaque() { asm volatile("" : "+v"(z)); }
+  // (wr >> 4) is a multiple of 8, so block J's segment is that of block 0 ^ J
+  __device__ __forceinline__ bf16x8 frag(const uint4* st, int s, int J) const {
+    const char* base =
+        reinterpret_cast<const char*>(st) + (z ^ (static_cast<uint32_t>(J) << 5)) + 32 * s * (kW4Rows * 2);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 4 * kW4Rows * 2));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+// acc += B A on v_mfma_f32_16x16x32_bf16 with acc held in AGPRs and tied
+// (dst = srcC). Written as inline assembly because with 64 separate
+// four-register accumulators filling all 256 AGPRs the register allocator,
+// given the builtin, moved accumulators between registers (hundreds of
+// v_accvgpr moves per k-tile, measured in the assembly); with the operand
+// pinned it keeps each in place. The compiler's hazard checks do not see
+// into the assembly, so mainloop_w4m keeps every hazard away by
+// construction:
+//   * no VALU writes an accumulator: the first k-step uses the srcC = 0 form
+//     (mfma16_agpr_first) instead of a zero fill;
+//   * after the last k-step, mfma16_agpr_drain holds the epilogue's reads of
+//     the accumulators written by the last 16 MFMAs behind 24 wait states
+//     (more than a 16-pass XDL write needs before a VALU read); every other
+//     accumulator was written 16 or more MFMAs before the end;
+//   * a fragment's VGPRs are refilled from LDS at least 11 MFMAs after the
+//     last MFMA that read them, and each accumulator is next read as srcC 64
+//     MFMAs after it was written.
+__device__ __forceinline__ void mfma16_agpr(f32x4v& acc, const bf16x8& b, const bf16x8& a) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ void mfma16_agpr_first(f32x4v& acc, const bf16x8& b, const bf16x8& a) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(b), "v"(a));
+}
+// 24 wait states after the MFMAs that wrote acc[6][*] and acc[7][*]; any read
+// of them depends on this statement's outputs and so comes after it.
+__device__ __forceinline__ void mfma16_agpr_drain(f32x4v (&acc)[8][8]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+               : "+a"(acc[6][0]), "+a"(acc[6][1]), "+a"(acc[6][2]), "+a"(acc[6][3]), "+a"(acc[6][4]),
+                 "+a"(acc[6][5]), "+a"(acc[6][6]), "+a"(acc[6][7]), "+a"(acc[7][0]), "+a"(acc[7][1]),
+                 "+a"(acc[7][2]), "+a"(acc[7][3]), "+a"(acc[7][4]), "+a"(acc[7][5]), "+a"(acc[7][6]),
+                 "+a"(acc[7][7]));
+}
+
+// The four-wave 16x16x32 pipeline's per-wave state (operand offsets, fragment
+// buffers) and its steps, shared by mainloop_w4m and gemm_persist_w4m_kernel.
+template <bool AK, bool BKM>
+struct W4MPipe {
+  static constexpr int kStageA = kW4Rows * 8;  // uint4 of the A tile (B follows)
+  static constexpr int NR = 8 * (M16Operand<AK>::kReads + M16Operand<BKM>::kReads);  // LDS reads per k-step
+  Operand oa, ob;
+  M16Operand<AK> A;
+  M16Operand<BKM> B;
+  bf16x8 af[2][8], bfr[2][8];
+  int wave, nseg, K;
+
+  __device__ __forceinline__ void init(const Params& p, int wave_, int lane) {
+    wave = wave_;
+    oa = make_operand(p.A, p.lda, p.a_span);
+    ob = make_operand(p.B, p.ldb, p.b_span);
+    A.init(oa, (wave >> 1) * 128, wave, lane);
+    B.init(ob, (wave & 1) * 128, wave, lane);
+    nseg = p.hilo ? p.nkt_seg : (1 << 29);  // k-tiles per hi/lo segment (none: never reached; 2 nseg < 2^31)
+    K = p.K;
+  }
+  // byte offsets of the tile origins (m0, n0)
+  __device__ __forceinline__ uint32_t aorg(int m0) const { return M16Operand<AK>::origin(m0, oa.ld2); }
+  __device__ __forceinline__ uint32_t borg(int n0) const { return M16Operand<BKM>::origin(n0, ob.ld2); }
+  // k offsets of k-tile tg of the product. Branch-free (selects), so the
+  // k-loop stays one basic block.
+  __device__ __forceinline__ void koffs(int tg, uint32_t& ao, uint32_t& bo) const {
+    const int seg = tg >= 2 * nseg ? 2 : (tg >= nseg ? 1 : 0);
+    const int k0 = (tg - seg * nseg) * BK;
+    ao = A.koff(k0, seg == 1 ? K : 0, oa.ld2);
+    bo = B.koff(k0, seg == 2 ? K : 0, ob.ld2);
+  }
+  __device__ __forceinline__ void load_tile(uint4* st, uint32_t ao, uint32_t bo, uint32_t ar, uint32_t br) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A.load(st, wave, i, ao, ar);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) B.load(st + kStageA, wave, i, bo, br);
+  }
+  // fragment r (0..15) of a k-step, in the order the MFMAs need them (I
+  // outer): A_0, B_0 .. B_7, A_1 .. A_7
+  __device__ __forceinline__ void read_frag(const uint4* st, int s, int buf, int r) {
+    if (r == 0)
+      af[buf][0] = A.frag(st, s, 0);
+    else if (r <= 8)
+      bfr[buf][r - 1] = B.frag(st + kStageA, s, r - 1);
+    else
+      af[buf][r - 8] = A.frag(st, s, r - 8);
+  }
+  __device__ __forceinline__ void read_all(const uint4* st, int s, int buf) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) read_frag(st, s, buf, r);
+  }
+  __device__ __forceinline__ void opaque() {
+    A.opaque();  // (volatile asm orders memory operations: before the loads)
+    B.opaque();
+  }
+  // One k-step in a fixed instruction order (a scheduling barrier after each
+  // MFMA keeps the compiler from reordering): the 64 MFMAs on fragment buffer
+  // CB (kFirst: acc = product, the first k-step of a tile); after MFMA 3 r,
+  // fragment r of the next k-step (stage rst, k-step rs) into buffer 1 - CB;
+  // the 16 loads of a k-tile (offsets ao, bo, origins ar, br) into stage lst,
+  // MG_W4M_LOAD_GROUP after MFMA MG_W4M_LOAD_FIRST + MG_W4M_LOAD_EVERY g.
+  template <int CB, bool kReads, bool kLoads, bool kFirst>
+  __device__ __forceinline__ void kstep(f32x4v (&acc)[8][8], const uint4* rst, int rs, uint4* lst, uint32_t ao,
+                                        uint32_t bo, uint32_t ar, uint32_t br) {
+    constexpr int LF = MG_W4M_LOAD_FIRST, LE = MG_W4M_LOAD_EVERY, LG = MG_W4M_LOAD_GROUP;
+#pragma unroll
+    for (int m = 0; m < 64; ++m) {
+      const int i = m >> 3, j = m & 7;
+      if constexpr (kFirst)
+        mfma16_agpr_first(acc[i][j], bfr[CB][j], af[CB][i]);
+      else
+        mfma16_agpr(acc[i][j], bfr[CB][j], af[CB][i]);
+      if constexpr (kReads) {
+        if (m % 3 == 0 && m / 3 < 16) read_frag(rst, rs, 1 - CB, m / 3);
+      }
+      if constexpr (kLoads) {
+        if (m >= LF && (m - LF) % LE == 0 && (m - LF) / LE < 16 / LG) {
+#pragma unroll
+          for (int v = (m - LF) / LE * LG; v < ((m - LF) / LE + 1) * LG; ++v) {
+            if (v < 8)
+              A.load(lst, wave, v, ao, ar);
+            else
+              B.load(lst + kStageA, wave, v - 8, bo, br);
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+};
+
+template <bool AK, bool BKM>
+__device__ __forceinline__ void mainloop_w4m(const Params& p, uint4* sa, uint4* sb, int m0, int n0, int kt0, int kt1,
+                                             f32x4v (&acc)[8][8]) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  W4MPipe<AK, BKM> P;
+  P.init(p, wave, lane);
+  const uint32_t ar = P.aorg(m0), br = P.borg(n0);
+  // k offsets of k-tile t (relative to kt0); tiles past kt1 reload tile kt1 - 1
+  auto koffs = [&](int t, uint32_t& ao, uint32_t& bo) { P.koffs(min(kt0 + t, kt1 - 1), ao, bo); };
+  const int n = kt1 - kt0;
+  // prologue: tiles 0 and 1 in flight, tile 0's k-step 0 multiplied, then the
+  // mid-tile barrier of tile 0
+  uint32_t ao, bo;
+  koffs(0, ao, bo);
+  P.load_tile(sa, ao, bo, ar, br);
+  koffs(1, ao, bo);
+  P.load_tile(sb, ao, bo, ar, br);
+  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // tile 0 (tile 1's 16 loads may still be in flight)
+  __syncthreads();
+  P.read_all(sa, 0, 0);
+  P.template kstep<0, true, false, true>(acc, sa, 1, sa, 0, 0, ar, br);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // From the mid-tile barrier of tile t to that of tile t + 1. No load is in
+  // flight at either end, so the loop's back edge carries none (the compiler
+  // then adds no wait of its own for the direct-to-LDS writes):
+  //   k-step 1 of tile t: the loads of tile t + 2 into `cur` (tile t's stage,
+  //     read out by now), tile t + 1's k-step 0 fragments read from `nxt`;
+  //   k-step 0 of tile t + 1, reading its k-step 1 fragments;
+  //   wait for the loads, barrier.
+  auto unit = [&](int t, uint4* cur, const uint4* nxt) __attribute__((always_inline)) {
+    P.opaque();
+    uint32_t lo, lb;
+    koffs(t + 2, lo, lb);
+    P.template kstep<1, true, true, false>(acc, nxt, 0, cur, lo, lb, ar, br);
+    P.template kstep<0, true, false, false>(acc, nxt, 1, cur, 0, 0, ar, br);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // tile t + 2 is in `cur` for every wave; every wave is done with `nxt`
+  };
+  int t = 0;
+  for (; t + 2 < n; t += 2) {
+    unit(t, sa, sb);
+    unit(t + 1, sb, sa);
+  }
+  if (t + 1 < n) unit(t, sa, sb);
+  // k-step 1 of the last tile (its fragments are in buffer 1)
+  P.template kstep<1, false, false, false>(acc, sa, 0, sa, 0, 0, ar, br);
+  mfma16_agpr_drain(acc);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // Ping-pong main loop, 256 x 256 tiles, 8 waves in two groups of four (one
 // wave of each group per SIMD; group g owns tile rows 128 g .. 128 g + 127,
 // each wave 128 x 64). The groups alternate, a workgroup barrier between
@@ -915,6 +1235,7 @@ __device__ __forceinline__ void gemm_tile(const Params& p, int bx, int by) {
   // 128 x 128 tiles keep their stages as two distinct objects (the
   // interleaved schedule needs that); 256 x 256 tiles one array of two.
   constexpr bool kW8 = BM == 256 && BN == 256 && WM == 4 && WN == 2;  // mainloop_w8
+  constexpr bool kW4M = BM == 256 && BN == 256 && WM == 2 && WN == 2 && EPI != EPI_GELU_GRAD && kUseW4M;
   constexpr bool kSplit = BM != 256 || WM * WN == 4 || kW8;
   __shared__ uint4 smem[kSplit ? kStage : 2 * kStage];
   __shared__ uint4 smem_b[kSplit ? kStage : 1];
@@ -934,8 +1255,11 @@ __device__ __forceinline__ void gemm_tile(const Params& p, int bx, int by) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int L = lane & 31, half = lane >> 5;
-  f32x16 acc[MB][NB];
-  if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
+  f32x16 acc[kW4M ? 1 : MB][kW4M ? 1 : NB];
+  f32x4v acc16[kW4M ? 8 : 1][kW4M ? 8 : 1];
+  if constexpr (kW4M)
+    mainloop_w4m<AK, BKM>(p, smem, stage1, m0, n0, kt0, kt1, acc16);
+  else if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 4 && AK && !BKM)
     mainloop_pp<AK, BKM>(p, smem, m0, n0, kt0, kt1, acc);  // both stages in smem (kSplit is false)
   else if constexpr (BM == 256 && BN == 256 && WM == 2 && WN == 2)
     mainloop_w4<AK, BKM>(p, smem, stage1, m0, n0, kt0, kt1, acc);
@@ -991,20 +1315,43 @@ __device__ __forceinline__ void gemm_tile(const Params& p, int bx, int by) {
   fetch_pre(0);
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
+    if constexpr (kW4M) {
+      // 16 x 16 blocks: lane l holds row 16 a + (l & 15), columns 16 J + 4 (l >> 4) .. + 3
+      const int hq = lane >> 4;
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
+      for (int a = 0; a < 2; ++a) {
+        const int r = 16 * a + (lane & 15);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int c = j * 32 + 8 * g + 4 * half;  // column within the wave's region
-        f4 x;
+        for (int J = 0; J < 8; ++J) {
+          const int c = 16 * J + 4 * hq;
+          f4 x;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x.v[e] = acc[i][j][4 * g + e];
-        if constexpr (sizeof(S) == 4) {
-          const int q = c / 4;
-          io4<float>::store(reinterpret_cast<float*>(stage + L * RB + ((q ^ (L % CQ)) * 16)), x);
-        } else {
-          const int q = c / 8;
-          io4<bf16_t>::store(reinterpret_cast<bf16_t*>(stage + L * RB + ((q ^ (L % CQ)) * 16) + 8 * half), x);
+          for (int e = 0; e < 4; ++e) x.v[e] = acc16[2 * i + a][J][e];
+          if constexpr (sizeof(S) == 4) {
+            const int q = c / 4;
+            io4<float>::store(reinterpret_cast<float*>(stage + r * RB + ((q ^ (r % CQ)) * 16)), x);
+          } else {
+            const int q = c / 8;
+            io4<bf16_t>::store(reinterpret_cast<bf16_t*>(stage + r * RB + ((q ^ (r % CQ)) * 16) + 8 * (hq & 1)), x);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = j * 32 + 8 * g + 4 * half;  // column within the wave's region
+          f4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x.v[e] = acc[i][j][4 * g + e];
+          if constexpr (sizeof(S) == 4) {
+            const int q = c / 4;
+            io4<float>::store(reinterpret_cast<float*>(stage + L * RB + ((q ^ (L % CQ)) * 16)), x);
+          } else {
+            const int q = c / 8;
+            io4<bf16_t>::store(reinterpret_cast<bf16_t*>(stage + L * RB + ((q ^ (L % CQ)) * 16) + 8 * half), x);
+          }
         }
       }
     }
@@ -1337,6 +1684,183 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(Params p) {
   }
 }
 
+// Persistent products on the four-wave 16x16x32 pipeline (W4MPipe): one
+// workgroup per CU walks tiles pid, pid + gridDim.x, ... as one continuous
+// k-tile pipeline: the last k-steps of a tile load the next tile's first two
+// k-tiles and read its first fragments, so a tile's epilogue runs with the
+// next tile's operands already in LDS. Needs an even k-tile count (every tile
+// then starts in stage sa).
+// Epilogue, per wave and in registers: bias, then bf16 rounding (round to
+// nearest, or stochastic for a gradient), 16 rows at a time into a
+// wave-private staging block, read back as 16-byte row chunks and stored (for
+// BIAS_GELU the staged values are the pre-activation: it is stored to aux and
+// C = gelu of it). The staging is the wave's own, so the epilogue needs no
+// workgroup barrier, and it is beside the operand stages, which hold the next
+// tile's k-tiles.
+template <bool AK, bool BKM, int EPI>
+__global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
+  using Pipe = W4MPipe<AK, BKM>;
+  constexpr int kStage = 2 * Pipe::kStageA;
+  constexpr bool kBias = EPI == EPI_BIAS || EPI == EPI_BIAS_GELU;
+  __shared__ uint4 sa[kStage];
+  __shared__ uint4 sb[kStage];
+  __shared__ uint4 stg_all[4 * 256];  // per wave: 16 rows x 128 bf16 (16 chunks of 16 bytes a row)
+  __shared__ float4 s_bias[kBias ? 2 : 1][64];
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int n = total_ktiles(p);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  Pipe P;
+  P.init(p, wave, lane);
+  f32x4v acc[8][8];
+  int pid = blockIdx.x;
+  auto origin = [&](int id, int& m0, int& n0) {
+    int tm, tn;
+    tile_of(id, p.tiles_m, p.tiles_n, tm, tn);
+    m0 = tm * 256;
+    n0 = tn * 256;
+  };
+  int m0, n0;
+  origin(pid, m0, n0);
+  uint32_t ar = P.aorg(m0), br = P.borg(n0);
+  __amdgpu_buffer_rsrc_t bias_rsrc;
+  if constexpr (kBias)
+    bias_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.bias), static_cast<short>(0), p.N * 4, 0x00020000);
+  auto load_bias = [&](int par, int col0) {  // wave 0; columns past N read as zero
+    if constexpr (kBias)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bias_rsrc, (__attribute__((address_space(3))) void*)(&s_bias[par][0]), 16,
+                                               static_cast<uint32_t>(col0 + 4 * lane) * 4u, 0, 0, 0);
+  };
+  if (wave == 0) load_bias(0, n0);
+  {  // the first tile: k-tiles 0 and 1 in flight, k-tile 0 waited for, its first fragments read
+    uint32_t ao, bo;
+    P.koffs(0, ao, bo);
+    P.load_tile(sa, ao, bo, ar, br);
+    P.koffs(1 % n, ao, bo);
+    P.load_tile(sb, ao, bo, ar, br);
+  }
+  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  __syncthreads();
+  P.read_all(sa, 0, 0);
+  unsigned char* const stg = reinterpret_cast<unsigned char*>(stg_all) + wave * 4096;
+  for (int it = 0;; ++it) {
+    const int next = pid + static_cast<int>(gridDim.x);
+    const bool has_next = next < ntiles;
+    int m1 = m0, n1 = n0;
+    if (has_next) origin(next, m1, n1);
+    const uint32_t ar1 = P.aorg(m1), br1 = P.borg(n1);
+    // k-step 0 of k-tile 0 (acc = product), reading its k-step 1 fragments;
+    // then k-tile 1 is waited for (with the previous tile's epilogue stores)
+    P.template kstep<0, true, false, true>(acc, sa, 1, sa, 0, 0, ar, br);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // units t = 0 .. n - 2 (as in mainloop_w4m): k-step 1 of k-tile t loading
+    // k-tile t + 2 (the next tile's k-tile 0 for t = n - 2), k-step 0 of
+    // k-tile t + 1
+    auto unit = [&](int t, uint4* cur, const uint4* nxt) __attribute__((always_inline)) {
+      P.opaque();
+      uint32_t lo, lb, la = ar, lbr = br;
+      if (t + 2 < n) {
+        P.koffs(t + 2, lo, lb);
+      } else {
+        P.koffs(0, lo, lb);
+        la = ar1;
+        lbr = br1;
+      }
+      P.template kstep<1, true, true, false>(acc, nxt, 0, cur, lo, lb, la, lbr);
+      P.template kstep<0, true, false, false>(acc, nxt, 1, cur, 0, 0, ar, br);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+    int t = 0;
+    for (; t + 3 < n; t += 2) {
+      unit(t, sa, sb);
+      unit(t + 1, sb, sa);
+    }
+    unit(t, sa, sb);  // t = n - 2
+    // k-step 1 of the last k-tile (stage sb): loads the next tile's k-tile 1
+    // into sb and reads its k-tile 0's first fragments from sa (the last
+    // tile reloads its own k-tile 1, harmlessly). With the GELU epilogue the
+    // fragments are read after it instead (held through it, they pushed its
+    // registers into spills).
+    constexpr bool kLateReads = EPI == EPI_BIAS_GELU;
+    {
+      P.opaque();
+      uint32_t lo, lb;
+      P.koffs(1 % n, lo, lb);
+      P.template kstep<1, !kLateReads, true, false>(acc, sa, 0, sb, lo, lb, ar1, br1);
+    }
+    mfma16_agpr_drain(acc);
+    if (wave == 0 && has_next) load_bias((it + 1) & 1, n1);
+
+    // epilogue (this wave's 128 x 128 block of the tile)
+    const int rl = lane & 15, hq = lane >> 4;
+    const int row0 = m0 + wm * 128, col0 = wn * 128;  // col0 within the tile
+    float4 bq[8];  // the bias of the lane's 4 columns of each 16-column block
+    if constexpr (kBias) {
+#pragma unroll
+      for (int J = 0; J < 8; ++J) bq[J] = s_bias[it & 1][(col0 + 16 * J + 4 * hq) / 4];
+    }
+#pragma unroll
+    for (int I = 0; I < 8; ++I) {
+      __builtin_amdgcn_sched_barrier(0);  // block I's accumulator reads stay here (hoisted, they spill)
+#pragma unroll
+      for (int J = 0; J < 8; ++J) {
+        const int c = col0 + 16 * J + 4 * hq;  // tile column of the lane's first value
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = acc[I][J][e];
+        if constexpr (kBias) {
+          x[0] += bq[J].x; x[1] += bq[J].y; x[2] += bq[J].z; x[3] += bq[J].w;
+        }
+        uint2 w;
+        if constexpr (EPI == EPI_SR) {
+          const uint32_t idx = static_cast<uint32_t>(static_cast<int64_t>(row0 + 16 * I + rl) * p.N + n0 + c);
+          w.x = pack_bf16x2_sr(x[0], x[1], idx, 0x9e5bu);
+          w.y = pack_bf16x2_sr(x[2], x[3], idx + 2, 0x9e5bu);
+        } else {
+          w.x = pack_bf16x2(x[0], x[1]);
+          w.y = pack_bf16x2(x[2], x[3]);
+        }
+        // row rl, 16-byte chunk (2 J + (hq >> 1)) ^ rl, half hq & 1
+        *reinterpret_cast<uint2*>(stg + rl * 256 + ((((2 * J) | (hq >> 1)) ^ rl) << 4) + 8 * (hq & 1)) = w;
+      }
+      // read back 4 rows x 256 bytes per instruction and store
+      const int cq = lane & 15;
+      const int ncol = n0 + col0 + 8 * cq;
+      constexpr int kUnroll = EPI == EPI_BIAS_GELU ? 1 : 4;
+#pragma unroll kUnroll
+      for (int u = 0; u < 4; ++u) {
+        const int rr = 4 * u + (lane >> 4);
+        const uint4 raw = *reinterpret_cast<const uint4*>(stg + rr * 256 + ((cq ^ rr) << 4));
+        const int m = row0 + 16 * I + rr;
+        if (m < p.M && ncol < p.N) {
+          if constexpr (EPI == EPI_BIAS_GELU) {
+            *reinterpret_cast<uint4*>(p.aux + static_cast<int64_t>(m) * p.ldaux + ncol) = raw;
+            const uint32_t wi[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint32_t wo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              wo[e] = pack_bf16x2(gelu(__uint_as_float(wi[e] << 16)), gelu(__uint_as_float(wi[e] & 0xffff0000u)));
+            *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) =
+                make_uint4(wo[0], wo[1], wo[2], wo[3]);
+          } else {
+            *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) = raw;
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    if constexpr (kLateReads) P.read_all(sa, 0, 0);
+    pid = next;
+    m0 = m1;
+    n0 = n1;
+    ar = ar1;
+    br = br1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last tile's spare loads land before the LDS is released
+}
+
 // ---------------------------------------------------------------- loss head
 //
 // Streaming cross-entropy head: logits = E W^T for 64 rows at a time with
@@ -1667,6 +2191,18 @@ int launch_persist(const Params& p0, hipStream_t stream) {
   return check_launch("mg_gemm");
 }
 
+// The persistent four-wave kernel (gemm_persist_w4m_kernel): one workgroup per CU.
+template <bool AK, bool BKM, int EPI>
+int launch_persist_w4m(const Params& p0, hipStream_t stream) {
+  Params p = p0;
+  p.tiles_m = (p.M + 255) / 256;
+  p.tiles_n = (p.N + 255) / 256;
+  p.kt_per_split = total_ktiles(p);
+  const int grid = std::min(p.tiles_m * p.tiles_n, kCUs);
+  hipLaunchKernelGGL((gemm_persist_w4m_kernel<AK, BKM, EPI>), dim3(grid), dim3(256), 0, stream, p);
+  return check_launch("mg_gemm");
+}
+
 // Whether a product that meets the eight-wave loop's conditions runs
 // persistent: a bf16 output written whole (no split, no accumulation), an
 // epilogue done in registers, an even k-tile count, and more tiles than CUs.
@@ -1679,15 +2215,27 @@ inline bool persist_ok(const Params& p, const Plan& pl, int epi, int c_dtype) {
   if (epi != EPI_NONE && epi != EPI_BIAS && epi != EPI_BIAS_GELU && epi != EPI_SR) return false;
   if (total_ktiles(p) % 2) return false;
   const int64_t tiles = int64_t((p.M + 255) / 256) * ((p.N + 255) / 256);
-  return tiles > kCUs || mode == 2;
+  // the four-wave kernel's epilogue (in registers, no workgroup barrier) also
+  // serves products of one tile per CU
+  return tiles > kCUs || mode == 2 || (kUseW4M && mode != 3 && epi != EPI_BIAS_GELU);
 }
 
 template <bool AK, bool BKM>
 int dispatch_persist(const Params& p, int epi, hipStream_t s) {
-  if (epi == EPI_NONE) return launch_persist<AK, BKM, EPI_NONE>(p, s);
-  if (epi == EPI_BIAS) return launch_persist<AK, BKM, EPI_BIAS>(p, s);
-  if (epi == EPI_BIAS_GELU) return launch_persist<AK, BKM, EPI_BIAS_GELU>(p, s);
-  return launch_persist<AK, BKM, EPI_SR>(p, s);
+  if constexpr (kUseW4M) {
+    if (epi == EPI_NONE) return launch_persist_w4m<AK, BKM, EPI_NONE>(p, s);
+    if (epi == EPI_BIAS) return launch_persist_w4m<AK, BKM, EPI_BIAS>(p, s);
+    // the GELU epilogue stays on the eight-wave kernel: with four waves each
+    // computing the GELU of its whole block it measured 199 against 169 us
+    // (16376 x 4096 x 1024)
+    if (epi == EPI_BIAS_GELU) return launch_persist<AK, BKM, EPI_BIAS_GELU>(p, s);
+    return launch_persist_w4m<AK, BKM, EPI_SR>(p, s);
+  } else {
+    if (epi == EPI_NONE) return launch_persist<AK, BKM, EPI_NONE>(p, s);
+    if (epi == EPI_BIAS) return launch_persist<AK, BKM, EPI_BIAS>(p, s);
+    if (epi == EPI_BIAS_GELU) return launch_persist<AK, BKM, EPI_BIAS_GELU>(p, s);
+    return launch_persist<AK, BKM, EPI_SR>(p, s);
+  }
 }
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BKM>
@@ -1732,6 +2280,14 @@ int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, 
         if (ak && !bk) return dispatch_persist<true, false>(p, epi, s);
         if (!ak && !bk) return dispatch_persist<false, false>(p, epi, s);
         return dispatch_persist<false, true>(p, epi, s);
+      }
+      // mainloop_w4m (2 x 2 waves); the GELU epilogue, like its persistent
+      // kernel, on mainloop_w8 (4 x 2), so the two give the same bits
+      if (kUseW4M && epi != EPI_BIAS_GELU) {
+        if (ak && bk) return dispatch_epi<256, 256, 2, 2, true, true>(p, pl, epi, c_dtype, s);
+        if (ak && !bk) return dispatch_epi<256, 256, 2, 2, true, false>(p, pl, epi, c_dtype, s);
+        if (!ak && !bk) return dispatch_epi<256, 256, 2, 2, false, false>(p, pl, epi, c_dtype, s);
+        return dispatch_epi<256, 256, 2, 2, false, true>(p, pl, epi, c_dtype, s);
       }
       if (ak && bk) return dispatch_epi<256, 256, 4, 2, true, true>(p, pl, epi, c_dtype, s);
       if (ak && !bk) return dispatch_epi<256, 256, 4, 2, true, false>(p, pl, epi, c_dtype, s);
@@ -1784,8 +2340,9 @@ inline int launch_pair(Params p0, Params p1, const PairPlan& pp, hipStream_t s) 
     p->kt_per_split = pp.kt_per_split;
     p->xcd_splits = pp.splits;
   }
-  hipLaunchKernelGGL((gemm_pair_kernel<256, 256, 4, 2, false, false>), dim3((pp.t0 + pp.t1) * pp.splits), dim3(512), 0,
-                     s, p0, p1, pp.t0 * pp.splits);
+  constexpr int kWM = kUseW4M ? 2 : 4;  // mainloop_w4m (2 x 2 waves) or mainloop_w8 (4 x 2)
+  hipLaunchKernelGGL((gemm_pair_kernel<256, 256, kWM, 2, false, false>), dim3((pp.t0 + pp.t1) * pp.splits),
+                     dim3(64 * kWM * 2), 0, s, p0, p1, pp.t0 * pp.splits);
   if (check_launch("mg_gemm_wgrad_pair")) return MG_ERR_HIP;
   for (const Params* p : {&p0, &p1}) {
     const int64_t n4 = int64_t(p->M) * (p->N / 4);
