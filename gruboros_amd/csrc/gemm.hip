@@ -55,6 +55,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "mg_common.h"
 
@@ -64,6 +65,7 @@ namespace gemm {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;
 
@@ -954,6 +956,81 @@ __device__ __forceinline__ void mfma16_agpr_drain(f32x4v (&acc)[8][8]) {
                  "+a"(acc[7][7]));
 }
 
+// ---------------------------------------------------------------- bf16 GELU by table
+// bf16(gelu(x)) for a bf16 x (gelu() of mg_common.h, rounded to nearest), as a
+// function of its 16 bits b, mag = b & 0x7fff:
+//   2^-9 <= |x| < 2^15 (biased exponent 118 .. 141): a table of 24 exponents
+//     x 128 mantissas x 2 signs (12 KB), entry 2 (mag - 0x3b00) + sign, filled
+//     from gelu() itself by each workgroup;
+//   2^-125 <= |x| < 2^-9: b - 0x80, i.e. x / 2. The erf term moves x / 2 by
+//     less than 0.8 |x| < 2^-9.3 relatively, under half a bf16 spacing, and
+//     x / 2 is itself a bf16 value;
+//   anything else (zero, subnormals, |x| >= 2^15, inf, NaN) is exceptional:
+//     flagged, and its chunk recomputed with gelu() (gelu_exact_chunk) under
+//     a wave-uniform branch.
+// So every result equals bf16(gelu(x)); a lookup is ~12 VALU operations and
+// one LDS read, against ~30 for erf.
+constexpr int kGeluLutN = 2 * 24 * 128;
+__device__ __forceinline__ void gelu_lut_fill(uint16_t* lut) {
+  for (int i = threadIdx.x; i < kGeluLutN; i += blockDim.x) {
+    const uint32_t b = ((static_cast<uint32_t>(i) & 1u) << 15) | ((static_cast<uint32_t>(i) >> 1) + 0x3b00u);
+    lut[i] = f32_to_bf16(gelu(__uint_as_float(b << 16)));
+  }
+}
+// table index of a value with magnitude bits mag and sign bit sg (clamped into
+// the table outside its range, where the entry is not used)
+__device__ __forceinline__ uint32_t gelu_lut_index(uint32_t mag, uint32_t sg) {
+  const int d = min(max(static_cast<int>(mag) - 0x3b00, 0), kGeluLutN / 2 - 1);
+  return static_cast<uint32_t>(d) * 2u + sg;
+}
+// is a value exceptional (outside both the table and the x / 2 range)?
+__device__ __forceinline__ bool gelu_exceptional(uint32_t mag) { return mag - 0x100u > 0x45ffu; }
+// bf16(gelu) of 8 bf16 values (one 16-byte chunk) from the table; exc is set
+// if one of them is exceptional (the result is then not used). The 8 table
+// reads are issued together (one LDS round trip per chunk).
+__device__ __forceinline__ uint4 gelu_lut_chunk(const uint4& w, const uint16_t* lut, bool& exc) {
+  const uint32_t wi[4] = {w.x, w.y, w.z, w.w};
+  uint32_t b[8], t[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) b[v] = (v & 1) ? (wi[v >> 1] >> 16) : (wi[v >> 1] & 0xffffu);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) t[v] = lut[gelu_lut_index(b[v] & 0x7fffu, b[v] >> 15)];
+  uint32_t wo[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const uint32_t mag = b[v] & 0x7fffu;
+    exc = exc || gelu_exceptional(mag);
+    const uint32_t y = mag < 0x3b00u ? b[v] - 0x80u : t[v];
+    wo[v >> 1] |= (v & 1) ? (y << 16) : y;
+  }
+  return make_uint4(wo[0], wo[1], wo[2], wo[3]);
+}
+// bf16(gelu) of 8 bf16 values (one 16-byte chunk) by gelu() itself
+__device__ __forceinline__ uint4 gelu_exact_chunk(const uint4& w) {
+  const uint32_t wi[4] = {w.x, w.y, w.z, w.w};
+  uint32_t wo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    wo[e] = pack_bf16x2(gelu(__uint_as_float(wi[e] << 16)), gelu(__uint_as_float(wi[e] & 0xffff0000u)));
+  return make_uint4(wo[0], wo[1], wo[2], wo[3]);
+}
+
+// The pre-activation (aux) of the bias + GELU epilogue: a non-temporal store.
+// It is read again only by the backward pass, long after; stored normally it
+// takes the place in the memory-side cache of the activation written beside
+// it, which the next product reads at once (that product measured ~10% slower
+// with the activation half evicted).
+__device__ __forceinline__ void store_aux(bf16_t* dst, const uint4& v) {
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
+}
+
+// f(std::integral_constant<int, M>{}) for each M, in order (a loop whose index
+// is a compile-time constant in the body)
+template <int... M, class F>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, M...>, F&& f) {
+  (f(std::integral_constant<int, M>{}), ...);
+}
+
 // The four-wave 16x16x32 pipeline's per-wave state (operand offsets, fragment
 // buffers) and its steps, shared by mainloop_w4m and gemm_persist_w4m_kernel.
 template <bool AK, bool BKM>
@@ -1020,18 +1097,18 @@ struct W4MPipe {
   __device__ __forceinline__ void kstep(f32x4v (&acc)[8][8], const uint4* rst, int rs, uint4* lst, uint32_t ao,
                                         uint32_t bo, uint32_t ar, uint32_t br) {
     constexpr int LF = MG_W4M_LOAD_FIRST, LE = MG_W4M_LOAD_EVERY, LG = MG_W4M_LOAD_GROUP;
-#pragma unroll
-    for (int m = 0; m < 64; ++m) {
-      const int i = m >> 3, j = m & 7;
+    static_for(std::make_integer_sequence<int, 64>{}, [&](auto mc) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value;
+      constexpr int i = m >> 3, j = m & 7;
       if constexpr (kFirst)
         mfma16_agpr_first(acc[i][j], bfr[CB][j], af[CB][i]);
       else
         mfma16_agpr(acc[i][j], bfr[CB][j], af[CB][i]);
       if constexpr (kReads) {
-        if (m % 3 == 0 && m / 3 < 16) read_frag(rst, rs, 1 - CB, m / 3);
+        if constexpr (m % 3 == 0 && m / 3 < 16) read_frag(rst, rs, 1 - CB, m / 3);
       }
       if constexpr (kLoads) {
-        if (m >= LF && (m - LF) % LE == 0 && (m - LF) / LE < 16 / LG) {
+        if constexpr (m >= LF && (m - LF) % LE == 0 && (m - LF) / LE < 16 / LG) {
 #pragma unroll
           for (int v = (m - LF) / LE * LG; v < ((m - LF) / LE + 1) * LG; ++v) {
             if (v < 8)
@@ -1042,7 +1119,7 @@ struct W4MPipe {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   }
 };
 
@@ -1704,8 +1781,15 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
   constexpr bool kBias = EPI == EPI_BIAS || EPI == EPI_BIAS_GELU;
   __shared__ uint4 sa[kStage];
   __shared__ uint4 sb[kStage];
-  __shared__ uint4 stg_all[4 * 256];  // per wave: 16 rows x 128 bf16 (16 chunks of 16 bytes a row)
+  // per wave: 16 rows x 128 bf16 (16 chunks of 16 bytes a row). Indexed
+  // through this array itself (not a byte pointer into it): the compiler then
+  // tells it apart from the operand stages and does not wait for the next
+  // tile's direct-to-LDS loads before the epilogue's LDS writes.
+  __shared__ uint2 stg2[4 * 512];
   __shared__ float4 s_bias[kBias ? 2 : 1][64];
+  // BIAS_GELU: C = gelu(aux) by table lookup in the epilogue
+  constexpr bool kGelu = EPI == EPI_BIAS_GELU;
+  __shared__ uint16_t s_gelu[kGelu ? kGeluLutN : 1];
   const int ntiles = p.tiles_m * p.tiles_n;
   const int n = total_ktiles(p);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1739,10 +1823,10 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
     P.koffs(1 % n, ao, bo);
     P.load_tile(sb, ao, bo, ar, br);
   }
+  if constexpr (kGelu) gelu_lut_fill(s_gelu);  // under the first loads; the barrier below publishes it
   asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
   __syncthreads();
   P.read_all(sa, 0, 0);
-  unsigned char* const stg = reinterpret_cast<unsigned char*>(stg_all) + wave * 4096;
   for (int it = 0;; ++it) {
     const int next = pid + static_cast<int>(gridDim.x);
     const bool has_next = next < ntiles;
@@ -1780,27 +1864,30 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
     unit(t, sa, sb);  // t = n - 2
     // k-step 1 of the last k-tile (stage sb): loads the next tile's k-tile 1
     // into sb and reads its k-tile 0's first fragments from sa (the last
-    // tile reloads its own k-tile 1, harmlessly). With the GELU epilogue the
-    // fragments are read after it instead (held through it, they pushed its
-    // registers into spills).
-    constexpr bool kLateReads = EPI == EPI_BIAS_GELU;
+    // tile reloads its own k-tile 1, harmlessly)
     {
       P.opaque();
       uint32_t lo, lb;
       P.koffs(1 % n, lo, lb);
-      P.template kstep<1, !kLateReads, true, false>(acc, sa, 0, sb, lo, lb, ar1, br1);
+      P.template kstep<1, true, true, false>(acc, sa, 0, sb, lo, lb, ar1, br1);
     }
     mfma16_agpr_drain(acc);
-    if (wave == 0 && has_next) load_bias((it + 1) & 1, n1);
 
-    // epilogue (this wave's 128 x 128 block of the tile)
-    const int rl = lane & 15, hq = lane >> 4;
+    // epilogue (this wave's 128 x 128 block of the tile). The lane index is
+    // made opaque here, so that the lane-dependent addresses below are
+    // computed per tile, not hoisted out of the tile loop and held in
+    // registers through the k-loop.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int rl = ln & 15, hq = ln >> 4;
     const int row0 = m0 + wm * 128, col0 = wn * 128;  // col0 within the tile
+    uint32_t excmask = 0;  // GELU: bit 4 I + u, chunk (I, u) has a value outside the table
     float4 bq[8];  // the bias of the lane's 4 columns of each 16-column block
     if constexpr (kBias) {
 #pragma unroll
       for (int J = 0; J < 8; ++J) bq[J] = s_bias[it & 1][(col0 + 16 * J + 4 * hq) / 4];
     }
+
 #pragma unroll
     for (int I = 0; I < 8; ++I) {
       __builtin_amdgcn_sched_barrier(0);  // block I's accumulator reads stay here (hoisted, they spill)
@@ -1823,35 +1910,53 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
           w.y = pack_bf16x2(x[2], x[3]);
         }
         // row rl, 16-byte chunk (2 J + (hq >> 1)) ^ rl, half hq & 1
-        *reinterpret_cast<uint2*>(stg + rl * 256 + ((((2 * J) | (hq >> 1)) ^ rl) << 4) + 8 * (hq & 1)) = w;
+        stg2[wave * 512 + rl * 32 + ((((2 * J) | (hq >> 1)) ^ rl) << 1) + (hq & 1)] = w;
       }
       // read back 4 rows x 256 bytes per instruction and store
-      const int cq = lane & 15;
+      const int cq = ln & 15;
       const int ncol = n0 + col0 + 8 * cq;
-      constexpr int kUnroll = EPI == EPI_BIAS_GELU ? 1 : 4;
-#pragma unroll kUnroll
+#pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int rr = 4 * u + (lane >> 4);
-        const uint4 raw = *reinterpret_cast<const uint4*>(stg + rr * 256 + ((cq ^ rr) << 4));
+        const int rr = 4 * u + hq;
+        const uint4 raw = reinterpret_cast<const uint4*>(stg2)[wave * 256 + rr * 16 + (cq ^ rr)];
         const int m = row0 + 16 * I + rr;
         if (m < p.M && ncol < p.N) {
-          if constexpr (EPI == EPI_BIAS_GELU) {
-            *reinterpret_cast<uint4*>(p.aux + static_cast<int64_t>(m) * p.ldaux + ncol) = raw;
-            const uint32_t wi[4] = {raw.x, raw.y, raw.z, raw.w};
-            uint32_t wo[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              wo[e] = pack_bf16x2(gelu(__uint_as_float(wi[e] << 16)), gelu(__uint_as_float(wi[e] & 0xffff0000u)));
-            *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) =
-                make_uint4(wo[0], wo[1], wo[2], wo[3]);
+          if constexpr (kGelu) {
+            store_aux(p.aux + static_cast<int64_t>(m) * p.ldaux + ncol, raw);
+            bool exc = false;
+            const uint4 y = gelu_lut_chunk(raw, s_gelu, exc);
+            *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) = y;
+            excmask |= exc ? 1u << (4 * I + u) : 0u;
           } else {
             *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) = raw;
           }
         }
       }
     }
+    if constexpr (kGelu) {
+      // the chunks with a value outside the table (rare), by gelu() itself,
+      // from the aux chunks the lane stored above (the same thread's store,
+      // waited for). Out of the unrolled block loop: inline there, the exact
+      // path's code made the compiler spill.
+      if (__builtin_amdgcn_ballot_w64(excmask != 0) != 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int ncol = n0 + col0 + 8 * (ln & 15);
+#pragma unroll 1
+        for (int q = 0; q < 32; ++q) {
+          if ((excmask >> q) & 1u) {
+            const int m = row0 + 4 * q + hq;  // block I = q / 4, rows 4 u + hq of it
+            const uint4 raw = *reinterpret_cast<const uint4*>(p.aux + static_cast<int64_t>(m) * p.ldaux + ncol);
+            *reinterpret_cast<uint4*>(static_cast<bf16_t*>(p.C) + static_cast<int64_t>(m) * p.ldc + ncol) =
+                gelu_exact_chunk(raw);
+          }
+        }
+      }
+    }
+    // the next tile's bias, once this epilogue's LDS accesses are issued (an LDS
+    // access after a direct-to-LDS load the compiler cannot tell apart from it
+    // waits for every load in flight)
+    if (wave == 0 && has_next) load_bias((it + 1) & 1, n1);
     if (!has_next) break;
-    if constexpr (kLateReads) P.read_all(sa, 0, 0);
     pid = next;
     m0 = m1;
     n0 = n1;
@@ -2217,7 +2322,7 @@ inline bool persist_ok(const Params& p, const Plan& pl, int epi, int c_dtype) {
   const int64_t tiles = int64_t((p.M + 255) / 256) * ((p.N + 255) / 256);
   // the four-wave kernel's epilogue (in registers, no workgroup barrier) also
   // serves products of one tile per CU
-  return tiles > kCUs || mode == 2 || (kUseW4M && mode != 3 && epi != EPI_BIAS_GELU);
+  return tiles > kCUs || mode == 2 || (kUseW4M && mode != 3);
 }
 
 template <bool AK, bool BKM>
@@ -2225,10 +2330,7 @@ int dispatch_persist(const Params& p, int epi, hipStream_t s) {
   if constexpr (kUseW4M) {
     if (epi == EPI_NONE) return launch_persist_w4m<AK, BKM, EPI_NONE>(p, s);
     if (epi == EPI_BIAS) return launch_persist_w4m<AK, BKM, EPI_BIAS>(p, s);
-    // the GELU epilogue stays on the eight-wave kernel: with four waves each
-    // computing the GELU of its whole block it measured 199 against 169 us
-    // (16376 x 4096 x 1024)
-    if (epi == EPI_BIAS_GELU) return launch_persist<AK, BKM, EPI_BIAS_GELU>(p, s);
+    if (epi == EPI_BIAS_GELU) return launch_persist_w4m<AK, BKM, EPI_BIAS_GELU>(p, s);
     return launch_persist_w4m<AK, BKM, EPI_SR>(p, s);
   } else {
     if (epi == EPI_NONE) return launch_persist<AK, BKM, EPI_NONE>(p, s);
@@ -2281,9 +2383,8 @@ int dispatch_layout(const Params& p, const Plan& pl, bool ak, bool bk, int epi, 
         if (!ak && !bk) return dispatch_persist<false, false>(p, epi, s);
         return dispatch_persist<false, true>(p, epi, s);
       }
-      // mainloop_w4m (2 x 2 waves); the GELU epilogue, like its persistent
-      // kernel, on mainloop_w8 (4 x 2), so the two give the same bits
-      if (kUseW4M && epi != EPI_BIAS_GELU) {
+      // mainloop_w4m (2 x 2 waves), else mainloop_w8 (4 x 2)
+      if (kUseW4M) {
         if (ak && bk) return dispatch_epi<256, 256, 2, 2, true, true>(p, pl, epi, c_dtype, s);
         if (ak && !bk) return dispatch_epi<256, 256, 2, 2, true, false>(p, pl, epi, c_dtype, s);
         if (!ak && !bk) return dispatch_epi<256, 256, 2, 2, false, false>(p, pl, epi, c_dtype, s);

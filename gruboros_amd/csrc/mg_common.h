@@ -297,13 +297,13 @@ __device__ __forceinline__ float erf_pos(float u, float& eu2) {
   return 1.0f - poly * eu2;
 }
 
-// gelu(x) = x/2 (1 + erf(x / sqrt 2)); gelu'(x) = (1 + erf(x / sqrt 2))/2 + x phi(x)
-__device__ __forceinline__ float gelu(float x) {
-  float eu2;
-  const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);
-  return 0.5f * x * (1.0f + copysignf(e, x));
-}
+// gelu(x) = x/2 (1 + erf(x / sqrt 2)), the exact form of nn.GELU(), evaluated in
+// fp32 in the order torch evaluates it (x * 0.5 * (1 + erf(x * 1/sqrt 2))),
+// with the device library's erff. Every forward GELU of this library calls it
+// (or reads the table gemm.hip fills from it), so all paths give the same bits.
+__device__ __forceinline__ float gelu(float x) { return x * 0.5f * (1.0f + erff(x * 0.70710678118654752f)); }
 
+// gelu'(x) = (1 + erf(x / sqrt 2))/2 + x phi(x)
 __device__ __forceinline__ float gelu_grad(float x) {
   float eu2;  // e^{-x^2/2}
   const float e = erf_pos(fabsf(x) * 0.70710678118654752f, eu2);

@@ -125,6 +125,54 @@ def test_gemm_epilogues_256_tiles():
     assert _rel(dx, (dy.float() @ w2.float()) * p.grad) < 4e-3
 
 
+def test_bias_gelu_epilogue_every_bf16_value():
+    """The bias + GELU epilogue over all 65536 bf16 values: x = 0 and bias =
+    every bf16 bit pattern (as fp32), so aux = bias and C = bf16(gelu(aux)).
+    The persistent kernel (512 x 65536: 512 tiles) looks GELU up in a table;
+    the per-tile kernel (16 rows) computes it: the two agree bit for bit.
+    Against torch's CPU GELU (the same fp32 formula x (1 + erf(x / sqrt 2)) / 2
+    with another erf): equal on >= 99.5% of the finite values, and within
+    |x| 2^-22 (the rounding of 1 + erf, which cancels for x < -3) plus one bf16
+    spacing everywhere. Checked by the formula's value instead: NaN -> NaN,
+    +inf -> +inf, -inf -> NaN, and x > 2^127 -> x (torch's CPU kernel forms
+    x (1 + erf) first and overflows there)."""
+    from gruboros_amd.gemm import EPI_BIAS_GELU, KCONTIG, gemm
+
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    vals = bits.view(torch.bfloat16)
+    N, K = vals.numel(), 128
+    bias = vals.float().to(DEV)
+    w = torch.randn(N, K, device=DEV).to(torch.bfloat16)
+    pre = vals.clone()
+    pre[bits == -32768] = 0.0  # aux = 0 + bias: +0 for -0
+    outs = []
+    for M in (512, 16):
+        x = torch.zeros(M, K, device=DEV, dtype=torch.bfloat16)
+        aux = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+        out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+        gemm(x, KCONTIG, w, KCONTIG, M, N, K, out, epilogue=EPI_BIAS_GELU, bias=bias, aux=aux)
+        torch.cuda.synchronize()
+        a = aux.cpu()
+        assert bool(((a.view(torch.int16) == pre.view(torch.int16)) | (a.isnan() & pre.isnan())).all())
+        outs.append(out.cpu())
+    big, small = outs
+    assert bool((big.view(torch.int16) == small[:1].view(torch.int16)).all())  # table == computed, every row
+    got = small[0]
+    assert bool(got[pre.isnan()].isnan().all())
+    inf = pre.isinf()
+    assert got[inf & (pre > 0)].item() == float("inf") and bool(got[inf & (pre < 0)].isnan().all())
+    huge = pre.float() > 2.0 ** 127
+    assert bool((got[huge].view(torch.int16) == pre[huge].view(torch.int16)).all())
+    fin = pre.isfinite() & ~huge
+    ref = torch.nn.functional.gelu(pre[fin].float()).bfloat16()
+    g = got[fin]
+    assert not bool(g.isnan().any())
+    same = g.view(torch.int16) == ref.view(torch.int16)
+    assert float(same.float().mean()) >= 0.995, int((~same).sum())
+    xd, gd, rd = pre[fin].double(), g.double(), ref.double()
+    assert bool(((gd - rd).abs() <= xd.abs() * 2.0 ** -22 + rd.abs() * 2.0 ** -7 + 2.0 ** -133).all())
+
+
 def test_gemm_accumulate_and_split():
     """fp32 dW-shaped product (long K, 79 k-tiles): split along K into slices
     of an odd k-tile count, summed by the reduction pass; accumulate adds to C."""
