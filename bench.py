@@ -308,6 +308,12 @@ def bench_kernels(reps=20, N=8 * 2047, D=1024, F=4096, V=256):
             ms = _event_time(fn, reps)
             gemms[f"{name}_{kind}"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
                                        "frac_bf16_peak": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+        if name == "ff_in":  # the FeedForward's first product as the step runs it: bias + GELU epilogue
+            ba = torch.randn(fout, device=dev, generator=g)
+            pre = torch.empty(N, fout, device=dev, dtype=torch.bfloat16)
+            ms = _event_time(lambda: gemm.linear_fwd(xa, wa, ba, gelu_pre=pre), reps)
+            gemms["ff_in_fwd_bias_gelu"] = {"us": ms * 1e3, "TFLOPs": fl / (ms * 1e-3) / 1e12,
+                                            "frac_bf16_peak": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
     out["mfma_gemm"] = gemms
     return out
 

@@ -27,7 +27,6 @@ are the fp32 residual stream's, the fp32 minGRU output's, and the bf16
 FeedForward output's (stochastically rounded by the next block's norm).
 """
 import torch
-import torch.nn.functional as F
 
 from . import _lib
 from . import gemm
@@ -39,12 +38,6 @@ from .scan import _launch_bwd as _scan_bwd
 from .scan import _launch_fwd as _scan_fwd
 
 BF16 = torch.bfloat16
-
-# FeedForward forward on mg_gemm (bias + GELU epilogue, then bias) instead of
-# hipBLASLt and torch's GELU. Off: on the cfg3 step it measured 0.4 ms slower
-# (13.3 against 12.9 ms, same process and box): the two products run 15-20%
-# below hipBLASLt's and the GELU epilogue adds ~45 us per layer to the first.
-FF_FORWARD_MG_GEMM = False
 
 # The FeedForward's two weight gradients in one K-split launch
 # (mg_gemm_wgrad_pair) instead of one launch each; likewise to_out's and
@@ -142,10 +135,9 @@ class FFBlock(torch.autograd.Function):
 
     x1 fp32 [B, T, D]; out fp32 [B, T, D] (the minGRU branch); FeedForward =
     Linear(D, F) -> GELU -> Linear(F, D) (reference mingru/minLM.py:17-23)
-    with fp32 masters; pending bf16. The forward products run on hipBLASLt
-    (torch) with torch's GELU, or with FF_FORWARD_MG_GEMM on mg_gemm (bias +
-    GELU epilogue writing pre-activation and activation in one pass, then the
-    bias epilogue); the backward products always on mg_gemm."""
+    with fp32 masters; pending bf16. Forward and backward products run on
+    mg_gemm: the first with the bias + GELU epilogue (pre-activation and
+    activation written in one pass), the second with the bias epilogue."""
 
     @staticmethod
     def forward(ctx, x1, out, w_norm, w1, b1, w2, b2):
@@ -154,14 +146,9 @@ class FFBlock(torch.autograd.Function):
         N = B * T
         x2, n2, rstd, _ = _norm_fwd(x1.reshape(N, D), out.reshape(N, D), w_norm, BF16)
         w1b, w2b = bf16_copy(w1), bf16_copy(w2)
-        if FF_FORWARD_MG_GEMM:
-            pre = torch.empty(N, w1.shape[0], dtype=BF16, device=x1.device)
-            act = gemm.linear_fwd(n2, w1b, _f32(b1), gelu_pre=pre)   # pre = n2 W1^T + b1, act = gelu(pre)
-            pend = gemm.linear_fwd(act, w2b, _f32(b2))                # act W2^T + b2
-        else:
-            pre = F.linear(n2, w1b, bf16_copy(b1))
-            act = F.gelu(pre)
-            pend = F.linear(act, w2b, bf16_copy(b2))
+        pre = torch.empty(N, w1.shape[0], dtype=BF16, device=x1.device)
+        act = gemm.linear_fwd(n2, w1b, _f32(b1), gelu_pre=pre)   # pre = n2 W1^T + b1, act = gelu(pre)
+        pend = gemm.linear_fwd(act, w2b, _f32(b2))                # act W2^T + b2
         ctx.save_for_backward(x2, w_norm, rstd, n2, pre, act, w1b, w2b)
         ctx.dims = (B, T, D)
         return x2.view(B, T, D), pend.view(B, T, D)

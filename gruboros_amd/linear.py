@@ -248,23 +248,25 @@ def linear(x, layer):
     return F.linear(x.to(w.dtype), w, b).to(x.dtype)
 
 
-# Where the GELU of the FeedForward runs (measured on MI355X in the cfg3
-# training step, 16376 rows):
-#   forward: hipBLASLt's x W1^T + b1 (94 us) and a GELU pass (43 us), against
-#     187 us for mg_gemm with the bias + GELU epilogue;
+# Where the GELU of the FeedForward runs (measured on MI355X, 16384 x 1024
+# activations, F = 4096):
+#   forward: mg_gemm with the bias + GELU epilogue (its GELU from a bf16
+#     table), 154 us, against 175 us for hipBLASLt's x W1^T + b1 and torch's
+#     GELU pass; the second product on mg_gemm too;
 #   backward: hipBLASLt's dY W2 and mg_gelu_bwd (fused with the first bias
 #     gradient), 208 us against 244 us for mg_gemm's GELU-gradient epilogue
 #     plus a column sum (that epilogue's VALU work runs after the tile's MFMA
 #     loop with nothing to overlap it).
-# Both fused forms are exact and tested; they stay off while slower.
-FUSED_GELU_FORWARD = False
+# Both fused forms are exact and tested.
+FUSED_GELU_FORWARD = True
 FUSED_GELU_BACKWARD = False
 
 
 class BF16FeedForward(torch.autograd.Function):
     """Linear -> GELU -> Linear (reference mingru/minLM.py:17-23) in bf16 with
-    fp32 weight gradients. Forward: either mg_gemm with the bias + GELU
-    epilogue (keeping bf16(x W1^T + b1) for the backward) or hipBLASLt (via
+    fp32 weight gradients. Forward: mg_gemm with the bias + GELU epilogue
+    (keeping bf16(x W1^T + b1) for the backward) and the bias epilogue, or
+    (FUSED_GELU_FORWARD off, or widths mg_gemm does not take) hipBLASLt (via
     torch) and a GELU pass. Backward: either mg_gemm's GELU-gradient
     epilogue on dY W2 or hipBLASLt's dY W2 and mg_gelu_bwd; weight gradients
     on mg_gemm, bias gradients on mg_column_sum / mg_gelu_bwd."""
@@ -277,11 +279,14 @@ class BF16FeedForward(torch.autograd.Function):
             x2 = x2.contiguous()
         if FUSED_GELU_FORWARD and gemm.fits(x2, w1b):
             pre = torch.empty(x2.shape[0], w1b.shape[0], device=x.device, dtype=torch.bfloat16)
-            h = gemm.linear_fwd(x2, w1b, b1.detach().contiguous(), gelu_pre=pre)
+            h = gemm.linear_fwd(x2, w1b, b1.detach().float().contiguous(), gelu_pre=pre)
         else:
             pre = F.linear(x2, w1b, b1b)
             h = F.gelu(pre)
-        y = F.linear(h, w2b, b2b)
+        if FUSED_GELU_FORWARD and gemm.fits(h, w2b):
+            y = gemm.linear_fwd(h, w2b, b2.detach().float().contiguous())
+        else:
+            y = F.linear(h, w2b, b2b)
         ctx.save_for_backward(x2, pre, h, w1b, w2b)
         return y.view(*shape[:-1], w2b.shape[0])
 

@@ -147,16 +147,22 @@ def test_minlm_with_dropout_eval_matches_oracle_and_train_drops():
 
 
 def test_minlm_bf16_feed_forward_forward_on_mg_gemm(monkeypatch):
-    """The FeedForward forward on mg_gemm's bias + GELU and bias epilogues
-    (blocks.FF_FORWARD_MG_GEMM) keeps the bf16 step within 2e-2 of fp64."""
-    from gruboros_amd import blocks
+    """The block path's FeedForward forward runs on mg_gemm's bias + GELU and
+    bias epilogues (torch's linear and GELU made to fail here) and keeps the
+    bf16 step within 2e-2 of fp64."""
+    import torch.nn.functional as F
 
-    monkeypatch.setattr(blocks, "FF_FORWARD_MG_GEMM", True)
+    def _no_torch(*a, **k):
+        raise AssertionError("the block path reached torch's linear or GELU")
+
     dim, depth, B, S = 64, 2, 2, 130
     m, sd = _model(dim, depth, 1.0, torch.bfloat16)
     ids = torch.randint(0, 256, (B, S), generator=torch.Generator().manual_seed(7))
-    loss = m(ids.to(DEV), return_loss=True)
-    loss.backward()
+    with monkeypatch.context() as mp:
+        mp.setattr(F, "linear", _no_torch)
+        mp.setattr(F, "gelu", _no_torch)
+        loss = m(ids.to(DEV), return_loss=True)
+        loss.backward()
     p = {k: v.double().requires_grad_(True) for k, v in sd.items()}
     ref, _ = O.minlm_forward(p, ids, depth, return_loss=True, dtype=torch.float64)
     ref.backward()
