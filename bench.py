@@ -192,57 +192,69 @@ def bench_ceilings(n=1 << 28, reps=10):
     return res
 
 
-def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64):
-    """Generation (reference generate.py:184-212) on the cfg3 model: tokens/s of
-    the per-token step, greedy sampling on the device, no host sync per token.
-    `model_call`: the drop-in model called once per token as generate.py does;
+def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64, expansion=1.0, ff_mult=4, cast=False):
+    """Generation (reference generate.py:184-212): tokens/s of the per-token step,
+    greedy sampling on the device, no host sync per token.
+    `model_call`: the drop-in model called once per token as generate.py does (its
+    one-token calls run on the decode kernels); `model_call_parallel_path`: the same
+    with minLM.decode_kernels off (the parallel forward on one position);
     `decoder_graph`: gruboros_amd.decode.Decoder (decode kernels, one HIP graph
-    replay per token). `weight_GBs`: bf16 weight bytes read per step / step time."""
+    replay per token). `weight_GBs`: bf16 weight bytes read per step / step time.
+    cast: the model's parameters cast with .to(torch.bfloat16) as generate.py:140-141
+    does; else fp32 masters with compute_dtype bf16."""
     import torch
 
     from gruboros_amd.decode import Decoder
     from gruboros_amd.mingru.minLM import minLM
 
     torch.manual_seed(0)
-    model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0,
-                  compute_dtype=torch.bfloat16).cuda().eval()
+    with torch.device("cuda"):
+        model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion,
+                      compute_dtype=None if cast else torch.bfloat16).eval()
+    if cast:
+        model = model.to(torch.bfloat16)
     wbytes = 2 * sum(p.numel() for n, p in model.named_parameters() if p.dim() == 2 and "token_emb" not in n)
-    res = {"model": f"minLM d{dim} L{depth} bf16", "steps": steps, "weight_bytes_per_step": wbytes}
+    res = {"model": f"minLM d{dim} L{depth} expansion {expansion} ff_mult {ff_mult} "
+                    f"{'cast to bf16' if cast else 'bf16 activations'}",
+           "steps": steps, "weight_bytes_per_step": wbytes}
     gen = torch.Generator(device="cuda").manual_seed(0)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, tok, n):
+        for _ in range(5):
+            tok = fn(tok)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            tok = fn(tok)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
     for B in batches:
         ids = torch.randint(0, 256, (B, prompt), device="cuda", generator=gen)
         row = {}
         with torch.no_grad():
-            # the model called once per token, as reference generate.py does
-            logits, hid = model(ids, return_prev_hiddens=True)
-            tok = logits[:, -1].argmax(-1)
-            for _ in range(5):
-                logits, hid = model(tok[:, None], return_prev_hiddens=True, prev_hiddens=hid)
-                tok = logits[:, -1].argmax(-1)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(steps):
-                logits, hid = model(tok[:, None], return_prev_hiddens=True, prev_hiddens=hid)
-                tok = logits[:, -1].argmax(-1)
-            e1.record()
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / steps
-            row["model_call"] = {"ms_per_token_step": ms, "tokens_per_s": B / (ms * 1e-3)}
+            for key, on in (("model_call", True), ("model_call_parallel_path", False)):
+                # the model called once per token, as reference generate.py does
+                model.decode_kernels = on
+                logits, hid = model(ids, return_prev_hiddens=True)
+                state = {"hid": hid}
+
+                def call(tok):
+                    logits, state["hid"] = model(tok[:, None], return_prev_hiddens=True, prev_hiddens=state["hid"])
+                    return logits[:, -1].argmax(-1)
+
+                ms = timed(call, logits[:, -1].argmax(-1), steps if on else max(steps // 4, 10))
+                row[key] = {"ms_per_token_step": ms, "tokens_per_s": B / (ms * 1e-3)}
+            model.decode_kernels = True
             dec = Decoder(model, B)
-            tok = dec.prefill(ids).argmax(-1)
-            for _ in range(5):
-                tok = dec.step(tok).argmax(-1)
-            torch.cuda.synchronize()
-            e0.record()
-            for _ in range(steps):
-                tok = dec.step(tok).argmax(-1)
-            e1.record()
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / steps
+            ms = timed(lambda tok: dec.step(tok).argmax(-1), dec.prefill(ids).argmax(-1), steps)
             row["decoder_graph"] = {"ms_per_token_step": ms, "tokens_per_s": B / (ms * 1e-3),
                                     "weight_GBs": wbytes / (ms * 1e-3) / 1e9}
         res[f"batch{B}"] = row
+    del model
+    torch.cuda.empty_cache()
     return res
 
 
@@ -475,6 +487,11 @@ def main():
     if args.only in (None, "decode"):
         dec = bench_decode()
         print(f"[bench] decode {json.dumps(dec)}", file=sys.stderr, flush=True)
+        # generate.py's own model at the reference's production run (train.cuda.sh:60-62:
+        # dim 1024, expansion 3.0, ff_mult 1.5, --params 1g -> depth 79), cast to bf16
+        dec_prod = bench_decode(steps=100, batches=(1, 8), dim=1024, depth=79, expansion=3.0, ff_mult=1.5,
+                                cast=True)
+        print(f"[bench] decode production {json.dumps(dec_prod)}", file=sys.stderr, flush=True)
     cfg5 = None
     if args.only is None and args.workload == "cfg3":
         # the ~1B-parameter configuration beside the headline: a few optimizer
@@ -545,6 +562,7 @@ def main():
         out["kernels"] = kern
     if dec:
         out["decode"] = dec
+        out["decode_production"] = dec_prod
     if ref:
         out["reference_loop"] = ref
     if cfg5:

@@ -30,6 +30,9 @@ SIGNATURES = {
     "mg_scan_fwd_noalloc_check": (_c_int, [_vp]),
     "mg_decode_mingru": (_c_int, [_c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                                   _vp]),
+    "mg_decode_mingru_expanded": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                           ctypes.c_float, _vp]),
+    "mg_decode_to_out": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_decode_ff": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
     "mg_decode_head": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
     "mg_scan_ckpt_elems": (_c_size, [_c_int, _c_int, _c_int]),

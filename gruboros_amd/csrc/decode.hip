@@ -2,28 +2,31 @@
 // fp32 residual stream and scan state: the generation loop of reference
 // generate.py:199-212, which calls minLM.forward on one token with the
 // previous hiddens (reference mingru/minLM.py:97-138; minGRU's one-step
-// path mingru/minGRU.py:45-52).
+// path mingru/minGRU.py:45-52, to_out mingru/minGRU.py:41,71).
 //
-// Per layer two launches, plus one for the head:
+// Per layer two launches (three with to_out), plus one for the head:
 //   mg_decode_mingru  x_in (+ pending) -> RMSNorm -> [hidden | gate] rows of
 //                     to_hidden_and_gate -> one recurrence step per channel
 //                     (state updated in place) -> x_out = x_in + pending + h
+//                     (expansion 1), or h -> h_out as bf16 (expansion != 1)
+//   mg_decode_to_out  h_out -> to_out rows -> x_out = x_in + pending + h W^T
 //   mg_decode_ff      RMSNorm(x) -> Linear + GELU (-> act) ; act -> Linear
 //                     -> pending (the FeedForward branch, added by the next
 //                     layer's mg_decode_mingru or by the head)
 //   mg_decode_head    x + pending -> RMSNorm -> to_logits
 // Each workgroup recomputes the RMSNorm of the B input rows (a few KiB) into
-// LDS as the bf16 vector the projection reads, then each wave produces R
-// output rows for all B inputs: lanes stride the reduction dimension in
-// 16-byte weight vectors, so the weights are read once, coalesced, and every
-// weight element is used for all B rows. The step is weight-bandwidth bound
-// (about 2 bytes per parameter per token); the launches are what a HIP graph
-// captures.
+// LDS as the bf16 vector the projection reads (or copies the B bf16 input
+// rows there), then each wave produces R output rows for all B inputs: lanes
+// stride the reduction dimension in 16-byte weight vectors, so the weights
+// are read once, coalesced, and every weight element is used for all B rows.
+// The step is weight-bandwidth bound (about 2 bytes per parameter per token);
+// the launches are what a HIP graph captures.
 //
 // Rounding follows the bf16 training path: the norm output, the projection
 // outputs, GELU's input and output and the FeedForward output are bf16
 // values; the residual stream and the scan state are fp32, and the scan
-// output joins the residual stream unrounded.
+// output joins the residual stream unrounded (expansion 1) or reaches to_out
+// as bf16, whose fp32 sum joins it unrounded.
 
 #include <algorithm>
 
@@ -37,12 +40,13 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxB = 8;
-constexpr int kLdsBytes = 64 * 1024;
+constexpr int kMaxStaged = 8192;  // longest bf16 input row a workgroup stages in LDS
 
-enum Mode { MINGRU = 0, FF1 = 1, FF2 = 2, HEAD = 3 };
+enum Mode { MINGRU = 0, FF1 = 1, FF2 = 2, HEAD = 3, TO_OUT = 4 };
 
 struct Args {
   int B, D, K, rows;             // batch, model dim, reduction length, output rows
+  int Di;                        // MINGRU: scan channels (rows Di .. 2 Di - 1 are the gates)
   int V;                         // embedding rows (tokens are clamped into [0, V))
   const int64_t* tokens;         // MINGRU of layer 0: x_in rows are emb[tokens[b]]
   const float* emb;              // [V, D]
@@ -52,8 +56,9 @@ struct Args {
   const float* norm_w;           // [D]
   const bf16_t* W;               // [rows, K] bf16
   const bf16_t* bias;            // [rows] bf16 (nullable)
-  float* state;                  // MINGRU: [B, D] fp32 recurrence state, in place
-  const bf16_t* act;             // FF2: [B, K] bf16 input
+  float* state;                  // MINGRU: [B, Di] fp32 recurrence state, in place
+  bf16_t* h_out;                 // MINGRU with to_out: the step's output h [B, Di] as bf16 (else null)
+  const bf16_t* act;             // FF2: [B, K] bf16 input; TO_OUT: h [B, Di]
   bf16_t* out;                   // FF1: act [B, F]; FF2: pending [B, D]; HEAD: logits [B, V]
   float eps;
 };
@@ -147,10 +152,14 @@ __device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
 // MODE: which step; BP: batch rows (padded); R: output rows per wave;
 // NC: 512-element chunks of the reduction a lane covers (K <= 512 NC); CPT:
 // columns per thread in the norm prologue (D <= 256 CPT; a multiple of 4, or
-// 1 where there is no norm).
+// 1 where there is no norm). The input rows are staged in a static LDS array
+// of BP x 512 NC bf16 values (at most 8 x 8192 = 128 KiB, within gfx950's
+// 160 KiB per workgroup).
 template <int MODE, int SRC, int BP, int R, int NC, int CPT>
 __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
-  extern __shared__ uint4 lds[];
+  static_assert(NC * 512 <= kMaxStaged, "staged row length");
+  constexpr bool kStagedInput = MODE == FF2 || MODE == TO_OUT;  // bf16 input rows, no norm
+  __shared__ uint4 lds[BP * NC * 64];
   bf16_t* s_in = reinterpret_cast<bf16_t*>(lds);  // [BP][K]
   __shared__ float s_part[kWaves][BP];
   __shared__ float s_rstd[BP];
@@ -163,8 +172,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
   const int g = blockIdx.x * kWaves + wave;  // row group
   int rows[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = MODE == MINGRU ? g + r * a.D : g * R + r;
-  const bool active = rows[0] < (MODE == MINGRU ? a.D : a.rows);
+  for (int r = 0; r < R; ++r) rows[r] = MODE == MINGRU ? g + r * a.Di : g * R + r;
+  const bool active = rows[0] < (MODE == MINGRU ? a.Di : a.rows);
   uint4 wv[NC][R];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -178,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     }
 
   // 1. the B input rows, as bf16, into LDS (rows B..BP-1 zero)
-  if constexpr (MODE == FF2) {
+  if constexpr (kStagedInput) {
     // kBatch 16-byte loads per thread in flight before their LDS stores (a
     // load-store pair per iteration would wait out one memory latency each)
     constexpr int kBatch = 8;
@@ -294,13 +303,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     const float hid = round_bf16(sum), gate = round_bf16(other);
     float coef, v;
     fwd_coeffs(gate, hid, coef, v);
-    float* st = a.state + static_cast<int64_t>(b) * a.D + d;
+    float* st = a.state + static_cast<int64_t>(b) * a.Di + d;
     const float h = coef * *st + v;
     *st = h;
-    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + h;
+    if (a.h_out) a.h_out[static_cast<int64_t>(b) * a.Di + d] = f32_to_bf16(h);
+    else a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + h;
     return;
   }
   if (lane % kCopies || b >= a.B) return;
+  if constexpr (MODE == TO_OUT) {
+    const int d = rows[0] + r;
+    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + sum;
+    return;
+  }
   bf16_t* o = a.out + static_cast<int64_t>(b) * a.rows + rows[0] + r;
   if constexpr (MODE == FF1) {
     *o = f32_to_bf16(gelu(round_bf16(sum + bf16_to_f32(a.bias[rows[0] + r]))));
@@ -311,40 +326,40 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
   }
 }
 
+// The staged-input modes (FF2, TO_OUT) take K <= 8192 (NC 8 up to 4096, else
+// 16); the norm modes K = D <= 2048 (NC 2 up to 1024, else 4). Every wave's
+// lane covers its chunks with K <= 512 NC, which check_shape guarantees.
 template <int MODE, int SRC, int BP, int R>
-int launch_bp(const Args& a, dim3 grid, size_t lds, hipStream_t st) {
-  if constexpr (MODE == FF2) {
-    if (a.K <= 4096) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 8, 1>), grid, dim3(kThreads), lds, st, a);
-    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 16, 1>), grid, dim3(kThreads), lds, st, a);
+int launch_bp(const Args& a, dim3 grid, hipStream_t st) {
+  if constexpr (MODE == FF2 || MODE == TO_OUT) {
+    if (a.K <= 4096) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 8, 1>), grid, dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 16, 1>), grid, dim3(kThreads), 0, st, a);
   } else {
-    if (a.K <= 1024) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 2, 4>), grid, dim3(kThreads), lds, st, a);
-    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 4, 8>), grid, dim3(kThreads), lds, st, a);
+    if (a.K <= 1024) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 2, 4>), grid, dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 4, 8>), grid, dim3(kThreads), 0, st, a);
   }
   return check_launch("mg_decode");
 }
 
 template <int MODE, int SRC, int R>
 int launch(const Args& a, hipStream_t st) {
-  const int groups = MODE == MINGRU ? a.D : a.rows / R;
+  const int groups = MODE == MINGRU ? a.Di : a.rows / R;
   const dim3 grid((groups + kWaves - 1) / kWaves);
   const int BP = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
-  const size_t lds = static_cast<size_t>(BP) * a.K * sizeof(bf16_t);
   switch (BP) {
-    case 1: return launch_bp<MODE, SRC, 1, R>(a, grid, lds, st);
-    case 2: return launch_bp<MODE, SRC, 2, R>(a, grid, lds, st);
-    case 4: return launch_bp<MODE, SRC, 4, R>(a, grid, lds, st);
-    default: return launch_bp<MODE, SRC, 8, R>(a, grid, lds, st);
+    case 1: return launch_bp<MODE, SRC, 1, R>(a, grid, st);
+    case 2: return launch_bp<MODE, SRC, 2, R>(a, grid, st);
+    case 4: return launch_bp<MODE, SRC, 4, R>(a, grid, st);
+    default: return launch_bp<MODE, SRC, 8, R>(a, grid, st);
   }
 }
 
-// kmax: 2048 for the model dimension (norm prologue), 8192 for the FeedForward width
+// kmax: 2048 for the model dimension (norm prologue), 8192 for a staged input
+// row (the FeedForward width, to_out's Di)
 inline int check_shape(const char* fn, int B, int K, int kmax) {
   if (B < 1 || B > kMaxB) return fail(MG_ERR_ARG, "%s: batch %d outside [1, %d]", fn, B, kMaxB);
   if (K < 8 || K % 8 || K > kmax)
     return fail(MG_ERR_ARG, "%s: length %d must be a positive multiple of 8, at most %d", fn, K, kmax);
-  const int BP = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
-  if (static_cast<size_t>(BP) * K * 2 > static_cast<size_t>(kLdsBytes))
-    return fail(MG_ERR_ARG, "%s: batch %d x length %d exceeds the 64 KiB input staging", fn, B, K);
   return MG_OK;
 }
 
@@ -364,13 +379,56 @@ extern "C" int mg_decode_mingru(int B, int D, const int64_t* tokens, const float
       (pending && !aligned(pending, 8)))
     return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
   decode::Args a{};
-  a.B = B; a.D = D; a.K = D; a.rows = 2 * D; a.V = V;
+  a.B = B; a.D = D; a.Di = D; a.K = D; a.rows = 2 * D; a.V = V;
   a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
   a.x_out = x_out; a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w_hg); a.state = state; a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (tokens) return decode::launch<decode::MINGRU, decode::SRC_TOKENS, 2>(a, st);
   if (pending) return decode::launch<decode::MINGRU, decode::SRC_X_PENDING, 2>(a, st);
   return decode::launch<decode::MINGRU, decode::SRC_X, 2>(a, st);
+}
+
+extern "C" int mg_decode_mingru_expanded(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                         const float* x_in, const void* pending, void* h_out, const float* norm_w,
+                                         const void* w_hg, float* state, float eps, void* stream) {
+  const char* fn = "mg_decode_mingru_expanded";
+  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
+  if (int rc = decode::check_shape(fn, B, Di, decode::kMaxStaged)) return rc;
+  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !h_out || !norm_w || !w_hg || !state)
+    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
+  if (!aligned(w_hg, 16) || !aligned(norm_w, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
+      (pending && !aligned(pending, 8)))
+    return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
+  decode::Args a{};
+  a.B = B; a.D = D; a.Di = Di; a.K = D; a.rows = 2 * Di; a.V = V;
+  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
+  a.h_out = static_cast<bf16_t*>(h_out); a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w_hg);
+  a.state = state; a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tokens) return decode::launch<decode::MINGRU, decode::SRC_TOKENS, 2>(a, st);
+  if (pending) return decode::launch<decode::MINGRU, decode::SRC_X_PENDING, 2>(a, st);
+  return decode::launch<decode::MINGRU, decode::SRC_X, 2>(a, st);
+}
+
+extern "C" int mg_decode_to_out(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                const float* x_in, const void* pending, const void* h, const void* w_out,
+                                float* x_out, void* stream) {
+  const char* fn = "mg_decode_to_out";
+  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
+  if (int rc = decode::check_shape(fn, B, Di, decode::kMaxStaged)) return rc;
+  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !h || !w_out || !x_out)
+    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
+  if (!aligned(w_out, 16) || !aligned(h, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
+      (pending && !aligned(pending, 8)))
+    return fail(MG_ERR_ARG, "%s: weight, h, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
+  decode::Args a{};
+  a.B = B; a.D = D; a.Di = Di; a.K = Di; a.rows = D; a.V = V;
+  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
+  a.act = static_cast<const bf16_t*>(h); a.W = static_cast<const bf16_t*>(w_out); a.x_out = x_out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tokens) return decode::launch<decode::TO_OUT, decode::SRC_TOKENS, 1>(a, st);
+  if (pending) return decode::launch<decode::TO_OUT, decode::SRC_X_PENDING, 1>(a, st);
+  return decode::launch<decode::TO_OUT, decode::SRC_X, 1>(a, st);
 }
 
 extern "C" int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const void* w1,

@@ -21,7 +21,7 @@ import torch.nn.functional as F
 from torch import nn
 from torch.nn import Module, ModuleList, RMSNorm
 
-from .. import blocks
+from .. import blocks, decode
 from .. import scan as scan_errors
 from ..embed import embedding
 from ..linear import feed_forward
@@ -74,7 +74,13 @@ def _ff(x, ff):
 
 
 class minLM(Module):
-    """Reference mingru/minLM.py:43-206."""
+    """Reference mingru/minLM.py:43-206.
+
+    decode_kernels: one-token calls under no_grad (the generation loop) run on the decode
+    kernels when they apply (gruboros_amd.decode.forward_one); False keeps them on the
+    parallel path."""
+
+    decode_kernels = True
 
     def __init__(
         self,
@@ -120,6 +126,13 @@ class minLM(Module):
             x, labels = x[:, :-1], x[:, 1:]
         if exists(prev_hiddens) and not return_loss:
             x = x[:, -1:]  # single-step decoding (reference :101-102; per-token ops commute with the slice)
+        if self.decode_kernels and not return_loss and x.is_cuda and x.shape[1] == 1 and \
+                not torch.is_grad_enabled():
+            # a one-token call of the generation loop (reference generate.py:199-203) runs on
+            # the decode kernels (one captured HIP graph per batch size) where they apply
+            out = decode.forward_one(self, x, prev_hiddens)
+            if out is not None:
+                return out if return_prev_hiddens else out[0]
 
         cd, accurate = self._dtypes()
         if accurate and blocks.supported(self):

@@ -446,25 +446,35 @@ int mg_embedding_bwd(const int64_t* ids, const float* dx, int64_t ldx, int64_t N
  * One-token decode step (generation), batch 1..8, bf16 weights, fp32
  * residual stream and recurrence state; replaces the per-token call of
  * minLM.forward in reference generate.py:199-212 (mingru/minLM.py:97-138 on
- * one position, minGRU's one-step path mingru/minGRU.py:45-52). Expansion
- * 1.0 (Di = D), no conv, no dropout. Per layer:
- *   mg_decode_mingru: x = (tokens ? emb[tokens] : x_in) + pending (bf16,
- *     nullable); n = bf16(RMSNorm(x) * norm_w); [hidden | gate] = bf16(n W_hg^T)
- *     (W_hg bf16 [2D, D]); state = a state + z g(hidden) (fp32 [B, D], in
- *     place); x_out = x + state. Tokens are clamped into [0, V).
+ * one position, minGRU's one-step path mingru/minGRU.py:45-52 and to_out
+ * :41,71). No conv, no dropout. Per layer:
+ *   mg_decode_mingru (expansion 1.0, Di = D): x = (tokens ? emb[tokens] :
+ *     x_in) + pending (bf16, nullable); n = bf16(RMSNorm(x) * norm_w);
+ *     [hidden | gate] = bf16(n W_hg^T) (W_hg bf16 [2D, D]); state = a state +
+ *     z g(hidden) (fp32 [B, D], in place); x_out = x + state. Tokens are
+ *     clamped into [0, V).
+ *   mg_decode_mingru_expanded (expansion != 1.0): the same with Di channels
+ *     (W_hg bf16 [2 Di, D], state fp32 [B, Di]); the step's output goes to
+ *     h_out = bf16(state) [B, Di] instead of the residual stream, then
+ *   mg_decode_to_out: x_out = x + h W_out^T (W_out bf16 [D, Di], fp32 sum),
+ *     x formed as in mg_decode_mingru from the same tokens / x_in / pending.
  *   mg_decode_ff: n = bf16(RMSNorm(x) * norm_w); act = bf16(gelu(bf16(n W1^T
  *     + b1))) (W1 bf16 [F, D], b1 bf16 [F], act bf16 [B, F] scratch);
  *     pending_out = bf16(act W2^T + b2) (W2 bf16 [D, F], b2 bf16 [D]).
  *   mg_decode_head: logits = bf16(bf16(RMSNorm(x_in + pending) * norm_w)
  *     W_out^T) (W_out bf16 [V, D], logits bf16 [B, V]).
- * RMSNorm: x / sqrt(mean(x^2) + eps). D <= 2048, F <= 8192, both multiples
- * of 8, with the batch (rounded up to 1, 2, 4 or 8) times max(D, F) bf16
- * values within 64 KiB; weights, act, x / x_in / emb and norm_w 16-byte
- * aligned, pending 8-byte aligned.
+ * RMSNorm: x / sqrt(mean(x^2) + eps). D <= 2048; F and Di <= 8192; all
+ * multiples of 8 (F also of 4 rows per wave); weights, act, h, x / x_in /
+ * emb and norm_w 16-byte aligned, pending 8-byte aligned.
  * ---------------------------------------------------------------------- */
 int mg_decode_mingru(int B, int D, const int64_t* tokens, const float* emb, int V, const float* x_in,
                      const void* pending, float* x_out, const float* norm_w, const void* w_hg,
                      float* state, float eps, void* stream);
+int mg_decode_mingru_expanded(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                              const float* x_in, const void* pending, void* h_out, const float* norm_w,
+                              const void* w_hg, float* state, float eps, void* stream);
+int mg_decode_to_out(int B, int D, int Di, const int64_t* tokens, const float* emb, int V, const float* x_in,
+                     const void* pending, const void* h, const void* w_out, float* x_out, void* stream);
 int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
                  const void* b1, void* act, const void* w2, const void* b2, void* pending_out,
                  float eps, void* stream);

@@ -151,7 +151,13 @@ def test_decode_argument_errors(L):
     # batch above 8, a dimension that is not a multiple of 8, a width over the LDS staging
     assert L.mg_decode_mingru(9, 64, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
     assert L.mg_decode_mingru(1, 60, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
-    assert L.mg_decode_ff(8, 64, 8192, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_ff(8, 64, 8200, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru_expanded(1, 64, 8200, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru_expanded(1, 64, 100, None, None, 0, 16, None, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru_expanded(1, 64, 96, None, None, 0, 16, None, None, 16, 16, 16, eps, None) == 1  # h_out
+    assert L.mg_decode_to_out(1, 64, 8200, None, None, 0, 16, None, 16, 16, 16, None) == 1
+    assert L.mg_decode_to_out(1, 64, 96, None, None, 0, 16, None, 24, 16, 16, None) == 1  # h misaligned
+    assert L.mg_decode_to_out(1, 64, 96, None, None, 0, 16, None, 16, 16, None, None) == 1  # x_out
     assert L.mg_decode_mingru(1, 64, 16, None, 256, None, None, 16, 16, 16, 16, eps, None) == 1  # no embedding
     assert L.mg_decode_head(1, 64, 0, 16, None, 16, 16, 16, eps, None) == 1
     # the norm prologue reads 16-byte groups of x / emb / norm weight and 8 bytes of pending:

@@ -26,14 +26,17 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm().clamp_min(1e-300))
 
 
-def _model(dim=256, depth=2, seed=0):
+def _model(dim=256, depth=2, seed=0, expansion=1.0, ff_mult=4):
     from gruboros_amd.mingru.minLM import minLM
 
     torch.manual_seed(seed)
-    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=1.0, compute_dtype=torch.bfloat16)
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion,
+              compute_dtype=torch.bfloat16)
     with torch.no_grad():
-        for layer in m.layers:  # non-zero second FF weights so every block contributes
+        for layer in m.layers:  # non-zero second FF (and to_out) weights so every block contributes
             layer[4][2].weight.normal_(0, 0.02)
+            if expansion != 1.0:
+                layer[2].to_out.weight.normal_(0, 1.0 / (layer[2].to_out.weight.shape[1] ** 0.5))
     return m.to(DEV).eval()
 
 
@@ -134,3 +137,88 @@ def test_decoder_matches_fp64_oracle_cfg3_shape(B):
             e_h = max(_rel(a, b) for a, b in zip(dec.hiddens(), ref_hid))
             print(f"decode vs fp64 B={B} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
             assert e_l < 2e-2 and e_h < 2e-2
+
+
+def _against_oracle(m, B, steps, tag, tol=2e-2):
+    """Decoder.prefill + Decoder.step against the fp64 restatement of the reference's
+    generation calls on m's parameters (as m computes with them): logits and per-layer
+    states within tol."""
+    from gruboros_amd.decode import Decoder
+    from oracle import mingru_oracle as O
+
+    depth = len(m.layers)
+    expansion = m.layers[0][2].to_hidden_and_gate.weight.shape[0] / (2 * m.dim)
+    sd = {k: v.detach().double().cpu() for k, v in m.state_dict().items()}
+    gen = torch.Generator(device=DEV).manual_seed(17 + B)
+    prompt = torch.randint(0, 256, (B, 13), device=DEV, generator=gen)
+    dec = Decoder(m, B)
+    with torch.no_grad():
+        last = dec.prefill(prompt)
+        ref_logits, ref_hid = O.minlm_forward(sd, prompt.cpu(), depth, return_loss=False, expansion=expansion)
+        assert _rel(last, ref_logits[:, -1]) < tol
+        for step in range(steps):
+            tok = torch.randint(0, 256, (B,), device=DEV, generator=gen)
+            got = dec.step(tok)
+            ref_logits, ref_hid = O.minlm_forward(sd, tok[:, None].cpu(), depth, return_loss=False,
+                                                  prev_hiddens=ref_hid, expansion=expansion)
+            e_l = _rel(got, ref_logits[:, -1])
+            e_h = max(_rel(a, b) for a, b in zip(dec.hiddens(), ref_hid))
+            print(f"{tag} B={B} step {step}: logits {e_l:.2e} states {e_h:.2e}", flush=True)
+            assert e_l < tol and e_h < tol
+
+
+@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("cast", [False, True], ids=["fp32_masters", "cast_bf16"])
+def test_decoder_production_ratios_match_fp64_oracle(B, cast):
+    """The reference's production widths (dim 1024, expansion 3.0, ff_mult 1.5:
+    train.cuda.sh:60-62): Di 3072 through mg_decode_mingru_expanded and
+    mg_decode_to_out, FeedForward 1536; a model with fp32 masters and
+    compute_dtype bf16, and one cast with .to(torch.bfloat16) as
+    generate.py:140-141 does (bf16 norm weights and embedding). Against the
+    fp64 restatement (mingru/minGRU.py:45-52,69-71, minLM.py:97-138)."""
+    m = _model(dim=1024, depth=3, seed=7, expansion=3.0, ff_mult=1.5)
+    if cast:
+        m = m.to(torch.bfloat16)
+    _against_oracle(m, B, 6, f"exp3 ff1.5 cast={cast}")
+
+
+def test_decoder_widest_feed_forward_at_batch_8():
+    """FeedForward width 8192 at batch 8: the second product stages 8 x 8192 bf16
+    (128 KiB) of input in LDS."""
+    m = _model(dim=1024, depth=2, seed=8, ff_mult=8)
+    with torch.no_grad():
+        for layer in m.layers:
+            layer[4][2].weight.normal_(0, 0.02 / 32)
+    _against_oracle(m, 8, 4, "ff8192")
+
+
+def test_model_calls_run_on_the_decoder():
+    """minLM.forward's one-token calls under no_grad (generate.py:199-203) return what
+    Decoder.step computes, bit for bit, with fresh hiddens per call; hiddens from
+    elsewhere (another branch of the same prompt) are copied in."""
+    from gruboros_amd import decode
+    from gruboros_amd.decode import Decoder
+
+    B = 2
+    m = _model(dim=512, depth=3, seed=9, expansion=1.5, ff_mult=1.5)
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    prompt = torch.randint(0, 256, (B, 7), device=DEV, generator=gen)
+    toks = [torch.randint(0, 256, (B,), device=DEV, generator=gen) for _ in range(4)]
+    dec = Decoder(m, B)
+    with torch.no_grad():
+        _, hid0 = m(prompt, return_prev_hiddens=True)
+        dec.prefill(prompt)
+        hid = hid0
+        for t in toks:
+            logits, hid = m(t[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+            ref = dec.step(t)
+            assert logits.shape == (B, 1, 256) and torch.equal(logits[:, 0], ref)
+            assert all(torch.equal(a.view(B, -1), b.view(B, -1)) for a, b in zip(hid, dec.hiddens()))
+        # a branch from the prompt's hiddens again: copied in, same first-step result
+        logits_b, _ = m(toks[0][:, None], return_prev_hiddens=True, prev_hiddens=hid0)
+        dec.set_hiddens(hid0)
+        assert torch.equal(logits_b[:, 0], dec.step(toks[0]))
+    assert any(isinstance(d, Decoder) for d in decode._CACHE[m].values())
+    with torch.enable_grad():  # a call that records gradients stays on the parallel path
+        m(toks[0][:, None], prev_hiddens=hid0)
+    assert sum(isinstance(d, Decoder) for d in decode._CACHE[m].values()) == 1

@@ -32,13 +32,13 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm().clamp_min(1e-300))
 
 
-def _model(dim, depth, expansion, dtype, seed=0, conv_kernel_size=None):
+def _model(dim, depth, expansion, dtype, seed=0, conv_kernel_size=None, ff_mult=4):
     from gruboros_amd.mingru.minLM import minLM
 
     torch.manual_seed(seed)
     kw = dict(enable_conv=True, conv_kernel_size=conv_kernel_size) if conv_kernel_size else {}
-    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=4, expansion=expansion, compute_dtype=dtype, **kw)
-    sd = O.make_minlm_state(256, dim, depth, ff_mult=4, expansion=expansion, seed=seed + 1,
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion, compute_dtype=dtype, **kw)
+    sd = O.make_minlm_state(256, dim, depth, ff_mult=ff_mult, expansion=expansion, seed=seed + 1,
                             conv_kernel_size=conv_kernel_size)
     gen = torch.Generator().manual_seed(seed + 2)
     for k in sd:
@@ -672,16 +672,21 @@ def test_generate_py_load_and_decode_path(cast):
     minLM from the checkpoint's model_config, load_state_dict, .eval(), cast
     the whole model (.to(torch.bfloat16) by default, .to(torch.float16) with
     --use-fp16), .to(device); then one parallel forward over the prompt with
-    return_prev_hiddens=True and single-token calls carrying prev_hiddens.
-    Checked per step against the fp64 restatement evaluated on the same cast
-    parameter values (the cast model's parameters are what it computes with):
-    logits and hiddens within 2e-2 (bf16 activations) / 5e-3 (fp16 products,
-    fp32 kernels)."""
+    return_prev_hiddens=True and single-token calls carrying prev_hiddens, at
+    the reference's production ratios (expansion 3.0, ff_mult 1.5,
+    train.cuda.sh:60-61). Checked per step against the fp64 restatement
+    evaluated on the same cast parameter values (the cast model's parameters
+    are what it computes with): logits and hiddens within 2e-2 (bf16
+    activations) / 5e-3 (fp16 products, fp32 kernels). The bf16 model's
+    one-token calls run on the decode kernels (gruboros_amd.decode), which
+    the test asserts, and hiddens a call returned keep their values after the
+    next call."""
+    from gruboros_amd import decode
     from gruboros_amd.mingru.minLM import minLM
 
-    cfg = {"num_tokens": 256, "dim": 128, "depth": 2, "ff_mult": 4.0, "expansion": 1.5, "enable_conv": False,
+    cfg = {"num_tokens": 256, "dim": 256, "depth": 2, "ff_mult": 1.5, "expansion": 3.0, "enable_conv": False,
            "dropout": 0.0}
-    _, sd = _model(128, 2, 1.5, torch.float32, seed=4)
+    _, sd = _model(256, 2, 3.0, torch.float32, seed=4, ff_mult=1.5)
     model = minLM(**cfg)
     model.load_state_dict(sd)
     model = model.eval()
@@ -692,15 +697,21 @@ def test_generate_py_load_and_decode_path(cast):
     tol = 2e-2 if cast == torch.bfloat16 else 5e-3
     with torch.no_grad():
         logits, hidden_states = model(prompt.to(DEV), return_prev_hiddens=True)
-        ref_logits, ref_hid = O.minlm_forward(p_cast, prompt, 2, return_loss=False, expansion=1.5)
+        ref_logits, ref_hid = O.minlm_forward(p_cast, prompt, 2, return_loss=False, expansion=3.0)
         assert _rel(logits[:, -1], ref_logits[:, -1]) <= tol
         prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)
+        kept = None
         for step in range(8):
             logits, hidden_states = model(prev_token, return_prev_hiddens=True, prev_hiddens=hidden_states)
             ref_logits, ref_hid = O.minlm_forward(p_cast, prev_token.cpu(), 2, return_loss=False,
-                                                  prev_hiddens=ref_hid, expansion=1.5)
+                                                  prev_hiddens=ref_hid, expansion=3.0)
             e_l = _rel(logits[:, -1], ref_logits[:, -1])
             e_h = max(_rel(a, b) for a, b in zip(hidden_states, ref_hid))
             print(f"{cast} step {step}: logits {e_l:.2e} hiddens {e_h:.2e}", flush=True)
             assert e_l <= tol and e_h <= tol
+            if kept is not None:  # the previous call's hiddens were not overwritten by this call
+                assert all(torch.equal(a, b) for a, b in zip(kept[0], kept[1]))
+            kept = (hidden_states, [h.clone() for h in hidden_states])
             prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)
+    routed = [d for d in decode._CACHE.get(model, {}).values() if isinstance(d, decode.Decoder)]
+    assert len(routed) == (1 if cast == torch.bfloat16 else 0)
