@@ -258,6 +258,38 @@ def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64, expans
     return res
 
 
+def bench_cfg1(steps=50, warmup=5):
+    """cfg1: one minGRU layer, dim 512, expansion 1.0, batch 4 x seq 1024,
+    fp32 (the reference's precision: to_hidden_and_gate on mg_gemm over three-limb bf16 splits, the fp32 scan),
+    x ~ N(0, 1), prev_hidden None; forward + backward of sum(out * dout) per step."""
+    import torch
+
+    from gruboros_amd.mingru.minGRU import minGRU
+
+    torch.manual_seed(0)
+    m = minGRU(512, 1.0).cuda()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(4, 1024, 512, device="cuda", generator=g).requires_grad_(True)
+    dout = torch.randn(4, 1024, 512, device="cuda", generator=g)
+
+    def step():
+        out = m(x)
+        out.backward(dout)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": "cfg1 minGRU layer fp32 (dim 512, expansion 1.0, B4 T1024) forward + backward",
+            "steps": steps, "ms_per_step": ms, "tokens_per_s": 4 * 1024 / (ms * 1e-3)}
+
+
 def bench_kernels(reps=20, N=8 * 2047, D=1024, F=4096, V=256):
     """Per-kernel figures at the cfg3 shapes (16,376 token rows): HBM GB/s of
     the fused norm (algorithmic bytes: fwd 12, bwd 16 per element) and the
@@ -426,7 +458,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode", "ceilings"], default=None)
+    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode", "ceilings", "cfg1"], default=None)
     ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
                     help="training workload for `value`: cfg3 (the BASELINE metric, default) or cfg5 "
                          "(~1B params: d2048 L24, batch 4 x seq 4096, gradient accumulation 4)")
@@ -492,6 +524,10 @@ def main():
         dec_prod = bench_decode(steps=100, batches=(1, 8), dim=1024, depth=79, expansion=3.0, ff_mult=1.5,
                                 cast=True)
         print(f"[bench] decode production {json.dumps(dec_prod)}", file=sys.stderr, flush=True)
+    cfg1 = None
+    if args.only in (None, "cfg1"):
+        cfg1 = bench_cfg1()
+        print(f"[bench] cfg1 {json.dumps(cfg1)}", file=sys.stderr, flush=True)
     cfg5 = None
     if args.only is None and args.workload == "cfg3":
         # the ~1B-parameter configuration beside the headline: a few optimizer
@@ -565,6 +601,8 @@ def main():
         out["decode_production"] = dec_prod
     if ref:
         out["reference_loop"] = ref
+    if cfg1:
+        out["cfg1"] = cfg1
     if cfg5:
         out["cfg5"] = cfg5
     if cpu:

@@ -47,6 +47,7 @@ SIGNATURES = {
     "mg_add_rmsnorm_fwd": (_c_int, [_fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _vp, _c_i64, _fp, _c_i64, _c_int,
                                     ctypes.c_float, _vp]),
     "mg_split_hilo": (_c_int, [_fp, _c_i64, _c_i64, _c_int, _vp, _c_i64, _vp]),
+    "mg_split_limbs": (_c_int, [_fp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp]),
     "mg_round_bf16_sr": (_c_int, [_fp, _c_i64, _vp, ctypes.c_uint32, _vp]),
     "mg_add_rmsnorm_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_add_rmsnorm_bwd": (_c_int, [_fp, _fp, _fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int, _vp,

@@ -27,6 +27,46 @@ __global__ __launch_bounds__(256) void split_hilo_kernel(const float* __restrict
   }
 }
 
+// fp32 -> three bf16 limbs h = bf16(x), m = bf16(x - h), l = bf16(x - h - m)
+// (each difference is exact in fp32, so h + m + l == x wherever l stays a
+// normal bf16 value), written as nseg segments, segment s holding limb
+// (pattern >> 2s) & 3 (0 h, 1 m, 2 l). stack_rows 0: segments side by side
+// along the columns, out[r, s cols + c] (K-contiguous operands); 1: stacked
+// along the rows, out[s rows + r, c] (MN-contiguous operands). Two operands
+// split with the patterns (h, m, h, m, l, h) and (h, h, m, m, h, l) make one
+// plain bf16 product over 6K the sum of the six limb products down to
+// 2^-16 relative (hh, mh, hm, mm, lh, hl): fp32 accuracy on MFMA.
+__global__ __launch_bounds__(256) void split_limbs_kernel(const float* __restrict__ x, int64_t ldx, int64_t rows,
+                                                          int cols, int pattern, int nseg, int stack_rows,
+                                                          bf16_t* __restrict__ out, int64_t ldo) {
+  const int q = cols / 4;
+  const int64_t n = rows * q;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / q;
+    const int c = static_cast<int>(i - r * q) * 4;
+    const f4 v = io4<float>::load(x + r * ldx + c);
+    f4 limb[3];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float h = bf16_to_f32(f32_to_bf16(v.v[j]));
+      const float r1 = v.v[j] - h;
+      const float m = bf16_to_f32(f32_to_bf16(r1));
+      limb[0].v[j] = h;
+      limb[1].v[j] = m;
+      limb[2].v[j] = r1 - m;  // rounded to bf16 by the store
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s >= nseg) break;
+      const int which = (pattern >> (2 * s)) & 3;
+      const f4 w = which == 0 ? limb[0] : which == 1 ? limb[1] : limb[2];
+      bf16_t* o = stack_rows ? out + (s * rows + r) * ldo + c : out + r * ldo + static_cast<int64_t>(s) * cols + c;
+      io4<bf16_t>::store(o, w);
+    }
+  }
+}
+
 // fp32 -> bf16 with stochastic rounding (gradients entering a bf16 product).
 __global__ __launch_bounds__(256) void round_sr_kernel(const float* __restrict__ x, int64_t n4, bf16_t* __restrict__ out,
                                                        uint32_t salt) {
@@ -54,6 +94,26 @@ extern "C" int mg_split_hilo(const float* x, int64_t ldx, int64_t rows, int cols
   const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
   hipLaunchKernelGGL(convert::split_hilo_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, ldx,
                      rows, cols, static_cast<bf16_t*>(out), ldo);
+  return check_launch(fn);
+}
+
+extern "C" int mg_split_limbs(const float* x, int64_t ldx, int64_t rows, int cols, int pattern, int nseg,
+                              int stack_rows, void* out, int64_t ldo, void* stream) {
+  const char* fn = "mg_split_limbs";
+  if (!x || !out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (rows < 0 || cols < 0 || cols % 4) return fail(MG_ERR_ARG, "%s: bad shape rows=%lld cols=%d (cols %% 4 == 0)", fn,
+                                                   (long long)rows, cols);
+  if (nseg < 1 || nseg > 8) return fail(MG_ERR_ARG, "%s: nseg %d outside [1, 8]", fn, nseg);
+  for (int s = 0; s < nseg; ++s)
+    if (((pattern >> (2 * s)) & 3) == 3) return fail(MG_ERR_ARG, "%s: pattern names limb 3 at segment %d", fn, s);
+  if (ldx < cols || ldx % 4 || ldo % 4 || ldo < (stack_rows ? cols : static_cast<int64_t>(nseg) * cols))
+    return fail(MG_ERR_ARG, "%s: bad strides ldx=%lld ldo=%lld", fn, (long long)ldx, (long long)ldo);
+  if (!aligned(x, 16) || !aligned(out, 8)) return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  if (rows == 0 || cols == 0) return MG_OK;
+  const int64_t n = rows * (cols / 4);
+  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(convert::split_limbs_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                     ldx, rows, cols, pattern, nseg, stack_rows ? 1 : 0, static_cast<bf16_t*>(out), ldo);
   return check_launch(fn);
 }
 

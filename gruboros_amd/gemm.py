@@ -130,14 +130,32 @@ def round_bf16_sr(x, salt=0x3c1d):
     return out
 
 
-def linear_fwd_hilo(x_pair, w_pair, out, K):
-    """out[N, O] = x w^T to fp32 accuracy from hi/lo pairs: x_pair [N, 2K], w_pair [O, 2K] (bf16);
-    out bf16 or fp32, any row stride."""
+def linear_fwd_hilo(x_pair, w_pair, out, K, bias=None):
+    """out[N, O] = x w^T (+ bias, fp32 [O]) to fp32 accuracy from hi/lo pairs: x_pair [N, 2K],
+    w_pair [O, 2K] (bf16); out bf16 or fp32, any row stride."""
     n, o = x_pair.shape[0], w_pair.shape[0]
     step = _row_step(n, 2 * x_pair.stride(0), out.stride(0) * out.element_size())
     for r0 in range(0, n, step):
         r1 = min(n, r0 + step)
-        gemm(x_pair[r0:r1], KCONTIG, w_pair, KCONTIG, r1 - r0, o, K, out[r0:r1], hilo=True)
+        gemm(x_pair[r0:r1], KCONTIG, w_pair, KCONTIG, r1 - r0, o, K, out[r0:r1], hilo=True,
+             epilogue=EPI_BIAS if bias is not None else EPI_NONE, bias=bias)
+    return out
+
+
+# limb patterns of mg_split_limbs (2 bits per segment: 0 h, 1 m, 2 l): a product of an operand
+# split with LIMBS_A and one split with LIMBS_B over the 6-fold K sums hh + mh + hm + mm + lh + hl
+LIMBS_A = 0 | 1 << 2 | 0 << 4 | 1 << 6 | 2 << 8 | 0 << 10   # h m h m l h
+LIMBS_B = 0 | 0 << 2 | 1 << 4 | 1 << 6 | 0 << 8 | 2 << 10   # h h m m h l
+
+
+def split_limbs(x, pattern, stack_rows):
+    """fp32 x [rows, cols] (unit inner stride) -> its six bf16 limb segments (mg_split_limbs):
+    [rows, 6 cols] side by side (stack_rows False: a K-contiguous operand over 6 cols) or
+    [6 rows, cols] stacked (stack_rows True: an MN-contiguous operand over 6 rows)."""
+    rows, cols = x.shape
+    out = torch.empty((6 * rows, cols) if stack_rows else (rows, 6 * cols), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.lib().mg_split_limbs(_lib.ptr(x), _rows(x, "x"), rows, cols, pattern, 6, int(stack_rows),
+                                         _lib.ptr(out), out.stride(0), _lib.stream_of(x)), "mg_split_limbs")
     return out
 
 

@@ -10,7 +10,9 @@ a bf16 copy next to its fp32 master:
     gossip/evolutionary_node.py:267-296, optimizer.eval()/train());
   * the backward produces the weight gradient directly in fp32 (bf16 x bf16
     GEMM with fp32 output), so no cast of the gradient either.
-With fp32 activations this is plain F.linear.
+With fp32 activations and fp32 weights (the reference's own precision: an
+unchanged train.py, cfg1's single layer) every product runs on mg_gemm over
+three-limb bf16 splits, fp32-accurate on MFMA: F32Linear.
 
 Two products are computed to fp32 accuracy from bf16 hi/lo pairs (mg_gemm
 HILO: A_hi B_hi + A_lo B_hi + A_hi B_lo on MFMA): the hidden half of
@@ -211,6 +213,56 @@ def accurate_linear_f32(x, layer):
     return y.view(*shape[:-1], w.shape[0])
 
 
+class F32Linear(torch.autograd.Function):
+    """y = x W^T (+ b) for fp32 x [N, K] and fp32 W [O, K] (reference nn.Linear in fp32:
+    mingru/minGRU.py:40-41,45,71; minLM.py:17-23,75,138), all three products on MFMA to
+    fp32 accuracy: each fp32 operand is split into three bf16 limbs (h + m + l == x,
+    mg_split_limbs) and one plain bf16 product over the 6-fold reduction sums the six limb
+    products through 2^-16 (hh, mh, hm, mm, lh, hl; the dropped ones are below 2^-24).
+    Forward y = x W^T (+ b in the epilogue); backward dx = dy W (dy's limbs side by side,
+    W's stacked), dW = dy^T x (both stacked along the rows, so no transposes and no
+    padding), db = column sums of dy. The limbs are formed per call, so nothing cached can
+    go stale when W changes.
+    (Two limbs, x = hi + lo to 2^-16, are not enough here: the reference's g(x) has a kink
+    at 0, and at cfg1's size a 4e-6 product error moves ~10 hidden pre-activations across
+    it, 8e-4 on dx and dW.)"""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        y = gemm.linear_fwd(gemm.split_limbs(x, gemm.LIMBS_A, False), gemm.split_limbs(w.detach(), gemm.LIMBS_B, False),
+                            b.detach().contiguous() if b is not None else None, out_dtype=torch.float32)
+        ctx.save_for_backward(x, w)
+        ctx.has_bias = b is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dy = dy.contiguous()
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = gemm.linear_dx(gemm.split_limbs(dy, gemm.LIMBS_A, False), gemm.split_limbs(w.detach(), gemm.LIMBS_B, True),
+                                out_dtype=torch.float32)
+        if ctx.needs_input_grad[1]:
+            dw = gemm.linear_dw(gemm.split_limbs(dy, gemm.LIMBS_A, True), gemm.split_limbs(x, gemm.LIMBS_B, True))
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = column_sum(dy)
+        return dx, dw, db
+
+
+def f32_linear_applies(x, w):
+    """Whether F32Linear takes x [.., K] and w [O, K]: fp32 CUDA tensors, O and K multiples of 8."""
+    return x.is_cuda and x.dtype == torch.float32 and w.dtype == torch.float32 and w.dim() == 2 and \
+        w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0
+
+
+def f32_linear(x, w, b=None):
+    """x W^T (+ b) for fp32 x and W on F32Linear, x of any leading shape."""
+    shape = x.shape
+    y = F32Linear.apply(x.reshape(-1, shape[-1]).contiguous(), w, b)
+    return y.view(*shape[:-1], w.shape[0])
+
+
 class BF16Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, b, wb):
@@ -237,11 +289,15 @@ class BF16Linear(torch.autograd.Function):
 
 
 def linear(x, layer):
-    """layer(x) in x's dtype: same dtypes -> F.linear; bf16 activations over fp32 masters ->
-    BF16Linear over the cached bf16 weight; parameters in another dtype (a model cast to
-    float16) -> the product in the parameters' dtype, the result back in x's."""
+    """layer(x) in x's dtype: fp32 activations and weights on the GPU -> F32Linear (mg_gemm
+    hi/lo, fp32-accurate); other equal dtypes, or widths F32Linear does not take -> F.linear;
+    bf16 activations over fp32 masters -> BF16Linear over the cached bf16 weight; parameters
+    in another dtype (a model cast to float16) -> the product in the parameters' dtype, the
+    result back in x's."""
     w, b = layer.weight, layer.bias
     if x.dtype == w.dtype:
+        if f32_linear_applies(x, w):
+            return f32_linear(x, w, b)
         return F.linear(x, w, b)
     if x.dtype == torch.bfloat16 and w.dtype == torch.float32:
         return BF16Linear.apply(x, w, b, bf16_copy(w))
@@ -314,7 +370,7 @@ def feed_forward(x, ff):
     """ff = nn.Sequential(Linear, GELU, Linear) applied to x in x's dtype."""
     l1, l2 = ff[0], ff[2]
     if x.dtype == l1.weight.dtype:
-        return l2(F.gelu(l1(x)))
+        return linear(F.gelu(linear(x, l1)), l2)
     if x.dtype != torch.bfloat16 or l1.weight.dtype != torch.float32:
         return l2(F.gelu(l1(x.to(l1.weight.dtype)))).to(x.dtype)  # parameters cast to another dtype
     if l1.bias is None or l2.bias is None:

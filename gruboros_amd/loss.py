@@ -9,7 +9,7 @@ import torch
 
 from . import gemm
 from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
-from .linear import _mm_f32, bf16_copy
+from .linear import _mm_f32, bf16_copy, f32_linear, f32_linear_applies
 
 
 def _ce(logits2d, labels1d, grad_dtype):
@@ -79,5 +79,8 @@ def logits_cross_entropy(embed, to_logits, labels):
     w = to_logits.weight
     if embed.dtype == torch.bfloat16 and w.dtype == torch.float32:
         return LogitsCrossEntropy.apply(e2.contiguous(), w, bf16_copy(w), lab)
-    logits = torch.nn.functional.linear(e2.to(w.dtype), w)  # (parameters cast to another dtype: product in it)
+    if f32_linear_applies(e2, w):
+        logits = f32_linear(e2, w)  # the fp32 path: the logits product on mg_gemm over bf16 limbs
+    else:
+        logits = torch.nn.functional.linear(e2.to(w.dtype), w)  # (parameters cast to another dtype: product in it)
     return CrossEntropyFromLogits.apply(logits.float().contiguous(), lab)

@@ -378,6 +378,22 @@ size_t mg_gemm_wgrad_pair_workspace_bytes(int M0, int N0, int M1, int N1, int K,
  * the operands of the accurate forms of reference mingru/minGRU.py:45 and :71. */
 int mg_split_hilo(const float* x, int64_t ldx, int64_t rows, int cols, void* out, int64_t ldo, void* stream);
 
+/* fp32 -> three bf16 limbs per value: h = bf16(x), m = bf16(x - h), l =
+ * bf16(x - h - m) (h + m + l == x; the differences are exact in fp32),
+ * written as nseg (1..8) segments, segment s holding limb (pattern >> 2s) & 3
+ * (0 h, 1 m, 2 l). stack_rows 0: the segments side by side along the
+ * columns, out[r, s cols + c] (ldo >= nseg cols), the form of a K-contiguous
+ * operand whose K grows nseg-fold; 1: stacked along the rows, out[s rows + r,
+ * c] (ldo >= cols), the form of an MN-contiguous one. Operands split with the
+ * patterns (h, m, h, m, l, h) and (h, h, m, m, h, l) make one plain mg_gemm
+ * product over 6K equal to the fp32 product to ~2^-24 relative (the six limb
+ * products through 2^-16). rows x cols with cols % 4 == 0; ldx, ldo % 4 == 0;
+ * x 16-byte and out 8-byte aligned. No reference counterpart: it prepares
+ * the operands of the fp32 nn.Linear products (reference mingru/minGRU.py:45,
+ * :71, mingru/minLM.py:17-23, :138 in fp32). */
+int mg_split_limbs(const float* x, int64_t ldx, int64_t rows, int cols, int pattern, int nseg, int stack_rows,
+                   void* out, int64_t ldo, void* stream);
+
 /* fp32 -> bf16 with stochastic rounding (as the gradient stores, keyed by the
  * element index and `salt`), n % 4 == 0 dense elements; x 16-byte and out
  * 8-byte aligned. For an fp32 gradient that must enter a bf16 product (the

@@ -567,3 +567,58 @@ def test_wgrad_pair_matches_fp64_and_single_products(shapes, K, paired, strided)
     d0, d1 = linear_dw_pair(dy0, x0, dy1, x1, deterministic=True)
     assert torch.equal(d0, linear_dw(dy0, x0, deterministic=True))
     assert torch.equal(d1, linear_dw(dy1, x1, deterministic=True))
+
+
+def test_split_limbs_reconstructs_fp32_exactly():
+    """mg_split_limbs: h + m + l == x for fp32 values over a wide range of magnitudes (the
+    differences x - h and x - h - m are exact in fp32), each limb a bf16 value, in both
+    segment layouts and for both patterns."""
+    from gruboros_amd import gemm
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 96, generator=g) * torch.exp2(torch.randint(-60, 60, (64, 96), generator=g).float())
+    xd = x.to(DEV)
+    for pattern, order in ((gemm.LIMBS_A, (0, 1, 0, 1, 2, 0)), (gemm.LIMBS_B, (0, 0, 1, 1, 0, 2))):
+        side = gemm.split_limbs(xd, pattern, False).float().cpu().view(64, 6, 96)
+        stack = gemm.split_limbs(xd, pattern, True).float().cpu().view(6, 64, 96)
+        assert torch.equal(side.transpose(0, 1), stack)
+        limbs = {}
+        for s, which in enumerate(order):
+            if which in limbs:
+                assert torch.equal(limbs[which], stack[s])
+            limbs[which] = stack[s]
+        h, m, l = limbs[0], limbs[1], limbs[2]
+        assert torch.equal(h, x.to(torch.bfloat16).float())
+        assert torch.equal(h.double() + m.double() + l.double(), x.double())
+
+
+@pytest.mark.parametrize("N,K,O,bias", [(4096, 512, 1024, False), (4092, 1024, 256, False), (37, 64, 200, True),
+                                        (1000, 1536, 1024, True)])
+def test_f32_linear_matches_fp64(N, K, O, bias):
+    """F32Linear (the fp32 path's nn.Linear, reference mingru/minGRU.py:45,71 and minLM.py:17-23,
+    :138 in fp32) against float64 for the output and the x, W and bias gradients: all three
+    products on mg_gemm over three-limb bf16 splits, fp32-accurate (within 2e-6,
+    norm-relative: an fp32 product's accumulation error at these K). N = 4092 and 37 put the
+    weight gradient's reduction off a multiple of 8; (4096, 512, 1024) is cfg1's
+    to_hidden_and_gate."""
+    from gruboros_amd.linear import f32_linear
+
+    g = torch.Generator().manual_seed(N + K + O)
+    x = torch.randn(N, K, generator=g, dtype=torch.float64)
+    w = torch.randn(O, K, generator=g, dtype=torch.float64) / K ** 0.5
+    b = torch.randn(O, generator=g, dtype=torch.float64) if bias else None
+    dy = torch.randn(N, O, generator=g, dtype=torch.float64)
+    xd = x.float().to(DEV).requires_grad_(True)
+    wd = w.float().to(DEV).requires_grad_(True)
+    bd = b.float().to(DEV).requires_grad_(True) if bias else None
+    y = f32_linear(xd, wd, bd)
+    y.backward(dy.float().to(DEV))
+    xr, wr = x.float().double().requires_grad_(True), w.float().double().requires_grad_(True)
+    br = b.float().double().requires_grad_(True) if bias else None
+    yr = torch.nn.functional.linear(xr, wr, br)
+    yr.backward(dy.float().double())
+    errs = {"y": _rel(y, yr), "dx": _rel(xd.grad, xr.grad), "dW": _rel(wd.grad, wr.grad)}
+    if bias:
+        errs["db"] = _rel(bd.grad, br.grad)
+    print(f"f32_linear N={N} K={K} O={O}", {k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
+    assert all(v <= 2e-6 for v in errs.values()), errs
