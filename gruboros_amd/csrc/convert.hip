@@ -36,19 +36,23 @@ __global__ __launch_bounds__(256) void split_hilo_kernel(const float* __restrict
 // split with the patterns (h, m, h, m, l, h) and (h, h, m, m, h, l) make one
 // plain bf16 product over 6K the sum of the six limb products down to
 // 2^-16 relative (hh, mh, hm, mm, lh, hl): fp32 accuracy on MFMA.
-__global__ __launch_bounds__(256) void split_limbs_kernel(const float* __restrict__ x, int64_t ldx, int64_t rows,
+// V values per thread (8 where cols % 8 == 0 and out is 16-byte aligned: one
+// 16-byte store per segment; else 4); IDX: the index type (32-bit where the
+// thread count allows).
+template <int V, typename IDX>
+__global__ __launch_bounds__(256) void split_limbs_kernel(const float* __restrict__ x, int64_t ldx, IDX rows,
                                                           int cols, int pattern, int nseg, int stack_rows,
                                                           bf16_t* __restrict__ out, int64_t ldo) {
-  const int q = cols / 4;
-  const int64_t n = rows * q;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t r = i / q;
-    const int c = static_cast<int>(i - r * q) * 4;
-    const f4 v = io4<float>::load(x + r * ldx + c);
-    f4 limb[3];
+  const IDX q = cols / V;
+  const IDX n = rows * q;
+  for (IDX i = blockIdx.x * static_cast<IDX>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<IDX>(gridDim.x) * blockDim.x) {
+    const IDX r = i / q;
+    const int c = static_cast<int>(i - r * q) * V;
+    const fv<V> v = iov<float, V>::load(x + static_cast<int64_t>(r) * ldx + c);
+    fv<V> limb[3];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < V; ++j) {
       const float h = bf16_to_f32(f32_to_bf16(v.v[j]));
       const float r1 = v.v[j] - h;
       const float m = bf16_to_f32(f32_to_bf16(r1));
@@ -60,9 +64,10 @@ __global__ __launch_bounds__(256) void split_limbs_kernel(const float* __restric
     for (int s = 0; s < 8; ++s) {
       if (s >= nseg) break;
       const int which = (pattern >> (2 * s)) & 3;
-      const f4 w = which == 0 ? limb[0] : which == 1 ? limb[1] : limb[2];
-      bf16_t* o = stack_rows ? out + (s * rows + r) * ldo + c : out + r * ldo + static_cast<int64_t>(s) * cols + c;
-      io4<bf16_t>::store(o, w);
+      const fv<V> w = which == 0 ? limb[0] : which == 1 ? limb[1] : limb[2];
+      bf16_t* o = stack_rows ? out + (static_cast<int64_t>(s) * rows + r) * ldo + c
+                             : out + static_cast<int64_t>(r) * ldo + static_cast<int64_t>(s) * cols + c;
+      iov<bf16_t, V>::store(o, w);
     }
   }
 }
@@ -110,10 +115,20 @@ extern "C" int mg_split_limbs(const float* x, int64_t ldx, int64_t rows, int col
     return fail(MG_ERR_ARG, "%s: bad strides ldx=%lld ldo=%lld", fn, (long long)ldx, (long long)ldo);
   if (!aligned(x, 16) || !aligned(out, 8)) return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
   if (rows == 0 || cols == 0) return MG_OK;
-  const int64_t n = rows * (cols / 4);
-  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
-  hipLaunchKernelGGL(convert::split_limbs_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x,
-                     ldx, rows, cols, pattern, nseg, stack_rows ? 1 : 0, static_cast<bf16_t*>(out), ldo);
+  const bool wide = cols % 8 == 0 && ldo % 8 == 0 && aligned(out, 16);
+  const int64_t n = rows * (cols / (wide ? 8 : 4));
+  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 8192));
+  const int sr = stack_rows ? 1 : 0;
+  bf16_t* o = static_cast<bf16_t*>(out);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n + 256LL * blocks < (int64_t(1) << 31)) {  // every thread index fits in 32 bits
+    const int r32 = static_cast<int>(rows);
+    if (wide) hipLaunchKernelGGL((convert::split_limbs_kernel<8, int>), dim3(blocks), dim3(256), 0, st, x, ldx, r32, cols, pattern, nseg, sr, o, ldo);
+    else hipLaunchKernelGGL((convert::split_limbs_kernel<4, int>), dim3(blocks), dim3(256), 0, st, x, ldx, r32, cols, pattern, nseg, sr, o, ldo);
+  } else {
+    if (wide) hipLaunchKernelGGL((convert::split_limbs_kernel<8, int64_t>), dim3(blocks), dim3(256), 0, st, x, ldx, rows, cols, pattern, nseg, sr, o, ldo);
+    else hipLaunchKernelGGL((convert::split_limbs_kernel<4, int64_t>), dim3(blocks), dim3(256), 0, st, x, ldx, rows, cols, pattern, nseg, sr, o, ldo);
+  }
   return check_launch(fn);
 }
 

@@ -590,6 +590,10 @@ def test_split_limbs_reconstructs_fp32_exactly():
         h, m, l = limbs[0], limbs[1], limbs[2]
         assert torch.equal(h, x.to(torch.bfloat16).float())
         assert torch.equal(h.double() + m.double() + l.double(), x.double())
+    # four values per thread (cols % 8 != 0)
+    y = torch.randn(5, 20, generator=g)
+    side = gemm.split_limbs(y.to(DEV), gemm.LIMBS_B, False).float().cpu().view(5, 6, 20)
+    assert torch.equal(side[:, 0] + side[:, 2] + side[:, 5], y)
 
 
 @pytest.mark.parametrize("N,K,O,bias", [(4096, 512, 1024, False), (4092, 1024, 256, False), (37, 64, 200, True),
