@@ -39,6 +39,8 @@ SIGNATURES = {
     "mg_scan_fwd_noalloc_max_bytes": (_c_size, []),
     "mg_scan_fwd_noalloc": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
                                      _c_int, _c_int, _c_int, _vp]),
+    "mg_scan_fwd_residual": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _fp, _fp, _c_i64, _c_i64, _fp, _fp,
+                                      _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
     "mg_scan_fwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,
                              _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
     "mg_scan_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp,

@@ -10,8 +10,10 @@ activations over fp32 master weights):
 
   MinGRUBlock   x1 = x + pending; n = RMSNorm(x1) as a hi/lo pair;
                 hg = [n W_h^T (fp32-accurate) | n W_g^T]; h = scan(hg) in fp32;
-                out = h, or to_out(h) (fp32-accurate) when expansion != 1.
-  FFBlock       x2 = x1 + out; n2 = RMSNorm(x2); pending = FeedForward(n2) (bf16).
+                expansion 1: the scan writes x2 = x1 + h itself (h is kept only as
+                fp32 checkpoints); else out = to_out(h) (fp32-accurate).
+  FFBlock       x2 = x1 + out (or x2 as given); n2 = RMSNorm(x2);
+                pending = FeedForward(n2) (bf16).
   FinalNormCE   embed = RMSNorm(x + pending); mean cross-entropy of
                 embed W_out^T (streaming loss kernel).
 
@@ -36,6 +38,7 @@ from .norm import _bwd as _norm_bwd
 from .norm import _fwd as _norm_fwd
 from .scan import _launch_bwd as _scan_bwd
 from .scan import _launch_fwd as _scan_fwd
+from .scan import _launch_fwd_residual as _scan_fwd_res
 
 BF16 = torch.bfloat16
 
@@ -44,6 +47,11 @@ BF16 = torch.bfloat16
 # to_hidden_and_gate's (expansion != 1).
 FF_DW_PAIR = True
 
+# At expansion 1 the scan adds its state to the residual stream itself
+# (mg_scan_fwd_residual) and keeps h only as fp32 checkpoints for the backward;
+# False: the scan writes h and the FeedForward's norm adds it.
+SCAN_RESIDUAL = True
+
 
 def _f32(b):
     """A bias as the fp32 contiguous vector the GEMM epilogue adds."""
@@ -51,12 +59,14 @@ def _f32(b):
 
 
 class MinGRUBlock(torch.autograd.Function):
-    """(x, pending) -> (x1 = x + pending, out, h_last); see the module docstring.
+    """(x, pending) -> (x_next, out, h_last); see the module docstring.
 
     x: fp32 [B, T, D] residual stream; pending: bf16 [B, T, D] (the previous
     FeedForward's output, not yet added) or None; w_norm fp32 [D]; w_hg fp32
     master [2 Di, D]; h0 fp32 [B, Di] or None; w_to fp32 master [D, Di] or None.
-    out: fp32 [B, T, Di] (h) or [B, T, D] (to_out(h)); h_last fp32 [B, 1, Di]."""
+    Without to_out (expansion 1): x_next = x + pending + h (the scan adds its
+    state to the residual stream) and out is None. With it: x_next = x + pending
+    and out = to_out(h), fp32 [B, T, D]. h_last fp32 [B, 1, Di]."""
 
     @staticmethod
     def forward(ctx, x, pending, w_norm, w_hg, h0, w_to):
@@ -72,6 +82,14 @@ class MinGRUBlock(torch.autograd.Function):
         gemm.linear_fwd_hilo(pair, whp[:Di], hg[:, :Di], D)                    # minGRU.py:45, hidden half
         gemm.gemm(n, gemm.KCONTIG, whb[Di:], gemm.KCONTIG, N, Di, D, hg[:, Di:])  # gate half
         hg3 = hg.view(B, T, 2 * Di)
+        if w_to is None and SCAN_RESIDUAL:
+            # minGRU.py:47-69 and the residual add of minLM.py:125 in one pass; the
+            # backward rebuilds h from the fp32 checkpoints
+            x2, h_last, ckpt = _scan_fwd_res(hg3[..., :Di], hg3[..., Di:], h0, xn.view(B, T, D))
+            ctx.save_for_backward(xn, w_norm, rstd, pair, hg, None, h0, whb, ckpt)
+            ctx.dims = (B, T, D, Di)
+            ctx.has_pending, ctx.has_to, ctx.res = pending is not None, False, True
+            return x2, None, h_last
         h, h_last, _ = _scan_fwd(hg3[..., :Di], hg3[..., Di:], h0, torch.float32)   # minGRU.py:47-69
         saved = [xn, w_norm, rstd, pair, hg, h, h0, whb]
         if w_to is not None:                                                   # minGRU.py:71
@@ -84,7 +102,7 @@ class MinGRUBlock(torch.autograd.Function):
             out = h
         ctx.save_for_backward(*saved)
         ctx.dims = (B, T, D, Di)
-        ctx.has_pending, ctx.has_to = pending is not None, w_to is not None
+        ctx.has_pending, ctx.has_to, ctx.res = pending is not None, w_to is not None, False
         x1 = x_out.view(B, T, D) if x_out is not None else x.view_as(x)
         return x1, out, h_last
 
@@ -94,9 +112,14 @@ class MinGRUBlock(torch.autograd.Function):
         N = B * T
         saved = ctx.saved_tensors
         xn, w_norm, rstd, pair, hg, h, h0, whb = saved[:8]
+        ckpt = None
         dev = xn.device
         dW_to = None
-        if dout is None:
+        if ctx.res:
+            # x_next = x1 + h: h and the residual get the same gradient
+            ckpt = saved[8]
+            dh = dx1
+        elif dout is None:
             dh = None
         elif ctx.has_to:
             h_pair, wtb = saved[8:10]
@@ -113,7 +136,7 @@ class MinGRUBlock(torch.autograd.Function):
             dhg.zero_()
             dh0 = torch.zeros_like(h0) if want_dh0 else None
         else:
-            dh0 = _scan_bwd(hg3[..., :Di], hg3[..., Di:], h0, h, None, dh, dh_last, dhg3[..., :Di], dhg3[..., Di:],
+            dh0 = _scan_bwd(hg3[..., :Di], hg3[..., Di:], h0, h, ckpt, dh, dh_last, dhg3[..., :Di], dhg3[..., Di:],
                             want_dh0)
         dn = gemm.linear_dx(dhg, whb, stochastic=True)             # bf16, stochastically rounded
         dW_hg = None
@@ -133,7 +156,8 @@ class MinGRUBlock(torch.autograd.Function):
 class FFBlock(torch.autograd.Function):
     """(x1, out) -> (x2 = x1 + out, pending = FeedForward(RMSNorm(x2))).
 
-    x1 fp32 [B, T, D]; out fp32 [B, T, D] (the minGRU branch); FeedForward =
+    x1 fp32 [B, T, D]; out fp32 [B, T, D] (the minGRU branch), or None when
+    x1 already holds it (then x2 is x1, returned as is); FeedForward =
     Linear(D, F) -> GELU -> Linear(F, D) (reference mingru/minLM.py:17-23)
     with fp32 masters; pending bf16. Forward and backward products run on
     mg_gemm: the first with the bias + GELU epilogue (pre-activation and
@@ -144,14 +168,17 @@ class FFBlock(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         B, T, D = x1.shape
         N = B * T
-        x2, n2, rstd, _ = _norm_fwd(x1.reshape(N, D), out.reshape(N, D), w_norm, BF16)
+        x2, n2, rstd, _ = _norm_fwd(x1.reshape(N, D), out.reshape(N, D) if out is not None else None, w_norm, BF16)
+        ctx.has_out = out is not None
+        if x2 is None:
+            x2 = x1.reshape(N, D)
         w1b, w2b = bf16_copy(w1), bf16_copy(w2)
         pre = torch.empty(N, w1.shape[0], dtype=BF16, device=x1.device)
         act = gemm.linear_fwd(n2, w1b, _f32(b1), gelu_pre=pre)   # pre = n2 W1^T + b1, act = gelu(pre)
         pend = gemm.linear_fwd(act, w2b, _f32(b2))                # act W2^T + b2
         ctx.save_for_backward(x2, w_norm, rstd, n2, pre, act, w1b, w2b)
         ctx.dims = (B, T, D)
-        return x2.view(B, T, D), pend.view(B, T, D)
+        return (x2.view(B, T, D) if ctx.has_out else x1), pend.view(B, T, D)
 
     @staticmethod
     def backward(ctx, dx2, dpend):
@@ -177,7 +204,7 @@ class FFBlock(torch.autograd.Function):
         # x2 = x1 + out: both inputs get the same gradient, written once and returned for both
         # (the consumer, MinGRUBlock.backward, only reads them)
         dx1, _, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, False)
-        return dx1.view(B, T, D), dx1.view(B, T, D), dw_norm, dW1, db1, dW2, db2
+        return dx1.view(B, T, D), (dx1.view(B, T, D) if ctx.has_out else None), dw_norm, dW1, db1, dW2, db2
 
 
 class FinalNormCE(torch.autograd.Function):

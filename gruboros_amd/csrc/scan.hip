@@ -296,12 +296,16 @@ __device__ __forceinline__ int scan_runs(RunMaps<kSubs>& m, int s, int cl, f4 A,
 
 // ------------------------------------------------------------------ forward
 
-template <typename Tin, typename Tout, bool kNT>
+// kRes: the output is res + h (fp32, res with the output's strides): the scan
+// state joins the residual stream here, and h itself is kept only as the fp32
+// checkpoints the backward rebuilds it from.
+template <typename Tin, typename Tout, bool kNT, bool kRes = false>
 __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
     const Tin* __restrict__ hidden, const Tin* __restrict__ gate, int64_t in_sb, int64_t in_ld,
     const float* __restrict__ h0, Tout* __restrict__ hout, int64_t out_sb, int64_t out_ld,
     float* __restrict__ h_last, float* __restrict__ ckpt, Geometry g, WsHeader* __restrict__ hdr,
-    uint32_t* __restrict__ counters, uint64_t* __restrict__ status) {
+    uint32_t* __restrict__ counters, uint64_t* __restrict__ status, const float* __restrict__ res) {
+  static_assert(!kRes || sizeof(Tout) == 4, "the residual sum is fp32");
   constexpr int kSubs = kFwdSubs, kRows = kFwdRows;
   __shared__ uint32_t s_ticket;
   __shared__ RunMaps<kSubs> s_maps;
@@ -338,7 +342,23 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
       A.v[j] = A.v[j] * a[i][j];
     }
   }
+  // kRes: the run's residual rows in two batches of half a run (all at once
+  // would cost a wave per SIMD); the first is requested before the look-back,
+  // so that it lands under it
+  constexpr int kHalf = kRows / 2;
+  const int64_t out_off =
+      (b * out_sb + static_cast<int64_t>(k) * kFwdTileRows * out_ld + d0) + (s * kRows * static_cast<int>(out_ld) + cl * kVec);
+  f4 rv[kRes ? kHalf : 1];
+  auto load_res = [&](int i0) {
+    if constexpr (kRes) {
+#pragma unroll
+      for (int i = 0; i < kHalf; ++i)
+        rv[i] = (ok && t0 + i0 + i < g.T) ? io4<float>::load(res + out_off + (i0 + i) * static_cast<int>(out_ld))
+                                           : io4<float>::fill(0.0f);
+    }
+  };
   const int buf = scan_runs<kSubs, false>(s_maps, s, cl, A, V);
+  load_res(0);
 
   // Wave 0 links the tile into its chain, one channel per lane: lane
   // (s, cl) takes channel cl * 4 + s.
@@ -365,16 +385,27 @@ __global__ __launch_bounds__(kChLanes * kFwdSubs) void scan_fwd_kernel(
 #pragma unroll
     for (int j = 0; j < kVec; ++j) h.v[j] = pa.v[j] * h.v[j] + pv.v[j];
   }
-  Tout* ob = hout + (b * out_sb + static_cast<int64_t>(k) * kFwdTileRows * out_ld + d0) + (s * kRows * old + cl * kVec);
+  Tout* ob = hout + out_off;
   // kFull: every row of the run is inside the sequence (all runs but the
   // tail's), so the stores need no per-row test.
   auto outputs = [&](auto full_tag) {
     constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
     for (int i = 0; i < kRows; ++i) {
+      if (kRes && i == kHalf) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_res(kHalf);
+      }
 #pragma unroll
       for (int j = 0; j < kVec; ++j) h.v[j] = a[i][j] * h.v[j] + v[i][j];
-      if (kFull || t0 + i < g.T) io4<Tout>::store_nt(ob + i * old, h);
+      if constexpr (kRes) {
+        f4 o;
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) o.v[j] = rv[i % kHalf].v[j] + h.v[j];
+        if (kFull || t0 + i < g.T) io4<Tout>::store_nt(ob + i * old, o);
+      } else {
+        if (kFull || t0 + i < g.T) io4<Tout>::store_nt(ob + i * old, h);
+      }
       if (!kFull && h_last && t0 + i == g.T - 1) io4<float>::store(h_last + c, h);
       if (ckpt && (i + 1) % kCkptRows == 0 && (kFull || t0 + i < g.T))
         io4<float>::store(ckpt + static_cast<int64_t>((t0 + i) / kCkptRows) * g.BD + c, h);
@@ -693,13 +724,16 @@ constexpr int64_t kFwdNtBytes = int64_t(512) << 20;
 template <typename Tin, typename Tout>
 void launch_fwd(const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld, const float* h0, void* h,
                 int64_t out_sb, int64_t out_ld, float* h_last, float* ckpt, const Geometry& g, void* ws,
-                hipStream_t st) {
+                hipStream_t st, const float* res = nullptr) {
   const bool nt = 2 * int64_t(sizeof(Tin)) * g.B * g.T * g.Di > kFwdNtBytes;
   auto kern = nt ? scan_fwd_kernel<Tin, Tout, true> : scan_fwd_kernel<Tin, Tout, false>;
+  if constexpr (sizeof(Tout) == 4) {
+    if (res) kern = nt ? scan_fwd_kernel<Tin, Tout, true, true> : scan_fwd_kernel<Tin, Tout, false, true>;
+  }
   hipLaunchKernelGGL(kern, dim3(g.ncb * g.ntiles), dim3(kChLanes * kFwdSubs), 0, st,
                      static_cast<const Tin*>(hidden), static_cast<const Tin*>(gate), in_sb, in_ld, h0,
                      static_cast<Tout*>(h), out_sb, out_ld, h_last, ckpt, g, ws_header(ws),
-                     ws_counters(ws, g, false), ws_status(ws, g, false));
+                     ws_counters(ws, g, false), ws_status(ws, g, false), res);
 }
 
 template <typename Tin, typename Th>
@@ -896,6 +930,27 @@ extern "C" int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate, i
                           workspace, stream);
 }
 
+extern "C" int mg_scan_fwd_residual(int in_dtype, const void* hidden, const void* gate, int64_t in_sb,
+                                    int64_t in_ld, const float* h0, const float* res, float* x_out, int64_t out_sb,
+                                    int64_t out_ld, float* h_last, float* ckpt, int B, int T, int Di,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "mg_scan_fwd_residual";
+  scan::Geometry g;
+  if (!ckpt) return fail(MG_ERR_ARG, "%s: ckpt is required (the backward rebuilds h from it)", fn);
+  if (int rc = scan::check_tensor(fn, "res", res, MG_F32, out_sb, out_ld)) return rc;
+  if (int rc = scan::fwd_check(fn, in_dtype, hidden, gate, in_sb, in_ld, h0, MG_F32, x_out, out_sb, out_ld, h_last,
+                               ckpt, B, T, Di, workspace, workspace_bytes, 0, g))
+    return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == MG_F32)
+    scan::launch_fwd<float, float>(hidden, gate, in_sb, in_ld, h0, x_out, out_sb, out_ld, h_last, ckpt, g, workspace,
+                                   st, res);
+  else
+    scan::launch_fwd<bf16_t, float>(hidden, gate, in_sb, in_ld, h0, x_out, out_sb, out_ld, h_last, ckpt, g,
+                                    workspace, st, res);
+  return check_launch(fn);
+}
+
 extern "C" size_t mg_scan_fwd_noalloc_max_bytes(void) { return scan::kNoAllocBytes; }
 
 extern "C" int mg_scan_fwd_noalloc(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
@@ -947,7 +1002,7 @@ extern "C" int mg_scan_bwd(int in_dtype, const void* hidden, const void* gate, i
   if ((rc = scan::check_common(fn, B, T, Di, scan::kBwdTileRows, workspace, workspace_bytes, g))) return rc;
   if ((rc = scan::check_tensor(fn, "hidden", hidden, in_dtype, in_sb, in_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "gate", gate, in_dtype, in_sb, in_ld))) return rc;
-  if ((rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
+  if (!(h == nullptr && ckpt) && (rc = scan::check_tensor(fn, "h", h, out_dtype, out_sb, out_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dh", dh, out_dtype, g_sb, g_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dhidden", dhidden, in_dtype, d_sb, d_ld))) return rc;
   if ((rc = scan::check_tensor(fn, "dgate", dgate, in_dtype, d_sb, d_ld))) return rc;

@@ -138,21 +138,42 @@ def _launch_fwd(hidden, gate, h0, out_dtype, need_ckpt=False):
     return h, h_last, ckpt
 
 
+def _launch_fwd_residual(hidden, gate, h0, res):
+    """x_out = res + scan(hidden, gate) (fp32, res's layout: [B, T, Di] with a unit inner stride),
+    with the scan state kept as fp32 checkpoints for the backward. Returns (x_out, h_last, ckpt)."""
+    B, T, Di = hidden.shape
+    L = lib()
+    x_out = torch.empty(B, T, Di, dtype=torch.float32, device=hidden.device)
+    h_last = torch.empty(B, 1, Di, dtype=torch.float32, device=hidden.device)
+    ckpt = torch.empty(L.mg_scan_ckpt_elems(B, T, Di), dtype=torch.float32, device=hidden.device)
+    if res.stride() != x_out.stride():
+        res = res.contiguous()
+    ws = _workspace(hidden.device, B, T, Di)
+    rc = L.mg_scan_fwd_residual(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
+                                ptr(h0), ptr(res), ptr(x_out), x_out.stride(0), x_out.stride(1), ptr(h_last),
+                                ptr(ckpt), B, T, Di, ptr(ws), ws.numel(), stream_of(hidden))
+    check(rc, "mg_scan_fwd_residual")
+    return x_out, h_last, ckpt
+
+
 def _launch_bwd(hidden, gate, h0, h, ckpt, dh, dh_last, dhidden, dgate, want_dh0):
-    """dhidden, dgate: outputs with a shared layout (their strides are passed)."""
+    """dhidden, dgate: outputs with a shared layout (their strides are passed). h may be None when
+    ckpt holds the forward's fp32 state checkpoints (the states are rebuilt from them)."""
     B, T, Di = hidden.shape
     L = lib()
     dev = hidden.device
+    hd = h.dtype if h is not None else torch.float32
     if dh is None:
-        dh = torch.zeros(B, T, Di, dtype=h.dtype, device=dev)
-    elif dh.dtype != h.dtype or not _vec_ok(dh):
-        dh = dh.to(h.dtype).contiguous()
+        dh = torch.zeros(B, T, Di, dtype=hd, device=dev)
+    elif dh.dtype != hd or not _vec_ok(dh):
+        dh = dh.to(hd).contiguous()
     if dh_last is not None:
         dh_last = dh_last.reshape(B, Di).to(torch.float32).contiguous()
     dh0 = torch.empty(B, 1, Di, dtype=torch.float32, device=dev) if want_dh0 else None
     ws = _workspace(dev, B, T, Di)
     rc = L.mg_scan_bwd(dtype_code(hidden.dtype), ptr(hidden), ptr(gate), hidden.stride(0), hidden.stride(1),
-                       ptr(h0), dtype_code(h.dtype), ptr(h), h.stride(0), h.stride(1), ptr(ckpt),
+                       ptr(h0), dtype_code(hd), ptr(h), h.stride(0) if h is not None else 0,
+                       h.stride(1) if h is not None else 0, ptr(ckpt),
                        ptr(dh), dh.stride(0), dh.stride(1), ptr(dh_last), ptr(dhidden), ptr(dgate),
                        dhidden.stride(0), dhidden.stride(1), ptr(dh0), B, T, Di, ptr(ws), ws.numel(),
                        stream_of(hidden))

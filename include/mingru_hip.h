@@ -128,6 +128,19 @@ int mg_scan_fwd(int in_dtype, const void* hidden, const void* gate,
                 int B, int T, int Di,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* mg_scan_fwd with the scan state joining the residual stream (the minGRU
+ * branch of reference mingru/minLM.py:121-125 at expansion 1, where the
+ * minGRU output is h itself): x_out = res + h, fp32, with res and x_out at
+ * (out_sb, out_ld); h itself is not written, only its fp32 checkpoints
+ * (ckpt, required: mg_scan_ckpt_elems(B, T, Di) floats), from which
+ * mg_scan_bwd (called with h = NULL and this ckpt) rebuilds it. h0, h_last,
+ * the workspace and the errors as for mg_scan_fwd; in_dtype MG_BF16 or
+ * MG_F32. res and x_out may be the same buffer. */
+int mg_scan_fwd_residual(int in_dtype, const void* hidden, const void* gate, int64_t in_sb, int64_t in_ld,
+                         const float* h0, const float* res, float* x_out, int64_t out_sb, int64_t out_ld,
+                         float* h_last, float* ckpt, int B, int T, int Di, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* Allocation-free mg_scan_fwd. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Same arguments and
@@ -162,9 +175,10 @@ int mg_scan_fwd_noalloc_check(void* stream);
  *   dgate_t   = lambda_t z_t (1 - z_t) (g(hidden_t) - h_{t-1}),
  *   dhidden_t = lambda_t z_t g'(hidden_t)   (g'(0) = 0, as relu'(0) = 0),
  *   dh0       = a_0 lambda_0.
- * h: the forward's output (same layout, dtype out_dtype). h_{t-1} is read
- * once per 8 steps from ckpt when given (the forward's fp32 checkpoints),
- * else once per 4 steps from h, and rebuilt in fp32 in between.
+ * h: the forward's output (same layout, dtype out_dtype); NULL when ckpt is
+ * given (then out_dtype only sets dh's dtype). h_{t-1} is read once per 8
+ * steps from ckpt when given (the forward's fp32 checkpoints), else once per
+ * 4 steps from h, and rebuilt in fp32 in between.
  * dh: gradient of h, dtype out_dtype, element (b,t,d) at b*g_sb + t*g_ld + d.
  * dh_last (nullable): fp32 [B, Di], gradient of h_last, added to dh_{T-1}.
  * dhidden/dgate: dtype in_dtype, element (b,t,d) at b*d_sb + t*d_ld + d

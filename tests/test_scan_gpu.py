@@ -324,3 +324,47 @@ def test_fp32_output_from_bf16_inputs():
     assert _rel_elem(nxt.detach().cpu(), ref[1]) <= 1e-5
     assert _rel_norm(hg.grad[..., :Di].float().cpu(), ref[2]) <= 1e-2
     assert _rel_norm(hg.grad[..., Di:].float().cpu(), ref[3]) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("B,T,Di,with_h0", [(2, 515, 132, True), (8, 2047, 1024, False), (1, 7, 64, False)])
+def test_residual_scan_matches_scan_plus_add(B, T, Di, with_h0, dtype):
+    """mg_scan_fwd_residual (the minLM block at expansion 1: x_out = res + h, h kept as fp32
+    checkpoints) against mg_scan_fwd followed by the add: x_out bit for bit, h_last and the
+    checkpoints equal; and the backward with h = NULL (states rebuilt from the checkpoints)
+    against the backward reading h: dhidden, dgate and dh0 equal, then both against the fp64
+    oracle (reference mingru/minGRU.py:16-20, :47-69). (8, 2047, 1024) is the cfg3 layer."""
+    from gruboros_amd import scan as S
+
+    hidden, gate, h0, dh, dlast = _make(B, T, Di, dtype, with_h0, seed=B * 31 + T)
+    hg = torch.cat([hidden, gate], -1).to(DEV)
+    hv, gv = hg[..., :Di], hg[..., Di:]
+    h0d = h0.to(DEV) if h0 is not None else None
+    res = torch.randn(B, T, Di, generator=torch.Generator().manual_seed(7)).to(DEV)
+    x_out, h_last_r, ckpt_r = S._launch_fwd_residual(hv, gv, h0d, res)
+    h, h_last, ckpt = S._launch_fwd(hv, gv, h0d, torch.float32, need_ckpt=False)
+    assert torch.equal(x_out, res + h)
+    assert torch.equal(h_last_r, h_last)
+    if dtype == torch.bfloat16:  # the checkpoints the bf16-output path writes (slots T // 8 on are never written)
+        _, _, ckpt_b = S._launch_fwd(hv, gv, h0d, torch.bfloat16, need_ckpt=True)
+        n = (T // 8) * B * Di
+        assert torch.equal(ckpt_r[:n], ckpt_b[:n])
+    dhd = dh.to(DEV).float()
+    dl = dlast.to(DEV)
+    g_ck, g_h = torch.empty_like(hg), torch.empty_like(hg)
+    dh0_ck = S._launch_bwd(hv, gv, h0d, None, ckpt_r, dhd, dl, g_ck[..., :Di], g_ck[..., Di:], with_h0)
+    dh0_h = S._launch_bwd(hv, gv, h0d, h, None, dhd, dl, g_h[..., :Di], g_h[..., Di:], with_h0)
+    S.check_workspaces()
+    # A checkpoint is the state at the end of a forward run, while the forward's next run
+    # starts from the composed run maps, so rebuilt and stored states differ by fp32
+    # rounding; the bf16 gradients' stochastic rounding then lands on the other side now
+    # and then (its hash reads the values). So: near-equal, and both against the oracle.
+    close = 1e-5 if dtype == torch.float32 else 4e-3
+    assert _rel_norm(g_ck.float().cpu(), g_h.float().cpu()) <= close
+    if with_h0:
+        assert _rel_norm(dh0_ck.cpu(), dh0_h.cpu()) <= close
+    if B * T * Di <= 1 << 20:
+        ref = _oracle(hidden, gate, h0, dh.float(), dlast)
+        tol = TOL[dtype]
+        assert _rel_norm(g_ck[..., :Di].float().cpu(), ref[2]) <= tol
+        assert _rel_norm(g_ck[..., Di:].float().cpu(), ref[3]) <= tol
