@@ -64,6 +64,9 @@ SIGNATURES = {
                                          ctypes.c_float, _vp]),
     "mg_column_sum_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_column_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_int, _fp, _vp, _c_size, _vp]),
+    "mg_ff_bias_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int]),
+    "mg_ff_bias_bwd": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_i64, _fp,
+                                _c_int, _vp, _c_size, _vp]),
     "mg_gelu_bwd": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _fp, _c_i64, _c_int, _vp, _c_size, _vp]),
     "mg_embedding_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int]),
     "mg_embedding_bwd": (_c_int, [_vp, _fp, _c_i64, _c_i64, _c_int, _c_int, _fp, _c_i64, _vp, _c_size, _vp]),

@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from . import gemm
-from .linear import bf16_copy, bf16_pair, column_sum, gelu_backward
+from .linear import bf16_copy, bf16_pair, column_sum, gelu_backward, gelu_backward_bias_grads
 from .norm import FP32_EPS  # noqa: F401  (the kernels' eps; norm._fwd passes it)
 from .norm import _bwd as _norm_bwd
 from .norm import _fwd as _norm_fwd
@@ -51,6 +51,10 @@ FF_DW_PAIR = True
 # (mg_scan_fwd_residual) and keeps h only as fp32 checkpoints for the backward;
 # False: the scan writes h and the FeedForward's norm adds it.
 SCAN_RESIDUAL = True
+
+# The FeedForward backward's GELU backward and both bias gradients in one launch
+# (mg_ff_bias_bwd); False: mg_gelu_bwd and mg_column_sum separately.
+FF_BIAS_BWD_FUSED = True
 
 
 def _f32(b):
@@ -194,8 +198,10 @@ class FFBlock(torch.autograd.Function):
             if dp.dtype != BF16 or not dp.is_contiguous():
                 dp = dp.to(BF16).contiguous()
             dact = gemm.linear_dx(dp, w2b, stochastic=True)            # bf16, stochastically rounded
-            dpre, db1 = gelu_backward(dact, pre)                        # bf16, stochastically rounded
-            db2 = column_sum(dp)
+            if FF_BIAS_BWD_FUSED:
+                dpre, db1, db2 = gelu_backward_bias_grads(dact, pre, dp)  # dpre bf16, stochastically rounded
+            else:
+                (dpre, db1), db2 = gelu_backward(dact, pre), column_sum(dp)
             dn2 = gemm.linear_dx(dpre, w1b, stochastic=True)           # bf16, stochastically rounded
             if FF_DW_PAIR:
                 dW2, dW1 = gemm.linear_dw_pair(dp, act, dpre, n2)     # one launch for both weight gradients

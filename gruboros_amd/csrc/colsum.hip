@@ -51,33 +51,41 @@ __device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// The column sums of workgroup (bx, by) of a bx x gy grid.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ x, int64_t ld, int64_t N, int C,
-                                                          float* __restrict__ part) {
-  const int c = blockIdx.x * kCols + threadIdx.x * kVecC;
+__device__ __forceinline__ void colsum_block(const T* __restrict__ x, int64_t ld, int64_t N, int C,
+                                             float* __restrict__ part, int bx, int by, int gy) {
+  const int c = bx * kCols + threadIdx.x * kVecC;
   if (c >= C) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll 4
-  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {
+  for (int64_t n = by; n < N; n += gy) {
     float v[8];
     load8<T>(x + n * ld + c, v);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += v[e];
   }
-  float* o = part + static_cast<int64_t>(blockIdx.y) * C + c;
+  float* o = part + static_cast<int64_t>(by) * C + c;
   reinterpret_cast<float4*>(o)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
   reinterpret_cast<float4*>(o)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
+template <typename T>
+__global__ __launch_bounds__(kThreads) void colsum_kernel(const T* __restrict__ x, int64_t ld, int64_t N, int C,
+                                                          float* __restrict__ part) {
+  colsum_block<T>(x, ld, N, C, part, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+// The GELU backward of workgroup (bx, by) of a bx x gy grid.
 template <typename Tg>
-__global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const Tg* __restrict__ dh, int64_t ld_dh,
-                                                            const bf16_t* __restrict__ pre, int64_t ld_pre,
-                                                            bf16_t* __restrict__ dpre, int64_t ld_out, int64_t N,
-                                                            int C, float* __restrict__ part) {
-  const int c = blockIdx.x * kCols + threadIdx.x * kVecC;
+__device__ __forceinline__ void gelu_bwd_block(const Tg* __restrict__ dh, int64_t ld_dh,
+                                               const bf16_t* __restrict__ pre, int64_t ld_pre,
+                                               bf16_t* __restrict__ dpre, int64_t ld_out, int64_t N, int C,
+                                               float* __restrict__ part, int bx, int by, int gy) {
+  const int c = bx * kCols + threadIdx.x * kVecC;
   if (c >= C) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {  // not unrolled: measured fastest
+  for (int64_t n = by; n < N; n += gy) {  // not unrolled: measured fastest
     float g[8], x[8];
     load8<Tg>(dh + n * ld_dh + c, g);
     load8<bf16_t>(pre + n * ld_pre + c, x);
@@ -93,20 +101,47 @@ __global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const Tg* __restrict
     *reinterpret_cast<uint4*>(dpre + n * ld_out + c) = make_uint4(w[0], w[1], w[2], w[3]);
   }
   if (part) {
-    float* o = part + static_cast<int64_t>(blockIdx.y) * C + c;
+    float* o = part + static_cast<int64_t>(by) * C + c;
     reinterpret_cast<float4*>(o)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     reinterpret_cast<float4*>(o)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
 }
 
+template <typename Tg>
+__global__ __launch_bounds__(kThreads) void gelu_bwd_kernel(const Tg* __restrict__ dh, int64_t ld_dh,
+                                                            const bf16_t* __restrict__ pre, int64_t ld_pre,
+                                                            bf16_t* __restrict__ dpre, int64_t ld_out, int64_t N,
+                                                            int C, float* __restrict__ part) {
+  gelu_bwd_block<Tg>(dh, ld_dh, pre, ld_pre, dpre, ld_out, N, C, part, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+// The FeedForward backward's elementwise work in one launch: the GELU
+// backward with the first bias gradient's partials (workgroups [0, g1): a
+// cb1 x rg1 grid) and the second bias gradient's column-sum partials of dy
+// (workgroups [g1, g1 + cb2 rg2)).
+template <typename Tg>
+__global__ __launch_bounds__(kThreads) void ff_bias_bwd_kernel(const Tg* __restrict__ dh, int64_t ld_dh,
+                                                               const bf16_t* __restrict__ pre, int64_t ld_pre,
+                                                               bf16_t* __restrict__ dpre, int64_t ld_out, int C1,
+                                                               float* __restrict__ part1, int cb1, int rg1,
+                                                               const bf16_t* __restrict__ dy, int64_t ld_dy, int C2,
+                                                               float* __restrict__ part2, int cb2, int rg2,
+                                                               int64_t N) {
+  const int bid = blockIdx.x, g1 = cb1 * rg1;
+  if (bid < g1)
+    gelu_bwd_block<Tg>(dh, ld_dh, pre, ld_pre, dpre, ld_out, N, C1, part1, bid % cb1, bid / cb1, rg1);
+  else
+    colsum_block<bf16_t>(dy, ld_dy, N, C2, part2, (bid - g1) % cb2, (bid - g1) / cb2, rg2);
+}
+
 // out[c] = sum_p part[p][c]: 16 columns (4 lanes x 4) by 64 row lanes per
 // workgroup; each row lane sums every 64th partial row, then a fixed-order
 // tree over the row lanes in LDS.
-__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ part, int P, int C,
-                                                              float* __restrict__ out) {
+__device__ __forceinline__ void reduce_partials_block(const float* __restrict__ part, int P, int C,
+                                                      float* __restrict__ out, int bx) {
   __shared__ float4 s[64][4];
   const int cl = threadIdx.x % 4, rl = threadIdx.x / 4;
-  const int c = blockIdx.x * 16 + cl * 4;
+  const int c = bx * 16 + cl * 4;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (c < C) {
 #pragma unroll 4
@@ -127,6 +162,21 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
     __syncthreads();
   }
   if (rl == 0 && c < C) *reinterpret_cast<float4*>(out + c) = s[0][cl];
+}
+
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ part, int P, int C,
+                                                              float* __restrict__ out) {
+  reduce_partials_block(part, P, C, out, blockIdx.x);
+}
+
+// Two reductions in one launch: workgroups [0, (C1 + 15) / 16) reduce set 1.
+__global__ __launch_bounds__(256) void reduce_partials2_kernel(const float* __restrict__ part1, int P1, int C1,
+                                                               float* __restrict__ out1,
+                                                               const float* __restrict__ part2, int P2, int C2,
+                                                               float* __restrict__ out2) {
+  const int n1 = (C1 + 15) / 16;
+  if (static_cast<int>(blockIdx.x) < n1) reduce_partials_block(part1, P1, C1, out1, blockIdx.x);
+  else reduce_partials_block(part2, P2, C2, out2, blockIdx.x - n1);
 }
 
 }  // namespace colsum
@@ -196,5 +246,47 @@ extern "C" int mg_gelu_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const vo
                        static_cast<const float*>(dh), ld_dh, static_cast<const bf16_t*>(pre), ld_pre,
                        static_cast<bf16_t*>(dpre), ld_out, N, C, part);
   if (dbias) launch_reduce_partials(part, RG, C, dbias, st);
+  return check_launch(fn);
+}
+
+extern "C" size_t mg_ff_bias_bwd_workspace_bytes(int64_t N, int C1, int C2) {
+  if (N < 1 || C1 < 1 || C2 < 1) return 16;
+  return (static_cast<size_t>(colsum::row_groups(N, C1, colsum::kGeluWgs)) * C1 +
+          static_cast<size_t>(colsum::row_groups(N, C2)) * C2) * sizeof(float);
+}
+
+extern "C" int mg_ff_bias_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre,
+                              void* dpre, int64_t ld_out, float* db1, int64_t N, int C1, const void* dy,
+                              int64_t ld_dy, float* db2, int C2, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  const char* fn = "mg_ff_bias_bwd";
+  if (!dh || !pre || !dpre || !db1 || !dy || !db2) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (dh_dtype != MG_F32 && dh_dtype != MG_BF16) return fail(MG_ERR_DTYPE, "%s: dh dtype %d unsupported", fn, dh_dtype);
+  if (N < 1 || C1 < 8 || C1 % 8 || ld_dh < C1 || ld_pre < C1 || ld_out < C1 || ld_dh % 8 || ld_pre % 8 ||
+      ld_out % 8 || C2 < 8 || C2 % 8 || ld_dy < C2 || ld_dy % 8)
+    return fail(MG_ERR_ARG, "%s: bad shape N=%lld C1=%d C2=%d", fn, (long long)N, C1, C2);
+  if (!aligned(dh, 16) || !aligned(pre, 16) || !aligned(dpre, 16) || !aligned(db1, 16) || !aligned(dy, 16) ||
+      !aligned(db2, 16))
+    return fail(MG_ERR_ARG, "%s: misaligned pointer", fn);
+  if (!workspace || workspace_bytes < mg_ff_bias_bwd_workspace_bytes(N, C1, C2) || !aligned(workspace, 16))
+    return fail(MG_ERR_WORKSPACE, "%s: workspace too small or misaligned", fn);
+  const int rg1 = colsum::row_groups(N, C1, colsum::kGeluWgs), rg2 = colsum::row_groups(N, C2);
+  const int cb1 = (C1 + colsum::kCols - 1) / colsum::kCols, cb2 = (C2 + colsum::kCols - 1) / colsum::kCols;
+  float* part1 = static_cast<float*>(workspace);
+  float* part2 = part1 + static_cast<size_t>(rg1) * C1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(cb1 * rg1 + cb2 * rg2);
+  if (dh_dtype == MG_BF16)
+    hipLaunchKernelGGL(colsum::ff_bias_bwd_kernel<bf16_t>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const bf16_t*>(dh), ld_dh, static_cast<const bf16_t*>(pre), ld_pre,
+                       static_cast<bf16_t*>(dpre), ld_out, C1, part1, cb1, rg1, static_cast<const bf16_t*>(dy),
+                       ld_dy, C2, part2, cb2, rg2, N);
+  else
+    hipLaunchKernelGGL(colsum::ff_bias_bwd_kernel<float>, grid, dim3(colsum::kThreads), 0, st,
+                       static_cast<const float*>(dh), ld_dh, static_cast<const bf16_t*>(pre), ld_pre,
+                       static_cast<bf16_t*>(dpre), ld_out, C1, part1, cb1, rg1, static_cast<const bf16_t*>(dy),
+                       ld_dy, C2, part2, cb2, rg2, N);
+  hipLaunchKernelGGL(colsum::reduce_partials2_kernel, dim3((C1 + 15) / 16 + (C2 + 15) / 16), dim3(256), 0, st,
+                     part1, rg1, C1, db1, part2, rg2, C2, db2);
   return check_launch(fn);
 }

@@ -304,6 +304,30 @@ def linear(x, layer):
     return F.linear(x.to(w.dtype), w, b).to(x.dtype)
 
 
+def gelu_backward_bias_grads(dh, pre, dy):
+    """(dpre, db1, db2) of the FeedForward backward in one launch (mg_ff_bias_bwd): dpre =
+    bf16(dh * gelu'(pre)) rounded stochastically with its fp32 column sums db1 (as
+    gelu_backward), and db2 = the fp32 column sums of dy (as column_sum). dh bf16 or fp32 and
+    pre bf16 [N, F], dy bf16 [N, D]; widths the kernels do not take fall back to the two
+    separate calls."""
+    N, C1 = pre.shape
+    C2 = dy.shape[1]
+    if (C1 % 8 or C2 % 8 or dy.dtype != torch.bfloat16 or pre.stride(1) != 1 or dh.stride(1) != 1 or
+            dy.stride(1) != 1 or pre.stride(0) % 8 or dh.stride(0) % 8 or dy.stride(0) % 8 or dy.data_ptr() % 16):
+        dpre, db1 = gelu_backward(dh, pre)
+        return dpre, db1, column_sum(dy)
+    L = lib()
+    dpre = torch.empty_like(pre)
+    db1 = torch.empty(C1, dtype=torch.float32, device=pre.device)
+    db2 = torch.empty(C2, dtype=torch.float32, device=pre.device)
+    wsb = L.mg_ff_bias_bwd_workspace_bytes(N, C1, C2)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=pre.device)
+    check(L.mg_ff_bias_bwd(dtype_code(dh.dtype), ptr(dh), dh.stride(0), ptr(pre), pre.stride(0), ptr(dpre),
+                           dpre.stride(0), ptr(db1), N, C1, ptr(dy), dy.stride(0), ptr(db2), C2, ptr(ws), wsb,
+                           stream_of(pre)), "mg_ff_bias_bwd")
+    return dpre, db1, db2
+
+
 # Where the GELU of the FeedForward runs (measured on MI355X, 16384 x 1024
 # activations, F = 4096):
 #   forward: mg_gemm with the bias + GELU epilogue (its GELU from a bf16

@@ -456,6 +456,17 @@ int mg_gelu_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, in
                 void* dpre, int64_t ld_out, float* dbias, int64_t N, int C,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* mg_gelu_bwd (with dbias = db1, over C1 columns) and mg_column_sum of dy
+ * (bf16 [N, C2], row stride ld_dy, into db2) in one launch, then both
+ * reductions in one more: the elementwise work of the FeedForward backward
+ * (reference mingru/minLM.py:17-23: GELU's backward and both Linear biases'
+ * gradients). Results equal the two separate calls' bit for bit. Workspace:
+ * mg_ff_bias_bwd_workspace_bytes(N, C1, C2). Shapes and alignment as above. */
+size_t mg_ff_bias_bwd_workspace_bytes(int64_t N, int C1, int C2);
+int mg_ff_bias_bwd(int dh_dtype, const void* dh, int64_t ld_dh, const void* pre, int64_t ld_pre, void* dpre,
+                   int64_t ld_out, float* db1, int64_t N, int C1, const void* dy, int64_t ld_dy, float* db2, int C2,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Token-embedding weight gradient (reference mingru/minLM.py:92,99: the
  * backward of nn.Embedding):

@@ -269,6 +269,25 @@ def test_column_sum_and_gelu_backward(N, C):
     assert (db.double() - dpre.double().sum(0)).abs().max() <= 1e-5 * (dpre.double().abs().sum(0).max() + 1)
 
 
+@pytest.mark.parametrize("N,C1,C2", [(16376, 4096, 1024), (37, 264, 16), (777, 1536, 1024), (5, 8, 2056)])
+@pytest.mark.parametrize("dh_dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_feed_forward_bias_grads_in_one_launch(N, C1, C2, dh_dtype):
+    """mg_ff_bias_bwd (the FeedForward backward's GELU backward and both bias gradients,
+    reference mingru/minLM.py:17-23) equals mg_gelu_bwd + mg_column_sum bit for bit: the same
+    per-element stochastic rounding, partial rows and reduction order. (16376, 4096, 1024) is
+    the cfg3 layer."""
+    from gruboros_amd.linear import column_sum, gelu_backward, gelu_backward_bias_grads
+
+    g = torch.Generator(device=DEV).manual_seed(N + C1 + C2)
+    dh = torch.randn(N, C1, device=DEV, generator=g).to(dh_dtype)
+    pre = (torch.randn(N, C1, device=DEV, generator=g) * 2).to(torch.bfloat16)
+    dy = torch.randn(N, C2, device=DEV, generator=g).to(torch.bfloat16)
+    dpre, db1, db2 = gelu_backward_bias_grads(dh, pre, dy)
+    dpre_r, db1_r = gelu_backward(dh, pre)
+    db2_r = column_sum(dy)
+    assert torch.equal(dpre, dpre_r) and torch.equal(db1, db1_r) and torch.equal(db2, db2_r)
+
+
 def test_gradient_rounding_is_stochastic_and_deterministic():
     """bf16 gradient stores round stochastically (as mg_gelu_bwd's dpre does):
     4 M equal fp32 values 0.3 ulp above a bf16 value round up in 30% of the
