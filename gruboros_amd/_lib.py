@@ -72,6 +72,7 @@ SIGNATURES = {
     "mg_embedding_bwd": (_c_int, [_vp, _fp, _c_i64, _c_i64, _c_int, _c_int, _fp, _c_i64, _vp, _c_size, _vp]),
     "mg_gemm": (_c_int, [_c_int, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp, _c_i64,
                          _c_int, _vp, _c_i64, _c_int, _vp, _c_size, _vp]),
+    "mg_gemm_hilo_prefix": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp]),
     "mg_gemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "mg_gemm_wgrad_pair": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _fp, _c_i64,
                                     _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _fp, _c_i64, _c_int, _c_int,

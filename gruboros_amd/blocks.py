@@ -56,6 +56,10 @@ SCAN_RESIDUAL = True
 # (mg_ff_bias_bwd); False: mg_gelu_bwd and mg_column_sum separately.
 FF_BIAS_BWD_FUSED = True
 
+# to_hidden_and_gate's forward as one launch (mg_gemm_hilo_prefix: the hidden
+# half's tiles hi/lo, the gate half's plain) instead of two.
+HG_ONE_LAUNCH = True
+
 
 def _f32(b):
     """A bias as the fp32 contiguous vector the GEMM epilogue adds."""
@@ -83,8 +87,11 @@ class MinGRUBlock(torch.autograd.Function):
         xn = x_out if x_out is not None else x2
         whp, whb = bf16_pair(w_hg), bf16_copy(w_hg)
         hg = torch.empty(N, 2 * Di, dtype=BF16, device=x.device)
-        gemm.linear_fwd_hilo(pair, whp[:Di], hg[:, :Di], D)                    # minGRU.py:45, hidden half
-        gemm.gemm(n, gemm.KCONTIG, whb[Di:], gemm.KCONTIG, N, Di, D, hg[:, Di:])  # gate half
+        if HG_ONE_LAUNCH and gemm.hilo_prefix_fits(pair, whp, D, Di):
+            gemm.linear_fwd_hilo_prefix(pair, whp, hg, D, Di)                   # minGRU.py:45, both halves
+        else:
+            gemm.linear_fwd_hilo(pair, whp[:Di], hg[:, :Di], D)                # minGRU.py:45, hidden half
+            gemm.gemm(n, gemm.KCONTIG, whb[Di:], gemm.KCONTIG, N, Di, D, hg[:, Di:])  # gate half
         hg3 = hg.view(B, T, 2 * Di)
         if w_to is None and SCAN_RESIDUAL:
             # minGRU.py:47-69 and the residual add of minLM.py:125 in one pass; the

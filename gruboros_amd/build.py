@@ -47,6 +47,28 @@ def _run(cmd, verbose):
     return proc.returncode, out
 
 
+# Kernels whose MFMAs are inline assembly on AGPR accumulators (the four-wave
+# 16x16x32 loop): the compiler's hazard checks do not see into that assembly,
+# whose instruction order keeps the hazards away only as written, so a spill the
+# compiler inserts between those instructions can change results. Their
+# register use is checked at every build.
+NO_SPILL_KERNELS = ("gemm_persist_w4m_kernel", "gemm_kernelILi256ELi256ELi2ELi2E", "gemm_pair_kernel")
+
+
+def _spilled_kernels(remarks):
+    """(kernel, VGPR spills) of every guarded kernel that spills, from hipcc's
+    -Rpass-analysis=kernel-resource-usage remarks."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name: " in line:
+            name = line.split("Function Name: ", 1)[1].split()[0]
+        elif "VGPRs Spill: " in line and name and any(k in name for k in NO_SPILL_KERNELS):
+            n = int(line.split("VGPRs Spill: ", 1)[1].split()[0])
+            if n:
+                bad.append((name, n))
+    return bad
+
+
 def build(verbose: bool = False) -> str:
     """Compile every csrc/*.hip (one hipcc process per file, in parallel) and link them into one
     shared library; returns its path."""
@@ -56,12 +78,20 @@ def build(verbose: bool = False) -> str:
         objs = [os.path.join(objdir, os.path.basename(s) + ".o") for s in srcs]
         jobs = max(1, min(len(srcs), os.cpu_count() or 1, 16))
         with ThreadPoolExecutor(jobs) as pool:
-            results = list(pool.map(lambda so: _run([hipcc(), *HIPCC_FLAGS, *inc, "-c", so[0], "-o", so[1]], verbose),
-                                    zip(srcs, objs)))
+            def compile_one(so):
+                extra = ["-Rpass-analysis=kernel-resource-usage"] if os.path.basename(so[0]) == "gemm.hip" else []
+                return _run([hipcc(), *HIPCC_FLAGS, *extra, *inc, "-c", so[0], "-o", so[1]], verbose and not extra)
+
+            results = list(pool.map(compile_one, zip(srcs, objs)))
         for src, (rc, out) in zip(srcs, results):
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {os.path.basename(src)} ({rc}):\n{out}")
-            if verbose and out.strip():
+            if os.path.basename(src) == "gemm.hip":
+                bad = _spilled_kernels(out)
+                if bad:
+                    raise RuntimeError("kernels with inline-assembly MFMAs spill registers (their results would not "
+                                       "be trustworthy): " + ", ".join(f"{k} ({n})" for k, n in bad))
+            elif verbose and out.strip():
                 print(out, flush=True)
         fd, tmp = tempfile.mkstemp(prefix=LIB_NAME + ".tmp", dir=HERE)
         os.close(fd)

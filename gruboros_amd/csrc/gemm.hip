@@ -86,6 +86,8 @@ struct Params {
   uint32_t aux_span;        // bytes of aux (GELU gradient's pre-activations)
   int hilo;                 // 1: hi/lo operands, three K segments of nkt_seg k-tiles
   int nkt_seg;              // k-tiles per K segment (ceil(K / 64))
+  int hilo_cols;            // persistent four-wave kernel only, > 0: only output columns below
+                            // it are hi/lo products, the rest take the hi halves' product alone
 };
 
 // k-tiles of the whole k-loop (three segments for hi/lo products)
@@ -1052,6 +1054,10 @@ struct W4MPipe {
     nseg = p.hilo ? p.nkt_seg : (1 << 29);  // k-tiles per hi/lo segment (none: never reached; 2 nseg < 2^31)
     K = p.K;
   }
+  // a tile of a product whose hi/lo mode varies by tile (Params::hilo_cols)
+  __device__ __forceinline__ void set_hilo(const Params& p, bool hilo_tile) {
+    nseg = __builtin_amdgcn_readfirstlane(hilo_tile ? p.nkt_seg : (1 << 29));  // wave-uniform: a scalar
+  }
   // byte offsets of the tile origins (m0, n0)
   __device__ __forceinline__ uint32_t aorg(int m0) const { return M16Operand<AK>::origin(m0, oa.ld2); }
   __device__ __forceinline__ uint32_t borg(int n0) const { return M16Operand<BKM>::origin(n0, ob.ld2); }
@@ -1774,7 +1780,11 @@ __global__ __launch_bounds__(512) void gemm_persist_kernel(Params p) {
 // C = gelu of it). The staging is the wave's own, so the epilogue needs no
 // workgroup barrier, and it is beside the operand stages, which hold the next
 // tile's k-tiles.
-template <bool AK, bool BKM, int EPI>
+// kPrefix: only the tiles of output columns below p.hilo_cols are hi/lo
+// products (three K segments), the others take the first segment alone
+// (mg_gemm_hilo_prefix); the tile ids [0, T1) walk the first kind, then the
+// others, each laid out as tile_of lays out a product of its own.
+template <bool AK, bool BKM, int EPI, bool kPrefix = false>
 __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
   using Pipe = W4MPipe<AK, BKM>;
   constexpr int kStage = 2 * Pipe::kStageA;
@@ -1791,7 +1801,8 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
   constexpr bool kGelu = EPI == EPI_BIAS_GELU;
   __shared__ uint16_t s_gelu[kGelu ? kGeluLutN : 1];
   const int ntiles = p.tiles_m * p.tiles_n;
-  const int n = total_ktiles(p);
+  const int tn1 = kPrefix ? p.hilo_cols / 256 : p.tiles_n;
+  const int T1 = p.tiles_m * tn1;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   Pipe P;
@@ -1800,12 +1811,22 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
   int pid = blockIdx.x;
   auto origin = [&](int id, int& m0, int& n0) {
     int tm, tn;
-    tile_of(id, p.tiles_m, p.tiles_n, tm, tn);
+    if (!kPrefix || id < T1) {
+      tile_of(id, p.tiles_m, tn1, tm, tn);
+    } else {
+      tile_of(id - T1, p.tiles_m, p.tiles_n - tn1, tm, tn);
+      tn += tn1;
+    }
     m0 = tm * 256;
     n0 = tn * 256;
   };
   int m0, n0;
   origin(pid, m0, n0);
+  int n = total_ktiles(p);
+  if constexpr (kPrefix) {
+    n = __builtin_amdgcn_readfirstlane(n0 < p.hilo_cols ? 3 * p.nkt_seg : p.nkt_seg);
+    P.set_hilo(p, n0 < p.hilo_cols);
+  }
   uint32_t ar = P.aorg(m0), br = P.borg(n0);
   __amdgpu_buffer_rsrc_t bias_rsrc;
   if constexpr (kBias)
@@ -1962,6 +1983,12 @@ __global__ __launch_bounds__(256) void gemm_persist_w4m_kernel(Params p) {
     n0 = n1;
     ar = ar1;
     br = br1;
+    if constexpr (kPrefix) {
+      // the next tile's k-tiles 0 and 1 (loaded above) lie in the first K segment
+      // whatever its mode; its mode sets where its later k-tiles come from
+      n = __builtin_amdgcn_readfirstlane(n0 < p.hilo_cols ? 3 * p.nkt_seg : p.nkt_seg);
+      P.set_hilo(p, n0 < p.hilo_cols);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last tile's spare loads land before the LDS is released
 }
@@ -2540,6 +2567,40 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
   const int64_t n4 = int64_t(M) * (N / 4);
   hipLaunchKernelGGL(gemm::split_reduce_kernel, dim3(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048))),
                      dim3(256), 0, s, p.part, pl.ysplits, M, N, static_cast<float*>(C), ldc, p.accumulate);
+  return check_launch(fn);
+}
+
+extern "C" int mg_gemm_hilo_prefix(const void* A, int64_t lda, const void* B, int64_t ldb, int M, int N, int K,
+                                   int hilo_cols, void* C, int64_t ldc, void* stream) {
+  const char* fn = "mg_gemm_hilo_prefix";
+  if (!A || !B || !C) return fail(MG_ERR_ARG, "%s: null operand", fn);
+  if (!gemm::kUseW4M) return fail(MG_ERR_ARG, "%s: needs the four-wave persistent kernel", fn);
+  if (M < 1 || N < 8 || N % 8 || K < 64 || K % 128)
+    return fail(MG_ERR_ARG, "%s: M=%d N=%d K=%d (N a multiple of 8, K of 128)", fn, M, N, K);
+  if (hilo_cols < 256 || hilo_cols % 256 || hilo_cols >= N)
+    return fail(MG_ERR_ARG, "%s: hilo_cols %d must be a multiple of 256 below N=%d", fn, hilo_cols, N);
+  if (lda < 2 * K || ldb < 2 * K || ldc < N || lda % 8 || ldb % 8 || ldc % 8)
+    return fail(MG_ERR_ARG, "%s: leading dimensions (rows of 2K hi/lo values, ldc >= N, multiples of 8)", fn);
+  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16)) return fail(MG_ERR_ARG, "%s: operands must be 16-byte aligned", fn);
+  const int64_t a_span = (int64_t(M - 1) * lda + 2 * K) * 2, b_span = (int64_t(N - 1) * ldb + 2 * K) * 2;
+  if (a_span + 256 * lda * 2 >= (int64_t(1) << 31) || b_span + 256 * ldb * 2 >= (int64_t(1) << 31))
+    return fail(MG_ERR_ARG, "%s: operands must span less than 2 GiB", fn);
+  gemm::Params p{};
+  p.A = static_cast<const bf16_t*>(A);
+  p.B = static_cast<const bf16_t*>(B);
+  p.C = C;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K;
+  p.a_span = static_cast<uint32_t>(a_span);
+  p.b_span = static_cast<uint32_t>(b_span);
+  p.hilo = 1;
+  p.nkt_seg = K / gemm::BK;  // even: K % 128 == 0
+  p.hilo_cols = hilo_cols;
+  p.tiles_m = (M + 255) / 256;
+  p.tiles_n = (N + 255) / 256;
+  p.kt_per_split = 3 * p.nkt_seg;
+  hipLaunchKernelGGL((gemm::gemm_persist_w4m_kernel<true, true, gemm::EPI_NONE, true>),
+                     dim3(std::min(p.tiles_m * p.tiles_n, gemm::kCUs)), dim3(256), 0, static_cast<hipStream_t>(stream), p);
   return check_launch(fn);
 }
 

@@ -110,6 +110,26 @@ def linear_fwd(x, w, bias=None, *, gelu_pre=None, out_dtype=torch.bfloat16):
     return y
 
 
+def hilo_prefix_fits(x_pair, w_pair, K, hilo_cols):
+    """Whether linear_fwd_hilo_prefix takes these operands (mg_gemm_hilo_prefix's rules)."""
+    N = w_pair.shape[0]
+    return (K % 128 == 0 and hilo_cols % 256 == 0 and 0 < hilo_cols < N and N % 8 == 0 and
+            all(t.dtype == torch.bfloat16 and t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.stride(0) >= 2 * K and
+                t.data_ptr() % 16 == 0 for t in (x_pair, w_pair)) and
+            spans_ok(x_pair.shape[0], x_pair.stride(0)) and spans_ok(N, w_pair.stride(0)))
+
+
+def linear_fwd_hilo_prefix(x_pair, w_pair, out, K, hilo_cols):
+    """out[N, O] (bf16) = x w^T from hi/lo pairs x_pair [N, 2K], w_pair [O, 2K]: columns below
+    hilo_cols to fp32 accuracy, the rest from the hi halves alone, in one launch
+    (mg_gemm_hilo_prefix)."""
+    L = _lib.lib()
+    _lib.check(L.mg_gemm_hilo_prefix(_lib.ptr(x_pair), _rows(x_pair, "x_pair"), _lib.ptr(w_pair), _rows(w_pair, "w_pair"),
+                                     x_pair.shape[0], w_pair.shape[0], K, hilo_cols, _lib.ptr(out), _rows(out, "out"),
+                                     _lib.stream_of(out)), "mg_gemm_hilo_prefix")
+    return out
+
+
 def split_hilo(x, out=None):
     """fp32 [rows, cols] (unit inner stride) -> bf16 [rows, 2 cols] = [bf16(x) | bf16(x - bf16(x))]
     (mg_split_hilo), the operand form of hilo products."""

@@ -361,6 +361,17 @@ int mg_gemm(int a_layout, const void* A, int64_t lda,
             int epilogue, const float* bias, void* aux, int64_t ldaux,
             int c_dtype, void* C, int64_t ldc, int flags,
             void* workspace, size_t workspace_bytes, void* stream);
+/* C[m, n] = sum_k A(m, k) B(n, k) for K-contiguous hi/lo pairs A [M, 2K] and
+ * B [N, 2K] (rows [hi (K) | lo (K)], lda, ldb >= 2K), bf16 C [M, N]: the
+ * columns n < hilo_cols to fp32 accuracy (A_hi B_hi + A_lo B_hi + A_hi B_lo,
+ * as MG_GEMM_HILO), the others from the hi halves alone (A_hi B_hi), in one
+ * persistent launch. It is the forward of reference mingru/minGRU.py:45
+ * (to_hidden_and_gate) with the hidden half accurate and the gate half a
+ * plain bf16 product, where two mg_gemm calls would each fill and drain the
+ * pipeline. K % 128 == 0, N % 8 == 0, hilo_cols a multiple of 256 below N,
+ * leading dimensions multiples of 8, 16-byte aligned operands. */
+int mg_gemm_hilo_prefix(const void* A, int64_t lda, const void* B, int64_t ldb, int M, int N, int K, int hilo_cols,
+                        void* C, int64_t ldc, void* stream);
 size_t mg_gemm_workspace_bytes(int a_layout, int b_layout, int M, int N, int K, int epilogue,
                                int c_dtype, int flags);
 

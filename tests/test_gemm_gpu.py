@@ -626,3 +626,27 @@ def test_f32_linear_matches_fp64(N, K, O, bias):
         errs["db"] = _rel(bd.grad, br.grad)
     print(f"f32_linear N={N} K={K} O={O}", {k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
     assert all(v <= 2e-6 for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("M,N,K,hc", [(16376, 2048, 1024, 1024), (300, 520, 128, 256), (1000, 1536, 256, 512),
+                                      (4, 264, 128, 256)])
+def test_hilo_prefix_matches_the_two_products(M, N, K, hc):
+    """mg_gemm_hilo_prefix (to_hidden_and_gate's forward in one launch, reference
+    mingru/minGRU.py:45) equals the hi/lo product of its first hc columns and the plain
+    product of the hi halves for the rest, bit for bit; and the hi/lo columns are
+    fp32-accurate against float64. (16376, 2048, 1024, 1024) is the cfg3 layer."""
+    from gruboros_amd import gemm
+
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    x = torch.randn(M, K, device=DEV, generator=g)
+    w = torch.randn(N, K, device=DEV, generator=g) / K ** 0.5
+    xp, wp = gemm.split_hilo(x), gemm.split_hilo(w)
+    assert gemm.hilo_prefix_fits(xp, wp, K, hc)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    gemm.linear_fwd_hilo_prefix(xp, wp, out, K, hc)
+    ref = torch.empty_like(out)
+    gemm.linear_fwd_hilo(xp, wp[:hc], ref[:, :hc], K)
+    gemm.gemm(xp[:, :K], gemm.KCONTIG, wp[hc:, :K], gemm.KCONTIG, M, N - hc, K, ref[:, hc:])
+    assert torch.equal(out, ref)
+    exact = (x.double() @ w.double().t())[:, :hc]
+    assert _rel(out[:, :hc], exact) <= 2 ** -8

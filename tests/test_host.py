@@ -151,3 +151,21 @@ def test_block_path_width_conditions():
     assert not ok(1000, 1.5)            # Di = 1500
     assert not ok(1024, 1.0, 4.001)     # F = 4097
     assert not ok(1004, 1.0)            # D = 1004
+
+
+def test_build_refuses_spills_in_inline_assembly_kernels():
+    """gruboros_amd.build reads hipcc's resource-usage remarks for gemm.hip and refuses a build
+    in which a kernel with inline-assembly MFMAs spills registers (such a spill once gave
+    wrong products); other kernels may spill."""
+    from gruboros_amd.build import _spilled_kernels
+
+    remarks = "\n".join([
+        "gemm.hip:1:1: remark: Function Name: _ZN2mg4gemm23gemm_persist_w4m_kernelILb1ELb1ELi0ELb1EEEvNS0_6ParamsE",
+        "gemm.hip:1:1: remark:     VGPRs Spill: 41",
+        "gemm.hip:1:1: remark: Function Name: _ZN2mg4gemm11gemm_kernelILi256ELi256ELi2ELi4ELb1ELb0ELi0EfLi2EEEvNS0_6ParamsE",
+        "gemm.hip:1:1: remark:     VGPRs Spill: 1",
+        "gemm.hip:1:1: remark: Function Name: _ZN2mg4gemm16gemm_pair_kernelILi256ELi256ELi2ELi2ELb0ELb0EEEvNS0_6ParamsES2_",
+        "gemm.hip:1:1: remark:     VGPRs Spill: 0",
+    ])
+    bad = _spilled_kernels(remarks)
+    assert [n for _, n in bad] == [41] and "persist_w4m" in bad[0][0]
