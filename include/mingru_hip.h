@@ -44,8 +44,9 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch): 201 = 0.2.1, the ABI
- * declared in this file (0.2.1 adds entry points to 0.2.0 and changes none). */
+/* Library version (major*10000 + minor*100 + patch): 202 = 0.2.2, the ABI
+ * declared in this file (0.2.1 and 0.2.2 add entry points to 0.2.0 and change
+ * none). */
 int mg_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
