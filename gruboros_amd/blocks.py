@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from . import gemm
-from .linear import bf16_copy, bf16_pair, column_sum, gelu_backward, gelu_backward_bias_grads
+from .linear import bf16_copy, bf16_pair, column_sum, gelu_backward, gelu_backward_bias_grads, grad_target
 from .norm import FP32_EPS  # noqa: F401  (the kernels' eps; norm._fwd passes it)
 from .norm import _bwd as _norm_bwd
 from .norm import _fwd as _norm_fwd
@@ -81,6 +81,7 @@ class MinGRUBlock(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         B, T, D = x.shape
         N, Di = B * T, w_hg.shape[0] // 2
+        ctx.w_hg, ctx.w_to = w_hg, w_to  # for their .grad (weight gradients added in place, grad_target)
         x2 = x.reshape(N, D)
         p2 = pending.reshape(N, D) if pending is not None else None
         x_out, n, rstd, pair = _norm_fwd(x2, p2, w_norm, BF16, with_lo=True)
@@ -137,7 +138,11 @@ class MinGRUBlock(torch.autograd.Function):
             dob = gemm.round_bf16_sr(dout.reshape(N, D).contiguous().float())
             dh = gemm.linear_dx(dob, wtb, out_dtype=torch.float32).view(B, T, Di)
             if ctx.needs_input_grad[5] and not (FF_DW_PAIR and ctx.needs_input_grad[3]):
-                dW_to = gemm.linear_dw(dob, h_pair[:, :Di])
+                g_to = grad_target(ctx.w_to)
+                if g_to is not None:
+                    gemm.linear_dw(dob, h_pair[:, :Di], out=g_to, accumulate=True)
+                else:
+                    dW_to = gemm.linear_dw(dob, h_pair[:, :Di])
         else:
             dh = dout.float()
         dhg = torch.empty(N, 2 * Di, dtype=BF16, device=dev)
@@ -152,9 +157,16 @@ class MinGRUBlock(torch.autograd.Function):
         dn = gemm.linear_dx(dhg, whb, stochastic=True)             # bf16, stochastically rounded
         dW_hg = None
         if ctx.needs_input_grad[3]:
+            g_hg = grad_target(ctx.w_hg)
             if ctx.has_to and dout is not None and ctx.needs_input_grad[5] and FF_DW_PAIR:
                 # to_out's and to_hidden_and_gate's weight gradients in one launch
-                dW_to, dW_hg = gemm.linear_dw_pair(dob, h_pair[:, :Di], dhg, pair[:, :D])
+                g_to = grad_target(ctx.w_to)
+                if g_to is not None and g_hg is not None:
+                    gemm.linear_dw_pair(dob, h_pair[:, :Di], dhg, pair[:, :D], out0=g_to, out1=g_hg, accumulate=True)
+                else:
+                    dW_to, dW_hg = gemm.linear_dw_pair(dob, h_pair[:, :Di], dhg, pair[:, :D])
+            elif g_hg is not None:
+                gemm.linear_dw(dhg, pair[:, :D], out=g_hg, accumulate=True)
             else:
                 dW_hg = gemm.linear_dw(dhg, pair[:, :D])
         dres = dx1.reshape(N, D) if dx1 is not None else None
@@ -179,6 +191,7 @@ class FFBlock(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         B, T, D = x1.shape
         N = B * T
+        ctx.w1, ctx.w2 = w1, w2  # for their .grad (weight gradients added in place, grad_target)
         x2, n2, rstd, _ = _norm_fwd(x1.reshape(N, D), out.reshape(N, D) if out is not None else None, w_norm, BF16)
         ctx.has_out = out is not None
         if x2 is None:
@@ -210,10 +223,20 @@ class FFBlock(torch.autograd.Function):
             else:
                 (dpre, db1), db2 = gelu_backward(dact, pre), column_sum(dp)
             dn2 = gemm.linear_dx(dpre, w1b, stochastic=True)           # bf16, stochastically rounded
-            if FF_DW_PAIR:
+            g1, g2 = grad_target(ctx.w1), grad_target(ctx.w2)
+            if FF_DW_PAIR and g1 is not None and g2 is not None:
+                gemm.linear_dw_pair(dp, act, dpre, n2, out0=g2, out1=g1, accumulate=True)  # into .grad
+            elif FF_DW_PAIR:
                 dW2, dW1 = gemm.linear_dw_pair(dp, act, dpre, n2)     # one launch for both weight gradients
             else:
-                dW2, dW1 = gemm.linear_dw(dp, act), gemm.linear_dw(dpre, n2)
+                if g2 is not None:
+                    gemm.linear_dw(dp, act, out=g2, accumulate=True)
+                else:
+                    dW2 = gemm.linear_dw(dp, act)
+                if g1 is not None:
+                    gemm.linear_dw(dpre, n2, out=g1, accumulate=True)
+                else:
+                    dW1 = gemm.linear_dw(dpre, n2)
         # x2 = x1 + out: both inputs get the same gradient, written once and returned for both
         # (the consumer, MinGRUBlock.backward, only reads them)
         dx1, _, dw_norm = _norm_bwd(x2, w_norm, rstd, dn2, dres, True, torch.float32, False)

@@ -195,31 +195,37 @@ def linear_dx(dy, w, *, gelu_pre=None, out_dtype=torch.bfloat16, stochastic=Fals
     return dx
 
 
-def linear_dw_pair(dy0, x0, dy1, x1, deterministic=None):
+def linear_dw_pair(dy0, x0, dy1, x1, deterministic=None, out0=None, out1=None, accumulate=False):
     """(dy0^T x0, dy1^T x1), fp32, over the same rows: the FeedForward's two weight gradients in one
     K-split launch (mg_gemm_wgrad_pair; each product alone where the pair does not apply). Operands
-    over 2 GiB go through linear_dw one product at a time."""
+    over 2 GiB go through linear_dw one product at a time. accumulate: added into out0 and out1
+    (both given, fp32 contiguous) instead of written."""
     n = dy0.shape[0]
     if deterministic is None:
         deterministic = torch.are_deterministic_algorithms_enabled()
     if dy1.shape[0] != n or x0.shape[0] != n or x1.shape[0] != n:
         raise _lib.MingruHipError("linear_dw_pair: the four operands must have the same number of rows")
+    if accumulate and (out0 is None or out1 is None):
+        raise _lib.MingruHipError("linear_dw_pair: accumulate needs both outputs")
     if _row_step(n, 2 * dy0.stride(0), 2 * x0.stride(0), 2 * dy1.stride(0), 2 * x1.stride(0)) < n:
-        return linear_dw(dy0, x0, deterministic=deterministic), linear_dw(dy1, x1, deterministic=deterministic)
+        return (linear_dw(dy0, x0, out=out0, accumulate=accumulate, deterministic=deterministic),
+                linear_dw(dy1, x1, out=out1, accumulate=accumulate, deterministic=deterministic))
     _lib.require_cuda(dy0, x0, dy1, x1)
     if any(t.dtype != torch.bfloat16 for t in (dy0, x0, dy1, x1)):
         raise _lib.MingruHipError("linear_dw_pair operands must be bfloat16")
     (m0, n0), (m1, n1) = (dy0.shape[1], x0.shape[1]), (dy1.shape[1], x1.shape[1])
-    out0 = torch.empty(m0, n0, device=dy0.device, dtype=torch.float32)
-    out1 = torch.empty(m1, n1, device=dy0.device, dtype=torch.float32)
-    flags = FLAG_DETERMINISTIC if deterministic else 0
+    if out0 is None:
+        out0 = torch.empty(m0, n0, device=dy0.device, dtype=torch.float32)
+    if out1 is None:
+        out1 = torch.empty(m1, n1, device=dy0.device, dtype=torch.float32)
+    flags = (FLAG_DETERMINISTIC if deterministic else 0) | (FLAG_ACCUMULATE if accumulate else 0)
     L = _lib.lib()
     wsb = L.mg_gemm_wgrad_pair_workspace_bytes(m0, n0, m1, n1, n, flags)
     ws = _workspace(out0.device, wsb) if wsb else None
     rc = L.mg_gemm_wgrad_pair(_lib.ptr(dy0), _rows(dy0, "dy0"), _lib.ptr(x0), _rows(x0, "x0"), m0, n0,
-                              _lib.ptr(out0), n0, _lib.ptr(dy1), _rows(dy1, "dy1"), _lib.ptr(x1), _rows(x1, "x1"),
-                              m1, n1, _lib.ptr(out1), n1, n, flags, _lib.ptr(ws), ws.numel() if ws is not None else 0,
-                              _lib.stream_of(out0))
+                              _lib.ptr(out0), _rows(out0, "out0"), _lib.ptr(dy1), _rows(dy1, "dy1"), _lib.ptr(x1),
+                              _rows(x1, "x1"), m1, n1, _lib.ptr(out1), _rows(out1, "out1"), n, flags, _lib.ptr(ws),
+                              ws.numel() if ws is not None else 0, _lib.stream_of(out0))
     _lib.check(rc, "mg_gemm_wgrad_pair")
     return out0, out1
 

@@ -48,6 +48,32 @@ def _mm_f32(a, b):
     return torch.mm(a, b).float()
 
 
+# Weight gradients added into an existing .grad by the product itself (gradient
+# accumulation over micro-steps or TBPTT chunks: every backward after the first)
+# instead of autograd adding the product's fresh result; see grad_target.
+ACCUMULATE_IN_PLACE = True
+
+
+def grad_target(w):
+    """w.grad, when this backward may add w's gradient into it directly and give autograd none:
+    the engine will run w's AccumulateGrad (a .backward() that accumulates, not
+    torch.autograd.grad), w.grad exists as an fp32 contiguous tensor of w's shape, and w has no
+    gradient hooks. Else None (the gradient is returned to autograd as usual). Called from a
+    backward."""
+    if not ACCUMULATE_IN_PLACE or not isinstance(w, torch.Tensor) or not w.requires_grad:
+        return None
+    g = w.grad
+    if (g is None or g.dtype != torch.float32 or g.shape != w.shape or not g.is_contiguous() or
+            g.device != w.device or w._backward_hooks or getattr(w, "_post_accumulate_grad_hooks", None)):
+        return None
+    try:
+        if not torch._C._will_engine_execute_node(torch.autograd.graph.get_gradient_edge(w).node):
+            return None
+    except (RuntimeError, AttributeError):
+        return None
+    return g
+
+
 def _dw_ok(dy2, x2):
     """Shapes the MFMA weight-gradient product takes (mg_gemm, both operands MN-contiguous)."""
     return (dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and dy2.stride(1) == 1 and x2.stride(1) == 1

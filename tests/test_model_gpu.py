@@ -715,3 +715,48 @@ def test_generate_py_load_and_decode_path(cast):
             prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)
     routed = [d for d in decode._CACHE.get(model, {}).values() if isinstance(d, decode.Decoder)]
     assert len(routed) == (1 if cast == torch.bfloat16 else 0)
+
+
+@pytest.mark.parametrize("expansion", [1.0, 1.5])
+def test_gradient_accumulation_in_place_matches_autograd(expansion):
+    """Micro-steps accumulating into .grad (train.py:798-800 with grad_accum 3): the weight
+    gradients that the products add into .grad themselves (linear.grad_target) equal autograd's
+    own accumulation bit for bit; a parameter with a hook, and torch.autograd.grad while .grad is
+    populated, keep autograd's semantics (the hook sees the gradient; autograd.grad returns it
+    and leaves .grad alone)."""
+    from gruboros_amd import linear
+
+    m, sd = _model(256, 2, expansion, torch.bfloat16, seed=12)
+    chunks = [torch.randint(0, 256, (2, 129), generator=torch.Generator().manual_seed(40 + i)).to(DEV) for i in range(3)]
+    grads = {}
+    for fused in (True, False):
+        linear.ACCUMULATE_IN_PLACE = fused
+        try:
+            m.zero_grad(set_to_none=True)
+            for c in chunks:
+                (m(c, return_loss=True) / 3).backward()
+        finally:
+            linear.ACCUMULATE_IN_PLACE = True
+        grads[fused] = {n: p.grad.clone() for n, p in m.named_parameters()}
+    for n in grads[True]:
+        assert torch.equal(grads[True][n], grads[False][n]), n
+    # a hook on one weight: it sees each micro-step's gradient, and the sum is unchanged
+    w = m.layers[0][4][0].weight
+    seen = []
+    h = w.register_hook(lambda g: seen.append(g.clone()))
+    m.zero_grad(set_to_none=True)
+    for c in chunks:
+        (m(c, return_loss=True) / 3).backward()
+    h.remove()
+    assert len(seen) == 3 and torch.equal(w.grad, grads[False]["layers.0.4.0.weight"])
+    # autograd.grad with .grad populated: .grad untouched, the returned gradient is the chunk's own
+    before = {n: p.grad.clone() for n, p in m.named_parameters()}
+    loss = m(chunks[0], return_loss=True)
+    params = [p for _, p in m.named_parameters()]
+    gs = torch.autograd.grad(loss, params)
+    for (n, p), g in zip(m.named_parameters(), gs):
+        assert torch.equal(p.grad, before[n]), n
+    m.zero_grad(set_to_none=True)
+    m(chunks[0], return_loss=True).backward()
+    for (n, p), g in zip(m.named_parameters(), gs):
+        assert torch.equal(g, p.grad), n
