@@ -3,9 +3,10 @@ mg_decode_mingru / mg_decode_ff / mg_decode_head) for the generation loop of
 reference generate.py:184-212.
 
 Checks:
-  * against the drop-in model's own one-token call (model(token,
-    prev_hiddens=...), reference mingru/minLM.py:101-102 with minGRU's
-    one-step path mingru/minGRU.py:47-52) step by step: logits and states;
+  * against the drop-in model's own one-token call on its parallel path
+    (model(token, prev_hiddens=...) with the decode routing off, reference
+    mingru/minLM.py:101-102 with minGRU's one-step path
+    mingru/minGRU.py:47-52) step by step: logits and states;
   * against one parallel forward over prompt + generated tokens (T single
     steps equal one T-long scan);
   * the captured HIP graph replays exactly what the launches compute, also
@@ -47,6 +48,7 @@ def test_decoder_matches_one_token_model_calls(B, dim):
     from gruboros_amd.decode import Decoder
 
     m = _model(dim=dim)
+    m.decode_kernels = False  # the reference calls below run the parallel path
     gen = torch.Generator(device=DEV).manual_seed(B)
     prompt = torch.randint(0, 256, (B, 17), device=DEV, generator=gen)
     dec = Decoder(m, B)
