@@ -51,6 +51,19 @@ __device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Non-temporal 16-byte load of 8 bf16 values. The GELU backward's inputs (the
+// saved pre-activation and the gradient dh just written, 134 MB each at cfg3)
+// are read once; loaded with the hint the cfg3 step measured 11.31 -> 11.19 ms.
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load8_stream(const bf16_t* p, float (&v)[8]) {
+  const u32x4_nt x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = __uint_as_float(x[q] << 16);
+    v[2 * q + 1] = __uint_as_float(x[q] & 0xffff0000u);
+  }
+}
+
 // The column sums of workgroup (bx, by) of a bx x gy grid.
 template <typename T>
 __device__ __forceinline__ void colsum_block(const T* __restrict__ x, int64_t ld, int64_t N, int C,
@@ -87,8 +100,11 @@ __device__ __forceinline__ void gelu_bwd_block(const Tg* __restrict__ dh, int64_
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int64_t n = by; n < N; n += gy) {  // not unrolled: measured fastest
     float g[8], x[8];
-    load8<Tg>(dh + n * ld_dh + c, g);
-    load8<bf16_t>(pre + n * ld_pre + c, x);
+    if constexpr (sizeof(Tg) == 2)
+      load8_stream(reinterpret_cast<const bf16_t*>(dh + n * ld_dh + c), g);
+    else
+      load8<Tg>(dh + n * ld_dh + c, g);
+    load8_stream(pre + n * ld_pre + c, x);
     uint32_t w[4];
     const uint32_t idx = static_cast<uint32_t>(n * C + c);
 #pragma unroll

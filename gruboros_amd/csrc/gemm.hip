@@ -2223,6 +2223,20 @@ __global__ __launch_bounds__(256) void logits_ce_kernel(Params p, const int64_t*
   if (threadIdx.x == 0) loss_part[blockIdx.x] = s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3];
 }
 
+// The split-K reduction reads each partial once and writes a weight gradient
+// the optimizer reads at the end of the step: both carry the non-temporal hint
+// (cfg3 step 11.19 -> 11.14 ms).
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4 load4_stream(const float* q) {
+  const f32x4_nt x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(q));
+  f4 r; r.v[0] = x[0]; r.v[1] = x[1]; r.v[2] = x[2]; r.v[3] = x[3];
+  return r;
+}
+__device__ __forceinline__ void store4_stream(float* q, const f4& r) {
+  const f32x4_nt x = {r.v[0], r.v[1], r.v[2], r.v[3]};
+  __builtin_nontemporal_store(x, reinterpret_cast<f32x4_nt*>(q));
+}
+
 // C[m, n] (+)= sum over the S split partials, added in split order.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                                            float* __restrict__ C, int64_t ldc, int accumulate) {
@@ -2234,12 +2248,29 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     float* cp = C + m * ldc + n;
     f4 sum = accumulate ? io4<float>::load(cp) : io4<float>::fill(0.0f);
     const float* pp = part + m * N + n;
-    for (int s = 0; s < S; ++s) {
-      const f4 v = io4<float>::load(pp + s * slice);
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {  // eight partials in flight
+      f4 v[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
+      for (int u = 0; u < 8; ++u) v[u] = load4_stream(pp + (s + u) * slice);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum.v[e] += v[u].v[e];
     }
-    io4<float>::store(cp, sum);
+    for (; s + 2 <= S; s += 2) {
+      const f4 v0 = load4_stream(pp + s * slice), v1 = load4_stream(pp + (s + 1) * slice);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += v0.v[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += v1.v[e];
+    }
+    for (; s < S; ++s) {
+      const f4 v0 = load4_stream(pp + s * slice);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += v0.v[e];
+    }
+    store4_stream(cp, sum);
   }
 }
 

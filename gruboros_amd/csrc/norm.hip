@@ -46,6 +46,24 @@ __device__ __forceinline__ f4 load_cols(const T* p, int col, int D) {
   return col < D ? io4<T>::load(p + col) : io4<T>::fill(0.0f);
 }
 
+// The fp32 residual stream is touched once per pass and read back only much
+// later (the next block's norm, the backward), so the forward's x loads and
+// x_out stores and the backward's loads of the saved x carry the
+// non-temporal hint; the bf16 outputs (read by the next product) do not.
+// Measured in the cfg3 step: 11.50 -> 11.39 ms.
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4 load_cols_stream(const float* p, int col, int D) {
+  if (col >= D) return io4<float>::fill(0.0f);
+  const f32x4_nt x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(p + col));
+  f4 r;
+  r.v[0] = x[0]; r.v[1] = x[1]; r.v[2] = x[2]; r.v[3] = x[3];
+  return r;
+}
+__device__ __forceinline__ void store4_stream(float* p, const f4& r) {
+  const f32x4_nt x = {r.v[0], r.v[1], r.v[2], r.v[3]};
+  __builtin_nontemporal_store(x, reinterpret_cast<f32x4_nt*>(p));
+}
+
 template <typename Td, typename Ty, int kSteps>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
     const float* __restrict__ x, const Td* __restrict__ delta, const float* __restrict__ w,
@@ -62,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
     const int64_t base = row * D;
     f4 xv[kSteps];
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i) xv[i] = load_cols(x + base, 4 * lane + kColsPerStep * i, D);
+    for (int i = 0; i < kSteps; ++i) xv[i] = load_cols_stream(x + base, 4 * lane + kColsPerStep * i, D);
     if (delta) {
 #pragma unroll
       for (int i = 0; i < kSteps; ++i) {
@@ -93,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
           for (int j = 0; j < 4; ++j) lo.v[j] = yv.v[j] - bf16_to_f32(f32_to_bf16(yv.v[j]));
           io4<bf16_t>::store(y_lo + ybase + col, lo);
         }
-        if (delta && x_out) io4<float>::store(x_out + base + col, xv[i]);
+        if (delta && x_out) store4_stream(x_out + base + col, xv[i]);
       }
     }
     if (lane == 0 && rstd) rstd[row] = r;
@@ -124,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < kSteps; ++i) {
       const int col = 4 * lane + kColsPerStep * i;
-      xh[i] = load_cols(xn + base, col, D);
+      xh[i] = load_cols_stream(xn + base, col, D);
       dyv[i] = load_cols(dy + base, col, D);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {

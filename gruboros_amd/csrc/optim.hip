@@ -47,6 +47,22 @@ __device__ __forceinline__ void update(float& y, float g, float& z, float& v, co
   z = z - h.lr * u;
 }
 
+// The fp32 state streams (parameter, gradient, z, v: 2.4 GB a step at cfg3,
+// each touched once) load and store with the non-temporal hint: measured
+// 504 -> 441 us a step at cfg3. The bf16 copies keep plain stores (with the
+// hint they measured slower: the next step's products read them).
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4 load4_stream(const float* q) {
+  const f32x4_nt x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(q));
+  f4 r;
+  r.v[0] = x[0]; r.v[1] = x[1]; r.v[2] = x[2]; r.v[3] = x[3];
+  return r;
+}
+__device__ __forceinline__ void store4_stream(float* q, const f4& r) {
+  const f32x4_nt x = {r.v[0], r.v[1], r.v[2], r.v[3]};
+  __builtin_nontemporal_store(x, reinterpret_cast<f32x4_nt*>(q));
+}
+
 __global__ __launch_bounds__(kThreads) void sf_adamw_kernel(const Tensor* __restrict__ ts, int nt, Hyper h) {
   // tensor owning this chunk: last t with chunk_start <= blockIdx.x
   int lo = 0, hi = nt - 1;
@@ -63,13 +79,12 @@ __global__ __launch_bounds__(kThreads) void sf_adamw_kernel(const Tensor* __rest
     const int64_t i = base + (static_cast<int64_t>(r) * kThreads + threadIdx.x) * 4;
     if (i >= t.n) break;
     if (vec) {
-      f4 y = io4<float>::load(t.p + i), g = io4<float>::load(t.g + i), z = io4<float>::load(t.z + i),
-         v = io4<float>::load(t.v + i);
+      f4 y = load4_stream(t.p + i), g = load4_stream(t.g + i), z = load4_stream(t.z + i), v = load4_stream(t.v + i);
 #pragma unroll
       for (int j = 0; j < 4; ++j) update(y.v[j], g.v[j], z.v[j], v.v[j], h);
-      io4<float>::store(t.p + i, y);
-      io4<float>::store(t.z + i, z);
-      io4<float>::store(t.v + i, v);
+      store4_stream(t.p + i, y);
+      store4_stream(t.z + i, z);
+      store4_stream(t.v + i, v);
       if (t.p_bf16) {
         if (t.pair_cols > 0) {  // row r = i / C: hi at r * 2C + c, lo at r * 2C + C + c (4 | C)
           const uint32_t C = static_cast<uint32_t>(t.pair_cols);
