@@ -79,6 +79,20 @@ def _f32(w):
     return cache[1]
 
 
+# Bumped whenever any module registers a parameter (a new Parameter object
+# assigned, load_state_dict(assign=True)): decoders then re-gather the
+# parameter objects they watch. In-place changes bump the tensors' own
+# versions instead.
+_PARAM_EPOCH = [0]
+
+
+def _on_param_registered(module, name, param):
+    _PARAM_EPOCH[0] += 1
+
+
+torch.nn.modules.module.register_module_parameter_registration_hook(_on_param_registered)
+
+
 class Decoder:
     def __init__(self, model, batch_size, graph=True, _weak=False):
         reason = unsupported_reason(model, batch_size)
@@ -104,6 +118,8 @@ class Decoder:
         self._graph = None
         self._weights = None
         self._returned = None  # hiddens forward_one returned last (their values still equal the state)
+        self._params, self._epoch = None, -1  # the parameters the weights come from
+        self._sig, self._sig_refs, self._wcache = None, None, None
 
     @property
     def model(self):
@@ -123,6 +139,36 @@ class Decoder:
                    bf16_copy(ff[2].weight, dense=True), bf16_copy(ff[2].bias, dense=True)]
         ws += [_f32(m.token_emb.weight), _f32(m.norm.weight), bf16_copy(m.to_logits.weight, dense=True)]
         return ws
+
+    def _param_list(self):
+        m = self.model
+        ps = []
+        for _, norm, gru, ff_norm, ff, _ in m.layers:
+            ps += [norm.weight, gru.to_hidden_and_gate.weight] + ([gru.to_out.weight] if self.expanded else [])
+            ps += [ff_norm.weight, ff[0].weight, ff[0].bias, ff[2].weight, ff[2].bias]
+        return ps + [m.token_emb.weight, m.norm.weight, m.to_logits.weight]
+
+    def _signature(self):
+        """What _current_weights depends on, cheaply: each parameter's version and storage
+        and the identity of its cached copies (bf16 copy, hi/lo pair, fp32 copy), which the
+        fused optimizer step drops or keeps current when it changes a parameter through a
+        raw pointer. Returns (ids, refs); refs keep the cached copies alive, so their ids
+        are not reused while they are compared."""
+        if self._params is None or self._epoch != _PARAM_EPOCH[0]:
+            self._params, self._epoch = self._param_list(), _PARAM_EPOCH[0]
+        refs = [(p.__dict__.get("_mg_bf16"), p.__dict__.get("_mg_pair"), p.__dict__.get("_mg_f32"))
+                for p in self._params]
+        sig = [(p._version, p.data_ptr(), id(r[0]), id(r[1]), id(r[2])) for p, r in zip(self._params, refs)]
+        return sig, refs
+
+    def _weights_now(self):
+        """_current_weights(), recomputed only when the signature changed (a per-token
+        rebuild of 8 cached copies per layer costs more host time than the token's kernels)."""
+        sig, _ = self._signature()
+        if self._wcache is None or sig != self._sig:
+            self._wcache = self._current_weights()
+            self._sig, self._sig_refs = self._signature()  # after the copies were (re)made
+        return self._wcache
 
     def _launch(self, weights):
         L = lib()
@@ -166,7 +212,7 @@ class Decoder:
         self._graph, self._weights = g, weights
 
     def _run(self):
-        weights = self._current_weights()
+        weights = self._weights_now()
         if not self.graph_enabled:
             self._launch(weights)
             return
@@ -189,7 +235,7 @@ class Decoder:
 
     def hiddens(self):
         """The current per-layer states as prev_hiddens views ([B, 1, Di] fp32)."""
-        return [s.view(self.B, 1, self.Di) for s in self.state]
+        return list(self.state_all.view(len(self.state), self.B, 1, self.Di).unbind(0))
 
     @torch.no_grad()
     def prefill(self, ids):
@@ -223,7 +269,7 @@ class Decoder:
         self.tokens.copy_(tokens.reshape(self.B))
         self._run()
         out = self.state_all.clone()
-        hiddens = [s.view(self.B, 1, self.Di) for s in out.unbind(0)]
+        hiddens = list(out.view(len(self.state), self.B, 1, self.Di).unbind(0))  # one call for all layers
         self._returned = hiddens
         return self.logits.clone().view(self.B, 1, self.V), hiddens
 

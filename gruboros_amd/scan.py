@@ -17,11 +17,16 @@ from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
 # on one stream run in order. Calls on different streams get different
 # workspaces.
 _WORKSPACES = {}
+# Keys of the workspaces a scan has used since their last poll (only those can
+# have set an error bit since; calls that run no scan, such as the decode
+# path's one-token calls, then enqueue no poll).
+_USED = set()
 
 
 def _workspace(device, B, T, Di):
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream, B, T, Di)
+    _USED.add(key)
     ws = _WORKSPACES.get(key)
     if ws is None:
         L = lib()
@@ -35,6 +40,7 @@ def _workspace(device, B, T, Di):
 def release_workspaces():
     """Free the cached look-back workspaces (they are re-made on demand)."""
     _WORKSPACES.clear()
+    _USED.clear()
 
 
 def check_workspaces():
@@ -68,9 +74,11 @@ def poll_workspaces(device=None):
     result reaches the host once that stream has passed the poll;
     raise_pending_errors reads it there."""
     L = lib()
-    for (dev, sid, B, T, Di), ws in list(_WORKSPACES.items()):
-        if device is not None and dev != device.index:
+    for key, ws in list(_WORKSPACES.items()):
+        dev, sid = key[0], key[1]
+        if (device is not None and dev != device.index) or key not in _USED:
             continue
+        _USED.discard(key)
         word = _err_word(dev)
         check(L.mg_scan_workspace_poll(ptr(ws), ctypes.c_void_p(word.data_ptr()), ctypes.c_void_p(sid)),
               "mg_scan_workspace_poll")

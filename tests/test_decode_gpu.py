@@ -224,3 +224,46 @@ def test_model_calls_run_on_the_decoder():
     with torch.enable_grad():  # a call that records gradients stays on the parallel path
         m(toks[0][:, None], prev_hiddens=hid0)
     assert sum(isinstance(d, Decoder) for d in decode._CACHE[m].values()) == 1
+
+
+def test_decoder_follows_optimizer_steps():
+    """A model's cached decoder (minLM.forward's one-token calls) sees the weights a fused
+    SF-AdamW step changed through raw pointers (no version bump; the step keeps the bf16
+    copies and hi/lo pairs current or drops them): after a training step, its logits equal a
+    fresh Decoder's bit for bit, as does a parameter replaced by a new Parameter object."""
+    from gruboros_amd.decode import Decoder
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    B = 2
+    m = _model(dim=256, depth=2, seed=12, expansion=1.5, ff_mult=1.5)
+    opt = AdamWScheduleFree(m.parameters(), lr=1e-2)
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    ids = torch.randint(0, 256, (B, 33), device=DEV, generator=gen)
+    tok = torch.randint(0, 256, (B, 1), device=DEV, generator=gen)
+
+    def one_token():
+        with torch.no_grad():
+            _, hid = m(ids[:, :8], return_prev_hiddens=True)
+            logits, _ = m(tok, return_prev_hiddens=True, prev_hiddens=hid)
+            fresh = Decoder(m, B)
+            fresh.set_hiddens(hid)
+            return logits[:, 0], fresh.step(tok[:, 0]).clone()
+
+    for case in ("before", "after a step", "after another step"):
+        if case != "before":
+            m.train()
+            opt.train()
+            loss = m(ids, return_loss=True)
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            m.eval()
+            opt.eval()
+        routed, fresh = one_token()
+        print(f"case: {case}", flush=True)
+        assert torch.equal(routed, fresh), case
+    with torch.no_grad():
+        w = m.layers[1][4][0].weight
+        m.layers[1][4][0].weight = torch.nn.Parameter(w.detach() * 0.5)
+    routed, fresh = one_token()
+    assert torch.equal(routed, fresh), "replaced parameter"
