@@ -54,6 +54,8 @@ SIGNATURES = {
     "mg_add_rmsnorm_bwd_workspace_bytes": (_c_size, [_c_i64, _c_int]),
     "mg_add_rmsnorm_bwd": (_c_int, [_fp, _fp, _fp, _c_int, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int, _vp,
                                     _c_size, _vp]),
+    "mg_add_rmsnorm_bwd_scaled": (_c_int, [_fp, _fp, _fp, _c_int, _vp, _vp, _fp, _fp, _c_int, _vp, _fp, _c_i64, _c_int,
+                                          _vp, _c_size, _vp]),
     "mg_cross_entropy_partials": (_c_int, [_c_i64]),
     "mg_cross_entropy_fwd_bwd": (_c_int, [_c_int, _vp, _vp, _c_int, _vp, _fp, _vp, _c_i64, _c_int, ctypes.c_float,
                                           _vp]),

@@ -273,12 +273,12 @@ class FinalNormCE(torch.autograd.Function):
     def backward(ctx, g):
         B, T, D = ctx.dims
         xn, w_norm, rstd, embed, dl, wob = ctx.saved_tensors
-        de = gemm.linear_dx(dl, wob, out_dtype=torch.float32)         # fp32 (scaled by g below)
+        de = gemm.linear_dx(dl, wob, out_dtype=torch.float32)         # fp32, unscaled
         dW = gemm.linear_dw(dl, embed) if ctx.needs_input_grad[3] else None
-        de.mul_(g)  # upstream scale (1 / grad_accum in the reference loop), in fp32; no host sync
         if dW is not None:
-            dW.mul_(g)
-        dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, de, None, True, BF16, ctx.has_pending)
+            dW.mul_(g)  # upstream scale (1 / grad_accum in the reference loop), in fp32; no host sync
+        # de's scale by g is the norm backward's, as it loads de (the same fp32 products)
+        dx, dpend, dw_norm = _norm_bwd(xn, w_norm, rstd, de, None, True, BF16, ctx.has_pending, dy_scale=g)
         return (dx.view(B, T, D), dpend.view(B, T, D) if dpend is not None else None,
                 dw_norm if ctx.needs_input_grad[2] else None, dW, None)
 

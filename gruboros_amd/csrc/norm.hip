@@ -121,9 +121,12 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_fwd_kernel(
 template <typename Tg, typename Td, int kSteps>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_kernel(
     const float* __restrict__ xn, const float* __restrict__ w, const float* __restrict__ rstd,
-    const Tg* __restrict__ dy, const float* __restrict__ dres, float* __restrict__ dx, Td* __restrict__ ddelta,
-    float* __restrict__ dw_part, int64_t N, int D) {
+    const Tg* __restrict__ dy, const float* __restrict__ dy_scale, const float* __restrict__ dres,
+    float* __restrict__ dx, Td* __restrict__ ddelta, float* __restrict__ dw_part, int64_t N, int D) {
   __shared__ f4 s_dw[kWaves][64];
+  // dy times a device scalar (the upstream gradient of a loss): the same fp32
+  // product a separate pass over dy would store; x 1 is exact
+  const float sc = dy_scale ? *dy_scale : 1.0f;
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
   f4 wv[kSteps], dwa[kSteps];
@@ -146,6 +149,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_kernel(
       dyv[i] = load_cols(dy + base, col, D);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        dyv[i].v[j] *= sc;
         xh[i].v[j] *= r;
         gv[i].v[j] = dyv[i].v[j] * wv[i].v[j];
         dot += gv[i].v[j] * xh[i].v[j];
@@ -224,8 +228,9 @@ int launch_fwd(const float* x, const void* delta, const float* w, float* x_out, 
 }
 
 template <typename Tg, typename Td>
-int launch_bwd(const float* xn, const float* w, const float* rstd, const void* dy, const float* dres, float* dx,
-               void* ddelta, float* dw, float* dw_part, int64_t N, int D, hipStream_t st) {
+int launch_bwd(const float* xn, const float* w, const float* rstd, const void* dy, const float* dy_scale,
+               const float* dres, float* dx, void* ddelta, float* dw, float* dw_part, int64_t N, int D,
+               hipStream_t st) {
   const int grid = grid_for(N);
   const Tg* g = static_cast<const Tg*>(dy);
   Td* dd = static_cast<Td*>(ddelta);
@@ -233,7 +238,7 @@ int launch_bwd(const float* xn, const float* w, const float* rstd, const void* d
 #define MG_NORM_BWD(S)                                                                                   \
   case S:                                                                                               \
     hipLaunchKernelGGL((add_rmsnorm_bwd_kernel<Tg, Td, S>), dim3(grid), dim3(kThreads), 0, st, xn, w, rstd, \
-                       g, dres, dx, dd, dw_part, N, D);                                                 \
+                       g, dy_scale, dres, dx, dd, dw_part, N, D);                                       \
     break;
     MG_NORM_BWD(1) MG_NORM_BWD(2) MG_NORM_BWD(4) MG_NORM_BWD(8) MG_NORM_BWD(16)
 #undef MG_NORM_BWD
@@ -294,9 +299,10 @@ extern "C" int mg_add_rmsnorm_fwd(const float* x, int delta_dtype, const void* d
              : norm::launch_fwd<float, float>(x, delta, w, x_out, y, nullptr, ldy, rstd, N, D, eps, st);
 }
 
-extern "C" int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* rstd, int dy_dtype, const void* dy,
-                                  const float* dres, float* dx, int ddelta_dtype, void* ddelta, float* dw,
-                                  int64_t N, int D, void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int mg_add_rmsnorm_bwd_scaled(const float* xn, const float* w, const float* rstd, int dy_dtype,
+                                         const void* dy, const float* dy_scale, const float* dres, float* dx,
+                                         int ddelta_dtype, void* ddelta, float* dw, int64_t N, int D,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "mg_add_rmsnorm_bwd";
   int rc;
   if (N < 1 || D < 4 || D % 4) return fail(MG_ERR_ARG, "%s: bad shape N=%lld D=%d (D %% 4 == 0)", fn, (long long)N, D);
@@ -305,6 +311,7 @@ extern "C" int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* 
   if ((rc = norm::check_ptr(fn, "rstd", rstd, 4, true))) return rc;
   if ((rc = norm::check_dtype(fn, "dy", dy_dtype))) return rc;
   if ((rc = norm::check_ptr(fn, "dy", dy, dy_dtype == MG_F32 ? 16 : 8, true))) return rc;
+  if ((rc = norm::check_ptr(fn, "dy_scale", dy_scale, 4, false))) return rc;
   if ((rc = norm::check_ptr(fn, "dres", dres, 16, false))) return rc;
   if ((rc = norm::check_ptr(fn, "dx", dx, 16, false))) return rc;
   if ((rc = norm::check_ptr(fn, "dw", dw, 16, true))) return rc;
@@ -319,8 +326,15 @@ extern "C" int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* 
   float* part = static_cast<float*>(workspace);
   const bool gbf = dy_dtype == MG_BF16, dbf = ddelta && ddelta_dtype == MG_BF16;
   if (gbf)
-    return dbf ? norm::launch_bwd<bf16_t, bf16_t>(xn, w, rstd, dy, dres, dx, ddelta, dw, part, N, D, st)
-               : norm::launch_bwd<bf16_t, float>(xn, w, rstd, dy, dres, dx, ddelta, dw, part, N, D, st);
-  return dbf ? norm::launch_bwd<float, bf16_t>(xn, w, rstd, dy, dres, dx, ddelta, dw, part, N, D, st)
-             : norm::launch_bwd<float, float>(xn, w, rstd, dy, dres, dx, ddelta, dw, part, N, D, st);
+    return dbf ? norm::launch_bwd<bf16_t, bf16_t>(xn, w, rstd, dy, dy_scale, dres, dx, ddelta, dw, part, N, D, st)
+               : norm::launch_bwd<bf16_t, float>(xn, w, rstd, dy, dy_scale, dres, dx, ddelta, dw, part, N, D, st);
+  return dbf ? norm::launch_bwd<float, bf16_t>(xn, w, rstd, dy, dy_scale, dres, dx, ddelta, dw, part, N, D, st)
+             : norm::launch_bwd<float, float>(xn, w, rstd, dy, dy_scale, dres, dx, ddelta, dw, part, N, D, st);
+}
+
+extern "C" int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* rstd, int dy_dtype, const void* dy,
+                                  const float* dres, float* dx, int ddelta_dtype, void* ddelta, float* dw,
+                                  int64_t N, int D, void* workspace, size_t workspace_bytes, void* stream) {
+  return mg_add_rmsnorm_bwd_scaled(xn, w, rstd, dy_dtype, dy, nullptr, dres, dx, ddelta_dtype, ddelta, dw, N, D,
+                                   workspace, workspace_bytes, stream);
 }

@@ -45,7 +45,8 @@ def _fwd(x, delta, w, out_dtype, with_lo=False):
     return x_out, y, rstd, pair
 
 
-def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta):
+def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta, dy_scale=None):
+    """dy_scale: an optional fp32 device scalar dy is multiplied by as it is loaded."""
     N, D = _rows(xn)
     dev = xn.device
     if dy is None:
@@ -60,9 +61,11 @@ def _bwd(xn, w, rstd, dy, dres, want_dx, delta_dtype, want_ddelta):
     L = lib()
     wsb = L.mg_add_rmsnorm_bwd_workspace_bytes(N, D)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-    rc = L.mg_add_rmsnorm_bwd(ptr(xn), ptr(w), ptr(rstd), dtype_code(dy.dtype), ptr(dy), ptr(dres), ptr(dx),
-                              dtype_code(delta_dtype) if want_ddelta else 0, ptr(ddelta), ptr(dw), N, D,
-                              ptr(ws), wsb, stream_of(xn))
+    if dy_scale is not None:
+        dy_scale = dy_scale.detach().to(device=dev, dtype=torch.float32).reshape(1)
+    rc = L.mg_add_rmsnorm_bwd_scaled(ptr(xn), ptr(w), ptr(rstd), dtype_code(dy.dtype), ptr(dy), ptr(dy_scale),
+                                     ptr(dres), ptr(dx), dtype_code(delta_dtype) if want_ddelta else 0,
+                                     ptr(ddelta), ptr(dw), N, D, ptr(ws), wsb, stream_of(xn))
     check(rc, "mg_add_rmsnorm_bwd")
     return dx, ddelta, dw
 

@@ -44,8 +44,8 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch): 202 = 0.2.2, the ABI
- * declared in this file (0.2.1 and 0.2.2 add entry points to 0.2.0 and change
+/* Library version (major*10000 + minor*100 + patch): 203 = 0.2.3, the ABI
+ * declared in this file (0.2.1 to 0.2.3 add entry points to 0.2.0 and change
  * none). */
 int mg_version(void);
 
@@ -233,6 +233,16 @@ int mg_add_rmsnorm_bwd(const float* xn, const float* w, const float* rstd,
                        float* dx, int ddelta_dtype, void* ddelta, float* dw,
                        int64_t N, int D, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* mg_add_rmsnorm_bwd with dy multiplied by the fp32 device scalar *dy_scale
+ * (NULL: 1) as it is loaded: the upstream gradient of a loss (reference
+ * train.py:800, (loss / grad_accum).backward()) applied without a separate
+ * pass over dy; results equal scaling dy in fp32 first. */
+int mg_add_rmsnorm_bwd_scaled(const float* xn, const float* w, const float* rstd,
+                              int dy_dtype, const void* dy, const float* dy_scale,
+                              const float* dres, float* dx, int ddelta_dtype,
+                              void* ddelta, float* dw, int64_t N, int D,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Cross-entropy loss head, forward and gradient in one pass.
