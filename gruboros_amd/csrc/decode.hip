@@ -27,6 +27,12 @@
 // values; the residual stream and the scan state are fp32, and the scan
 // output joins the residual stream unrounded (expansion 1) or reaches to_out
 // as bf16, whose fp32 sum joins it unrounded.
+//
+// The *_f32 entry points run the same kernels for a model kept in fp32
+// (reference generate.py:277 --use-f32): fp32 weights, biases and branch
+// outputs, no rounding point; each lane then reads 32 bytes of a weight row
+// per 8 elements, and the staged input rows take twice the LDS (at batch 5-8
+// the staged rows are at most 4096 long).
 
 #include <algorithm>
 
@@ -44,6 +50,25 @@ constexpr int kMaxStaged = 8192;  // longest bf16 input row a workgroup stages i
 
 enum Mode { MINGRU = 0, FF1 = 1, FF2 = 2, HEAD = 3, TO_OUT = 4 };
 
+// Element type of a decode path (weights, biases, staged rows, branch outputs).
+template <typename T> struct Elem;
+template <> struct Elem<bf16_t> {
+  static constexpr int kVec = 1;  // uint4 per 8 elements
+  __device__ __forceinline__ static float round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+  __device__ __forceinline__ static float get(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+  __device__ __forceinline__ static void put(bf16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+template <> struct Elem<float> {
+  static constexpr int kVec = 2;
+  __device__ __forceinline__ static float round(float x) { return x; }
+  __device__ __forceinline__ static float get(const float* p, int64_t i) { return p[i]; }
+  __device__ __forceinline__ static void put(float* p, int64_t i, float v) { p[i] = v; }
+};
+// 8 consecutive elements of a row
+template <typename T> struct Vec8 {
+  uint4 q[Elem<T>::kVec];
+};
+
 struct Args {
   int B, D, K, rows;             // batch, model dim, reduction length, output rows
   int Di;                        // MINGRU: scan channels (rows Di .. 2 Di - 1 are the gates)
@@ -51,19 +76,17 @@ struct Args {
   const int64_t* tokens;         // MINGRU of layer 0: x_in rows are emb[tokens[b]]
   const float* emb;              // [V, D]
   const float* x_in;             // [B, D] fp32 residual stream
-  const bf16_t* pending;         // [B, D] bf16 branch output to add first (nullable)
+  const void* pending;           // [B, D] branch output (element type) to add first (nullable)
   float* x_out;                  // MINGRU: x_in + pending + h
   const float* norm_w;           // [D]
-  const bf16_t* W;               // [rows, K] bf16
-  const bf16_t* bias;            // [rows] bf16 (nullable)
+  const void* W;                 // [rows, K]
+  const void* bias;              // [rows] (nullable)
   float* state;                  // MINGRU: [B, Di] fp32 recurrence state, in place
-  bf16_t* h_out;                 // MINGRU with to_out: the step's output h [B, Di] as bf16 (else null)
-  const bf16_t* act;             // FF2: [B, K] bf16 input; TO_OUT: h [B, Di]
-  bf16_t* out;                   // FF1: act [B, F]; FF2: pending [B, D]; HEAD: logits [B, V]
+  void* h_out;                   // MINGRU with to_out: the step's output h [B, Di] (else null)
+  const void* act;               // FF2: [B, K] input; TO_OUT: h [B, Di]
+  void* out;                     // FF1: act [B, F]; FF2: pending [B, D]; HEAD: logits [B, V]
   float eps;
 };
-
-__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 // Sum each of a lane's N values over the wave (N a power of two <= 64) with
 // log2(N) halving exchanges plus a butterfly: at the exchange with lane ^ o
@@ -118,7 +141,7 @@ enum Src { SRC_X = 0, SRC_X_PENDING = 1, SRC_TOKENS = 2 };
 
 // Residual-stream value (b, c) before the norm: x_in (or the embedding row)
 // plus the pending branch output.
-template <int SRC>
+template <typename T, int SRC>
 __device__ __forceinline__ float stream_at(const Args& a, int b, int c) {
   float x;
   if constexpr (SRC == SRC_TOKENS) {
@@ -127,12 +150,12 @@ __device__ __forceinline__ float stream_at(const Args& a, int b, int c) {
   } else {
     x = a.x_in[static_cast<int64_t>(b) * a.D + c];
   }
-  if constexpr (SRC == SRC_X_PENDING) x += bf16_to_f32(a.pending[static_cast<int64_t>(b) * a.D + c]);
+  if constexpr (SRC == SRC_X_PENDING) x += Elem<T>::get(static_cast<const T*>(a.pending), static_cast<int64_t>(b) * a.D + c);
   return x;
 }
 
 // The same for columns c .. c + 3 (c a multiple of 4; rows are 16-byte aligned).
-template <int SRC>
+template <typename T, int SRC>
 __device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
   f4 x;
   if constexpr (SRC == SRC_TOKENS) {
@@ -142,7 +165,7 @@ __device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
     x = io4<float>::load(a.x_in + static_cast<int64_t>(b) * a.D + c);
   }
   if constexpr (SRC == SRC_X_PENDING) {
-    const f4 p = io4<bf16_t>::load(a.pending + static_cast<int64_t>(b) * a.D + c);
+    const f4 p = io4<T>::load(static_cast<const T*>(a.pending) + static_cast<int64_t>(b) * a.D + c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) x.v[e] += p.v[e];
   }
@@ -155,12 +178,14 @@ __device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
 // 1 where there is no norm). The input rows are staged in a static LDS array
 // of BP x 512 NC bf16 values (at most 8 x 8192 = 128 KiB, within gfx950's
 // 160 KiB per workgroup).
-template <int MODE, int SRC, int BP, int R, int NC, int CPT>
+template <typename T, int MODE, int SRC, int BP, int R, int NC, int CPT>
 __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
   static_assert(NC * 512 <= kMaxStaged, "staged row length");
-  constexpr bool kStagedInput = MODE == FF2 || MODE == TO_OUT;  // bf16 input rows, no norm
-  __shared__ uint4 lds[BP * NC * 64];
-  bf16_t* s_in = reinterpret_cast<bf16_t*>(lds);  // [BP][K]
+  constexpr bool kStagedInput = MODE == FF2 || MODE == TO_OUT;  // input rows as they are, no norm
+  constexpr int kV = Elem<T>::kVec;
+  __shared__ uint4 lds[BP * NC * 64 * kV];
+  T* s_in = reinterpret_cast<T*>(lds);  // [BP][K]
+  const T* W = static_cast<const T*>(a.W);
   __shared__ float s_part[kWaves][BP];
   __shared__ float s_rstd[BP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -174,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) rows[r] = MODE == MINGRU ? g + r * a.Di : g * R + r;
   const bool active = rows[0] < (MODE == MINGRU ? a.Di : a.rows);
-  uint4 wv[NC][R];
+  Vec8<T> wv[NC][R];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -183,7 +208,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
       // past the end are never used, chunks past K are skipped below
       const int k0 = min(c * 512 + lane * 8, K - 8);
       const int row = active ? rows[r] : 0;
-      wv[c][r] = *reinterpret_cast<const uint4*>(a.W + static_cast<int64_t>(row) * K + k0);
+#pragma unroll
+      for (int j = 0; j < kV; ++j)
+        wv[c][r].q[j] = reinterpret_cast<const uint4*>(W + static_cast<int64_t>(row) * K + k0)[j];
     }
 
   // 1. the B input rows, as bf16, into LDS (rows B..BP-1 zero)
@@ -191,15 +218,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     // kBatch 16-byte loads per thread in flight before their LDS stores (a
     // load-store pair per iteration would wait out one memory latency each)
     constexpr int kBatch = 8;
-    const int n16 = BP * (K / 8);
+    constexpr int kPer16 = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
+    const int n16 = BP * (K / kPer16);
+    const T* act = static_cast<const T*>(a.act);
     for (int i0 = 0; i0 < n16; i0 += kBatch * kThreads) {
       uint4 v[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int i = i0 + u * kThreads + tid;
-        const int b = i / (K / 8), c8 = i % (K / 8);
+        const int b = i / (K / kPer16), c16 = i % (K / kPer16);
         v[u] = make_uint4(0, 0, 0, 0);
-        if (i < n16 && b < a.B) v[u] = *reinterpret_cast<const uint4*>(a.act + static_cast<int64_t>(b) * K + c8 * 8);
+        if (i < n16 && b < a.B)
+          v[u] = *reinterpret_cast<const uint4*>(act + static_cast<int64_t>(b) * K + c16 * kPer16);
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
@@ -221,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const int c = 4 * (tid + q * kThreads);
-        const f4 x = stream4_at<SRC>(a, min(b, a.B - 1), min(c, K - 4));  // unconditional load
+        const f4 x = stream4_at<T, SRC>(a, min(b, a.B - 1), min(c, K - 4));  // unconditional load
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           xr[b][4 * q + e] = (b < a.B && c < K) ? x.v[e] : 0.0f;
@@ -252,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
           f4 y;
 #pragma unroll
           for (int e = 0; e < 4; ++e) y.v[e] = xr[b][4 * q + e] * s_rstd[b] * w.v[e];
-          io4<bf16_t>::store(s_in + b * K + c, y);
+          io4<T>::store(s_in + b * K + c, y);
         }
       }
     }
@@ -272,15 +302,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     if (k0 >= K) break;
 #pragma unroll
     for (int b = 0; b < BP; ++b) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(s_in + b * K + k0);
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+      if constexpr (kV == 1) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(s_in + b * K + k0);
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t ww[4] = {wv[c][r].x, wv[c][r].y, wv[c][r].z, wv[c][r].w};
+        for (int r = 0; r < R; ++r) {
+          const uint4 wq = wv[c][r].q[0];
+          const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q)  // two bf16 products per instruction, fp32 accumulation
-          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, ww[q]),
-                                                      __builtin_bit_cast(bf16x2, xw[q]), acc[r][b], false);
+          for (int q = 0; q < 4; ++q)  // two bf16 products per instruction, fp32 accumulation
+            acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, ww[q]),
+                                                        __builtin_bit_cast(bf16x2, xw[q]), acc[r][b], false);
+        }
+      } else {
+        const float4 x0 = reinterpret_cast<const float4*>(s_in + b * K + k0)[0];
+        const float4 x1 = reinterpret_cast<const float4*>(s_in + b * K + k0)[1];
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint4 w0 = wv[c][r].q[0], w1 = wv[c][r].q[1];
+          const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][b] = __builtin_fmaf(__uint_as_float(ww[e]), xs[e], acc[r][b]);
+        }
       }
     }
   }
@@ -300,67 +344,165 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
     const float other = __shfl_xor(sum, 32, 64);
     if (lane % kCopies || r != 0 || b >= a.B) return;
     const int d = g;
-    const float hid = round_bf16(sum), gate = round_bf16(other);
+    const float hid = Elem<T>::round(sum), gate = Elem<T>::round(other);
     float coef, v;
     fwd_coeffs(gate, hid, coef, v);
     float* st = a.state + static_cast<int64_t>(b) * a.Di + d;
     const float h = coef * *st + v;
     *st = h;
-    if (a.h_out) a.h_out[static_cast<int64_t>(b) * a.Di + d] = f32_to_bf16(h);
-    else a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + h;
+    if (a.h_out) Elem<T>::put(static_cast<T*>(a.h_out), static_cast<int64_t>(b) * a.Di + d, h);
+    else a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<T, SRC>(a, b, d) + h;
     return;
   }
   if (lane % kCopies || b >= a.B) return;
   if constexpr (MODE == TO_OUT) {
     const int d = rows[0] + r;
-    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<SRC>(a, b, d) + sum;
+    a.x_out[static_cast<int64_t>(b) * a.D + d] = stream_at<T, SRC>(a, b, d) + sum;
     return;
   }
-  bf16_t* o = a.out + static_cast<int64_t>(b) * a.rows + rows[0] + r;
+  T* o = static_cast<T*>(a.out);
+  const int64_t oi = static_cast<int64_t>(b) * a.rows + rows[0] + r;
   if constexpr (MODE == FF1) {
-    *o = f32_to_bf16(gelu(round_bf16(sum + bf16_to_f32(a.bias[rows[0] + r]))));
+    Elem<T>::put(o, oi, gelu(Elem<T>::round(sum + Elem<T>::get(static_cast<const T*>(a.bias), rows[0] + r))));
   } else if constexpr (MODE == FF2) {
-    *o = f32_to_bf16(sum + bf16_to_f32(a.bias[rows[0] + r]));
+    Elem<T>::put(o, oi, sum + Elem<T>::get(static_cast<const T*>(a.bias), rows[0] + r));
   } else {
-    *o = f32_to_bf16(sum);
+    Elem<T>::put(o, oi, sum);
   }
 }
 
 // The staged-input modes (FF2, TO_OUT) take K <= 8192 (NC 8 up to 4096, else
 // 16); the norm modes K = D <= 2048 (NC 2 up to 1024, else 4). Every wave's
-// lane covers its chunks with K <= 512 NC, which check_shape guarantees.
-template <int MODE, int SRC, int BP, int R>
+// lane covers its chunks with K <= 512 NC, which check_shape guarantees. fp32
+// rows take twice the LDS, so at batch 5-8 an fp32 staged row is at most 4096
+// long (the 16-chunk variant is not built there).
+template <typename T, int MODE, int SRC, int BP, int R>
 int launch_bp(const Args& a, dim3 grid, hipStream_t st) {
   if constexpr (MODE == FF2 || MODE == TO_OUT) {
-    if (a.K <= 4096) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 8, 1>), grid, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 16, 1>), grid, dim3(kThreads), 0, st, a);
+    if (a.K <= 4096) {
+      hipLaunchKernelGGL((decode_kernel<T, MODE, SRC, BP, R, 8, 1>), grid, dim3(kThreads), 0, st, a);
+    } else {
+      if constexpr (sizeof(T) == 4 && BP == 8)
+        return fail(MG_ERR_ARG, "mg_decode: fp32 staged rows of %d > 4096 at batch %d", a.K, a.B);
+      else
+        hipLaunchKernelGGL((decode_kernel<T, MODE, SRC, BP, R, 16, 1>), grid, dim3(kThreads), 0, st, a);
+    }
   } else {
-    if (a.K <= 1024) hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 2, 4>), grid, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL((decode_kernel<MODE, SRC, BP, R, 4, 8>), grid, dim3(kThreads), 0, st, a);
+    if (a.K <= 1024) hipLaunchKernelGGL((decode_kernel<T, MODE, SRC, BP, R, 2, 4>), grid, dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL((decode_kernel<T, MODE, SRC, BP, R, 4, 8>), grid, dim3(kThreads), 0, st, a);
   }
   return check_launch("mg_decode");
 }
 
-template <int MODE, int SRC, int R>
+template <typename T, int MODE, int SRC, int R>
 int launch(const Args& a, hipStream_t st) {
   const int groups = MODE == MINGRU ? a.Di : a.rows / R;
   const dim3 grid((groups + kWaves - 1) / kWaves);
   const int BP = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
   switch (BP) {
-    case 1: return launch_bp<MODE, SRC, 1, R>(a, grid, st);
-    case 2: return launch_bp<MODE, SRC, 2, R>(a, grid, st);
-    case 4: return launch_bp<MODE, SRC, 4, R>(a, grid, st);
-    default: return launch_bp<MODE, SRC, 8, R>(a, grid, st);
+    case 1: return launch_bp<T, MODE, SRC, 1, R>(a, grid, st);
+    case 2: return launch_bp<T, MODE, SRC, 2, R>(a, grid, st);
+    case 4: return launch_bp<T, MODE, SRC, 4, R>(a, grid, st);
+    default: return launch_bp<T, MODE, SRC, 8, R>(a, grid, st);
   }
 }
 
 // kmax: 2048 for the model dimension (norm prologue), 8192 for a staged input
-// row (the FeedForward width, to_out's Di)
+// row (the FeedForward width, to_out's Di); fp32 staged rows at batch 5-8: 4096
 inline int check_shape(const char* fn, int B, int K, int kmax) {
   if (B < 1 || B > kMaxB) return fail(MG_ERR_ARG, "%s: batch %d outside [1, %d]", fn, B, kMaxB);
   if (K < 8 || K % 8 || K > kmax)
     return fail(MG_ERR_ARG, "%s: length %d must be a positive multiple of 8, at most %d", fn, K, kmax);
   return MG_OK;
+}
+template <typename T>
+int staged_max(int B) {
+  return sizeof(T) == 4 && B > 4 ? 4096 : kMaxStaged;
+}
+
+// Alignment of the element-type vectors read 16 (weights, staged rows) or 4
+// elements (pending) at a time.
+template <typename T>
+constexpr size_t kPendAlign = 4 * sizeof(T);
+
+template <typename T>
+int mingru_impl(const char* fn, int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                const float* x_in, const void* pending, float* x_out, void* h_out, const float* norm_w,
+                const void* w_hg, float* state, float eps, void* stream) {
+  if (int rc = check_shape(fn, B, D, 2048)) return rc;
+  if (h_out)
+    if (int rc = check_shape(fn, B, Di, staged_max<T>(B))) return rc;
+  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !(h_out || x_out) || !norm_w || !w_hg || !state)
+    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
+  if (!aligned(w_hg, 16) || !aligned(norm_w, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
+      (pending && !aligned(pending, kPendAlign<T>)))
+    return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not %zu-byte aligned",
+                fn, kPendAlign<T>);
+  Args a{};
+  a.B = B; a.D = D; a.Di = Di; a.K = D; a.rows = 2 * Di; a.V = V;
+  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = pending;
+  a.x_out = x_out; a.h_out = h_out; a.norm_w = norm_w; a.W = w_hg; a.state = state; a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tokens) return launch<T, MINGRU, SRC_TOKENS, 2>(a, st);
+  if (pending) return launch<T, MINGRU, SRC_X_PENDING, 2>(a, st);
+  return launch<T, MINGRU, SRC_X, 2>(a, st);
+}
+
+template <typename T>
+int to_out_impl(const char* fn, int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                const float* x_in, const void* pending, const void* h, const void* w_out, float* x_out,
+                void* stream) {
+  if (int rc = check_shape(fn, B, D, 2048)) return rc;
+  if (int rc = check_shape(fn, B, Di, staged_max<T>(B))) return rc;
+  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !h || !w_out || !x_out)
+    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
+  if (!aligned(w_out, 16) || !aligned(h, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
+      (pending && !aligned(pending, kPendAlign<T>)))
+    return fail(MG_ERR_ARG, "%s: weight, h, emb or x_in not 16-byte aligned, or pending not %zu-byte aligned", fn,
+                kPendAlign<T>);
+  Args a{};
+  a.B = B; a.D = D; a.Di = Di; a.K = Di; a.rows = D; a.V = V;
+  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = pending;
+  a.act = h; a.W = w_out; a.x_out = x_out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tokens) return launch<T, TO_OUT, SRC_TOKENS, 1>(a, st);
+  if (pending) return launch<T, TO_OUT, SRC_X_PENDING, 1>(a, st);
+  return launch<T, TO_OUT, SRC_X, 1>(a, st);
+}
+
+template <typename T>
+int ff_impl(const char* fn, int B, int D, int F, const float* x, const float* norm_w, const void* w1, const void* b1,
+            void* act, const void* w2, const void* b2, void* pending_out, float eps, void* stream) {
+  if (int rc = check_shape(fn, B, D, 2048)) return rc;
+  if (int rc = check_shape(fn, B, F, staged_max<T>(B))) return rc;
+  if (!x || !norm_w || !w1 || !b1 || !act || !w2 || !b2 || !pending_out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
+  if (F % 4 || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(act, 16) || !aligned(x, 16) || !aligned(norm_w, 16))
+    return fail(MG_ERR_ARG, "%s: F %% 4, 16-byte weights, act, x and norm weight required", fn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Args a{};
+  a.B = B; a.D = D; a.K = D; a.rows = F;
+  a.x_in = x; a.norm_w = norm_w; a.W = w1; a.bias = b1; a.out = act; a.eps = eps;
+  if (int rc = launch<T, FF1, SRC_X, 4>(a, st)) return rc;
+  Args c{};
+  c.B = B; c.D = D; c.K = F; c.rows = D;
+  c.act = act; c.W = w2; c.bias = b2; c.out = pending_out;
+  return launch<T, FF2, SRC_X, 1>(c, st);
+}
+
+template <typename T>
+int head_impl(const char* fn, int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
+              const void* w_out, void* logits, float eps, void* stream) {
+  if (int rc = check_shape(fn, B, D, 2048)) return rc;
+  if (V < 1 || !x_in || !norm_w || !w_out || !logits) return fail(MG_ERR_ARG, "%s: bad argument", fn);
+  if (!aligned(w_out, 16) || !aligned(x_in, 16) || !aligned(norm_w, 16) || (pending && !aligned(pending, kPendAlign<T>)))
+    return fail(MG_ERR_ARG, "%s: weight, x_in or norm weight not 16-byte aligned, or pending not %zu-byte aligned", fn,
+                kPendAlign<T>);
+  Args a{};
+  a.B = B; a.D = D; a.K = D; a.rows = V;
+  a.x_in = x_in; a.pending = pending; a.norm_w = norm_w; a.W = w_out; a.out = logits; a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (pending) return launch<T, HEAD, SRC_X_PENDING, 1>(a, st);
+  return launch<T, HEAD, SRC_X, 1>(a, st);
 }
 
 }  // namespace decode
@@ -371,100 +513,63 @@ using namespace mg;
 extern "C" int mg_decode_mingru(int B, int D, const int64_t* tokens, const float* emb, int V, const float* x_in,
                                 const void* pending, float* x_out, const float* norm_w, const void* w_hg,
                                 float* state, float eps, void* stream) {
-  const char* fn = "mg_decode_mingru";
-  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
-  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !x_out || !norm_w || !w_hg || !state)
-    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
-  if (!aligned(w_hg, 16) || !aligned(norm_w, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
-      (pending && !aligned(pending, 8)))
-    return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
-  decode::Args a{};
-  a.B = B; a.D = D; a.Di = D; a.K = D; a.rows = 2 * D; a.V = V;
-  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
-  a.x_out = x_out; a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w_hg); a.state = state; a.eps = eps;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (tokens) return decode::launch<decode::MINGRU, decode::SRC_TOKENS, 2>(a, st);
-  if (pending) return decode::launch<decode::MINGRU, decode::SRC_X_PENDING, 2>(a, st);
-  return decode::launch<decode::MINGRU, decode::SRC_X, 2>(a, st);
+  if (!x_out) return fail(MG_ERR_ARG, "mg_decode_mingru: x_out is NULL");
+  return decode::mingru_impl<bf16_t>("mg_decode_mingru", B, D, D, tokens, emb, V, x_in, pending, x_out, nullptr,
+                                     norm_w, w_hg, state, eps, stream);
 }
 
 extern "C" int mg_decode_mingru_expanded(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
                                          const float* x_in, const void* pending, void* h_out, const float* norm_w,
                                          const void* w_hg, float* state, float eps, void* stream) {
-  const char* fn = "mg_decode_mingru_expanded";
-  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
-  if (int rc = decode::check_shape(fn, B, Di, decode::kMaxStaged)) return rc;
-  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !h_out || !norm_w || !w_hg || !state)
-    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
-  if (!aligned(w_hg, 16) || !aligned(norm_w, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
-      (pending && !aligned(pending, 8)))
-    return fail(MG_ERR_ARG, "%s: weight, norm weight, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
-  decode::Args a{};
-  a.B = B; a.D = D; a.Di = Di; a.K = D; a.rows = 2 * Di; a.V = V;
-  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
-  a.h_out = static_cast<bf16_t*>(h_out); a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w_hg);
-  a.state = state; a.eps = eps;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (tokens) return decode::launch<decode::MINGRU, decode::SRC_TOKENS, 2>(a, st);
-  if (pending) return decode::launch<decode::MINGRU, decode::SRC_X_PENDING, 2>(a, st);
-  return decode::launch<decode::MINGRU, decode::SRC_X, 2>(a, st);
+  if (!h_out) return fail(MG_ERR_ARG, "mg_decode_mingru_expanded: h_out is NULL");
+  return decode::mingru_impl<bf16_t>("mg_decode_mingru_expanded", B, D, Di, tokens, emb, V, x_in, pending, nullptr,
+                                     h_out, norm_w, w_hg, state, eps, stream);
 }
 
 extern "C" int mg_decode_to_out(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
                                 const float* x_in, const void* pending, const void* h, const void* w_out,
                                 float* x_out, void* stream) {
-  const char* fn = "mg_decode_to_out";
-  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
-  if (int rc = decode::check_shape(fn, B, Di, decode::kMaxStaged)) return rc;
-  if (!(tokens ? (emb != nullptr && V >= 1) : x_in != nullptr) || !h || !w_out || !x_out)
-    return fail(MG_ERR_ARG, "%s: NULL pointer or empty embedding", fn);
-  if (!aligned(w_out, 16) || !aligned(h, 16) || (tokens ? !aligned(emb, 16) : !aligned(x_in, 16)) ||
-      (pending && !aligned(pending, 8)))
-    return fail(MG_ERR_ARG, "%s: weight, h, emb or x_in not 16-byte aligned, or pending not 8-byte aligned", fn);
-  decode::Args a{};
-  a.B = B; a.D = D; a.Di = Di; a.K = Di; a.rows = D; a.V = V;
-  a.tokens = tokens; a.emb = emb; a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending);
-  a.act = static_cast<const bf16_t*>(h); a.W = static_cast<const bf16_t*>(w_out); a.x_out = x_out;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (tokens) return decode::launch<decode::TO_OUT, decode::SRC_TOKENS, 1>(a, st);
-  if (pending) return decode::launch<decode::TO_OUT, decode::SRC_X_PENDING, 1>(a, st);
-  return decode::launch<decode::TO_OUT, decode::SRC_X, 1>(a, st);
+  return decode::to_out_impl<bf16_t>("mg_decode_to_out", B, D, Di, tokens, emb, V, x_in, pending, h, w_out, x_out,
+                                     stream);
 }
 
 extern "C" int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
                             const void* b1, void* act, const void* w2, const void* b2, void* pending_out, float eps,
                             void* stream) {
-  const char* fn = "mg_decode_ff";
-  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
-  if (int rc = decode::check_shape(fn, B, F, 8192)) return rc;
-  if (!x || !norm_w || !w1 || !b1 || !act || !w2 || !b2 || !pending_out) return fail(MG_ERR_ARG, "%s: NULL pointer", fn);
-  if (F % 4 || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(act, 16) || !aligned(x, 16) || !aligned(norm_w, 16))
-    return fail(MG_ERR_ARG, "%s: F %% 4, 16-byte weights, act, x and norm weight required", fn);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  decode::Args a{};
-  a.B = B; a.D = D; a.K = D; a.rows = F;
-  a.x_in = x; a.norm_w = norm_w; a.W = static_cast<const bf16_t*>(w1); a.bias = static_cast<const bf16_t*>(b1);
-  a.out = static_cast<bf16_t*>(act); a.eps = eps;
-  if (int rc = decode::launch<decode::FF1, decode::SRC_X, 4>(a, st)) return rc;
-  decode::Args c{};
-  c.B = B; c.D = D; c.K = F; c.rows = D;
-  c.act = static_cast<const bf16_t*>(act); c.W = static_cast<const bf16_t*>(w2); c.bias = static_cast<const bf16_t*>(b2);
-  c.out = static_cast<bf16_t*>(pending_out);
-  return decode::launch<decode::FF2, decode::SRC_X, 1>(c, st);
+  return decode::ff_impl<bf16_t>("mg_decode_ff", B, D, F, x, norm_w, w1, b1, act, w2, b2, pending_out, eps, stream);
 }
 
 extern "C" int mg_decode_head(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
                               const void* w_out, void* logits, float eps, void* stream) {
-  const char* fn = "mg_decode_head";
-  if (int rc = decode::check_shape(fn, B, D, 2048)) return rc;
-  if (V < 1 || !x_in || !norm_w || !w_out || !logits) return fail(MG_ERR_ARG, "%s: bad argument", fn);
-  if (!aligned(w_out, 16) || !aligned(x_in, 16) || !aligned(norm_w, 16) || (pending && !aligned(pending, 8)))
-    return fail(MG_ERR_ARG, "%s: weight, x_in or norm weight not 16-byte aligned, or pending not 8-byte aligned", fn);
-  decode::Args a{};
-  a.B = B; a.D = D; a.K = D; a.rows = V;
-  a.x_in = x_in; a.pending = static_cast<const bf16_t*>(pending); a.norm_w = norm_w;
-  a.W = static_cast<const bf16_t*>(w_out); a.out = static_cast<bf16_t*>(logits); a.eps = eps;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (pending) return decode::launch<decode::HEAD, decode::SRC_X_PENDING, 1>(a, st);
-  return decode::launch<decode::HEAD, decode::SRC_X, 1>(a, st);
+  return decode::head_impl<bf16_t>("mg_decode_head", B, D, V, x_in, pending, norm_w, w_out, logits, eps, stream);
+}
+
+// fp32 models (reference generate.py --use-f32): the same steps over fp32
+// weights, biases, branch outputs and logits.
+extern "C" int mg_decode_mingru_f32(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                    const float* x_in, const float* pending, float* x_out, float* h_out,
+                                    const float* norm_w, const float* w_hg, float* state, float eps, void* stream) {
+  if (!x_out == !h_out) return fail(MG_ERR_ARG, "mg_decode_mingru_f32: exactly one of x_out and h_out");
+  if (!h_out && Di != D) return fail(MG_ERR_ARG, "mg_decode_mingru_f32: Di %d != D %d needs h_out", Di, D);
+  return decode::mingru_impl<float>("mg_decode_mingru_f32", B, D, Di, tokens, emb, V, x_in, pending, x_out, h_out,
+                                    norm_w, w_hg, state, eps, stream);
+}
+
+extern "C" int mg_decode_to_out_f32(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                    const float* x_in, const float* pending, const float* h, const float* w_out,
+                                    float* x_out, void* stream) {
+  return decode::to_out_impl<float>("mg_decode_to_out_f32", B, D, Di, tokens, emb, V, x_in, pending, h, w_out, x_out,
+                                    stream);
+}
+
+extern "C" int mg_decode_ff_f32(int B, int D, int F, const float* x, const float* norm_w, const float* w1,
+                                const float* b1, float* act, const float* w2, const float* b2, float* pending_out,
+                                float eps, void* stream) {
+  return decode::ff_impl<float>("mg_decode_ff_f32", B, D, F, x, norm_w, w1, b1, act, w2, b2, pending_out, eps,
+                                stream);
+}
+
+extern "C" int mg_decode_head_f32(int B, int D, int V, const float* x_in, const float* pending, const float* norm_w,
+                                  const float* w_out, float* logits, float eps, void* stream) {
+  return decode::head_impl<float>("mg_decode_head_f32", B, D, V, x_in, pending, norm_w, w_out, logits, eps, stream);
 }

@@ -16,10 +16,13 @@ the host.
 
 Requirements (``unsupported_reason``): bf16 activations, i.e. a minLM built
 with ``compute_dtype=torch.bfloat16`` over fp32 parameters, or one whose
-parameters were cast with ``.to(torch.bfloat16)`` (generate.py:140-141); no
-conv; dropout only in eval mode (where it is the identity); batch 1..8; dim
-a multiple of 8 and at most 2048; the scan width Di = dim * expansion and
-the FeedForward width multiples of 8 and at most 8192.
+parameters were cast with ``.to(torch.bfloat16)`` (generate.py:140-141); or
+a model kept in fp32 (generate.py --use-f32: fp32 parameters and no
+compute_dtype), which runs the *_f32 steps (fp32 weights and activations, no
+rounding point); no conv; dropout only in eval mode (where it is the
+identity); batch 1..8; dim a multiple of 8 and at most 2048; the scan width
+Di = dim * expansion and the FeedForward width multiples of 8 and at most
+8192 (4096 for an fp32 model at batch 5-8).
 """
 import weakref
 
@@ -45,15 +48,17 @@ def unsupported_reason(model, batch_size):
     from .mingru.minGRU import minGRU
 
     cd, _ = model._dtypes()
-    if cd != torch.bfloat16:
-        return ("Decoder needs bf16 activations: a minLM built with compute_dtype=torch.bfloat16, or one cast "
-                "with .to(torch.bfloat16)")
+    f32 = cd == torch.float32 and model.token_emb.weight.dtype == torch.float32
+    if cd != torch.bfloat16 and not f32:
+        return ("Decoder needs bf16 activations (a minLM built with compute_dtype=torch.bfloat16, or one cast "
+                "with .to(torch.bfloat16)) or an fp32 model; float16 parameters run the parallel path")
     if not 1 <= batch_size <= MAX_BATCH:
         return f"Decoder batch {batch_size} outside [1, {MAX_BATCH}]"
     D, Di, F, V = _widths(model)
-    if D % 8 or D > MAX_DIM or Di % 8 or Di > MAX_STAGED or F % 8 or F > MAX_STAGED or V < 1:
+    staged = MAX_STAGED if not f32 or batch_size <= 4 else MAX_STAGED // 2
+    if D % 8 or D > MAX_DIM or Di % 8 or Di > staged or F % 8 or F > staged or V < 1:
         return (f"Decoder widths: dim {D} (multiple of 8, <= {MAX_DIM}), scan width {Di} and FeedForward width "
-                f"{F} (multiples of 8, <= {MAX_STAGED})")
+                f"{F} (multiples of 8, <= {staged})")
     for conv, _, gru, _, ff, dropout in model.layers:
         if conv is not None:
             return "Decoder does not run the causal conv (enable_conv)"
@@ -104,15 +109,17 @@ class Decoder:
         self._model = weakref.ref(model) if _weak else (lambda m=model: m)
         self.B, self.graph_enabled = batch_size, graph
         self.D, self.Di, self.F, self.V = _widths(model)
+        self.f32 = model._dtypes()[0] == torch.float32  # an fp32 model: the *_f32 steps
+        et = torch.float32 if self.f32 else torch.bfloat16  # weights, branch outputs, logits
         self.expanded = self.Di != self.D
         B, D, Di, F, V, L = self.B, self.D, self.Di, self.F, self.V, len(model.layers)
         self.device = dev
         self.tokens = torch.zeros(B, dtype=torch.int64, device=dev)
         self.x = [torch.zeros(B, D, device=dev) for _ in range(2)]
-        self.pending = torch.zeros(B, D, dtype=torch.bfloat16, device=dev)
-        self.h = torch.zeros(B, Di, dtype=torch.bfloat16, device=dev) if self.expanded else None
-        self.act = torch.zeros(B, F, dtype=torch.bfloat16, device=dev)
-        self.logits = torch.zeros(B, V, dtype=torch.bfloat16, device=dev)
+        self.pending = torch.zeros(B, D, dtype=et, device=dev)
+        self.h = torch.zeros(B, Di, dtype=et, device=dev) if self.expanded else None
+        self.act = torch.zeros(B, F, dtype=et, device=dev)
+        self.logits = torch.zeros(B, V, dtype=et, device=dev)
         self.state_all = torch.zeros(L, B, Di, device=dev)  # one tensor: one copy in or out for all layers
         self.state = list(self.state_all.unbind(0))
         self._graph = None
@@ -131,6 +138,13 @@ class Decoder:
     # -- weights: the bf16 copies the training path also uses; fp32 norm weights and embedding
     def _current_weights(self):
         m = self.model
+        if self.f32:  # the parameters themselves
+            ws = []
+            for _, norm, gru, ff_norm, ff, _ in m.layers:
+                ws += [norm.weight, gru.to_hidden_and_gate.weight, gru.to_out.weight if self.expanded else None,
+                       ff_norm.weight, ff[0].weight, ff[0].bias, ff[2].weight, ff[2].bias]
+            return [w if w is None else w.detach() for w in ws] + \
+                [m.token_emb.weight.detach(), m.norm.weight.detach(), m.to_logits.weight.detach()]
         ws = []
         for _, norm, gru, ff_norm, ff, _ in m.layers:
             ws += [_f32(norm.weight), bf16_copy(gru.to_hidden_and_gate.weight, dense=True),
@@ -183,19 +197,32 @@ class Decoder:
                 src = (ptr(self.tokens), ptr(emb), V, None, None)
             else:
                 src = (None, None, 0, ptr(self.x[cur]), ptr(self.pending))
-            if self.expanded:
-                check(L.mg_decode_mingru_expanded(B, D, Di, *src, ptr(self.h), ptr(norm_w), ptr(whg),
-                                                  ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_expanded")
-                check(L.mg_decode_to_out(B, D, Di, *src, ptr(self.h), ptr(w_to), ptr(self.x[nxt]), st),
-                      "mg_decode_to_out")
+            if self.f32:
+                if self.expanded:
+                    check(L.mg_decode_mingru_f32(B, D, Di, *src, None, ptr(self.h), ptr(norm_w), ptr(whg),
+                                                 ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_f32")
+                    check(L.mg_decode_to_out_f32(B, D, Di, *src, ptr(self.h), ptr(w_to), ptr(self.x[nxt]), st),
+                          "mg_decode_to_out_f32")
+                else:
+                    check(L.mg_decode_mingru_f32(B, D, Di, *src, ptr(self.x[nxt]), None, ptr(norm_w), ptr(whg),
+                                                 ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_f32")
+                check(L.mg_decode_ff_f32(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act),
+                                         ptr(w2), ptr(b2), ptr(self.pending), FP32_EPS, st), "mg_decode_ff_f32")
             else:
-                check(L.mg_decode_mingru(B, D, *src, ptr(self.x[nxt]), ptr(norm_w), ptr(whg), ptr(self.state[i]),
-                                         FP32_EPS, st), "mg_decode_mingru")
-            check(L.mg_decode_ff(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act),
-                                 ptr(w2), ptr(b2), ptr(self.pending), FP32_EPS, st), "mg_decode_ff")
+                if self.expanded:
+                    check(L.mg_decode_mingru_expanded(B, D, Di, *src, ptr(self.h), ptr(norm_w), ptr(whg),
+                                                      ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_expanded")
+                    check(L.mg_decode_to_out(B, D, Di, *src, ptr(self.h), ptr(w_to), ptr(self.x[nxt]), st),
+                          "mg_decode_to_out")
+                else:
+                    check(L.mg_decode_mingru(B, D, *src, ptr(self.x[nxt]), ptr(norm_w), ptr(whg),
+                                             ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru")
+                check(L.mg_decode_ff(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act),
+                                     ptr(w2), ptr(b2), ptr(self.pending), FP32_EPS, st), "mg_decode_ff")
             cur = nxt
-        check(L.mg_decode_head(B, D, V, ptr(self.x[cur]), ptr(self.pending), ptr(final_norm), ptr(w_logits),
-                               ptr(self.logits), FP32_EPS, st), "mg_decode_head")
+        head = L.mg_decode_head_f32 if self.f32 else L.mg_decode_head
+        check(head(B, D, V, ptr(self.x[cur]), ptr(self.pending), ptr(final_norm), ptr(w_logits), ptr(self.logits),
+                   FP32_EPS, st), "mg_decode_head")
 
     def _capture(self, weights):
         side = torch.cuda.Stream(device=self.device)
@@ -247,8 +274,9 @@ class Decoder:
 
     @torch.no_grad()
     def step(self, tokens):
-        """One token per batch row (tokens [B] int64, on the device) -> logits [B, V] bf16.
-        The returned tensor is the decoder's buffer, overwritten by the next step."""
+        """One token per batch row (tokens [B] int64, on the device) -> logits [B, V] (bf16;
+        fp32 for an fp32 model). The returned tensor is the decoder's buffer, overwritten by the
+        next step."""
         self.tokens.copy_(tokens.reshape(self.B))
         self._returned = None
         self._run()
@@ -257,7 +285,7 @@ class Decoder:
     @torch.no_grad()
     def forward_one(self, tokens, prev_hiddens):
         """minLM.forward's one-token call (reference generate.py:199-203, mingru/minLM.py:97-138
-        on one position): tokens [B, 1] and prev_hiddens (or None) -> (logits [B, 1, V] bf16,
+        on one position): tokens [B, 1] and prev_hiddens (or None) -> (logits [B, 1, V] (bf16, fp32 for an fp32 model),
         next_prev_hiddens [B, 1, Di] fp32 per layer). Both are new tensors, so hiddens the
         caller keeps are never overwritten; when prev_hiddens are the hiddens this call
         returned last (the generation loop), the states are already in place and nothing is

@@ -44,8 +44,8 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch): 203 = 0.2.3, the ABI
- * declared in this file (0.2.1 to 0.2.3 add entry points to 0.2.0 and change
+/* Library version (major*10000 + minor*100 + patch): 204 = 0.2.4, the ABI
+ * declared in this file (0.2.1 to 0.2.4 add entry points to 0.2.0 and change
  * none). */
 int mg_version(void);
 
@@ -543,6 +543,25 @@ int mg_decode_ff(int B, int D, int F, const float* x, const float* norm_w, const
                  float eps, void* stream);
 int mg_decode_head(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
                    const void* w_out, void* logits, float eps, void* stream);
+
+/* The same steps for a model kept in fp32 (reference generate.py:277-278,
+ * --use-f32, which loads the model without a cast): fp32 weights, biases,
+ * pending, act, h and logits, and no rounding point (the norm output and the
+ * projections stay fp32). mg_decode_mingru_f32 writes x_out (expansion 1.0,
+ * Di == D) or h_out (Di != D), exactly one of them. Staged rows (F, Di) are
+ * at most 8192 long at batch 1-4 and 4096 at batch 5-8; pending 16-byte
+ * aligned. */
+int mg_decode_mingru_f32(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                         const float* x_in, const float* pending, float* x_out, float* h_out,
+                         const float* norm_w, const float* w_hg, float* state, float eps, void* stream);
+int mg_decode_to_out_f32(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                         const float* x_in, const float* pending, const float* h, const float* w_out,
+                         float* x_out, void* stream);
+int mg_decode_ff_f32(int B, int D, int F, const float* x, const float* norm_w, const float* w1,
+                     const float* b1, float* act, const float* w2, const float* b2, float* pending_out,
+                     float eps, void* stream);
+int mg_decode_head_f32(int B, int D, int V, const float* x_in, const float* pending, const float* norm_w,
+                       const float* w_out, float* logits, float eps, void* stream);
 
 #ifdef __cplusplus
 }

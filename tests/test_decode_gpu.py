@@ -267,3 +267,60 @@ def test_decoder_follows_optimizer_steps():
         m.layers[1][4][0].weight = torch.nn.Parameter(w.detach() * 0.5)
     routed, fresh = one_token()
     assert torch.equal(routed, fresh), "replaced parameter"
+
+
+def _model_f32(dim, depth, seed, expansion=1.0, ff_mult=4):
+    """An fp32 minLM as generate.py --use-f32 leaves it (no cast, no compute_dtype)."""
+    from gruboros_amd.mingru.minLM import minLM
+
+    torch.manual_seed(seed)
+    m = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion)
+    with torch.no_grad():
+        for layer in m.layers:
+            layer[4][2].weight.normal_(0, 0.02)
+            if expansion != 1.0:
+                layer[2].to_out.weight.normal_(0, 1.0 / (layer[2].to_out.weight.shape[1] ** 0.5))
+    return m.to(DEV).eval()
+
+
+@pytest.mark.parametrize("B,dim,expansion,ff_mult", [
+    (1, 1024, 3.0, 1.5),   # generate.py --use-f32 at the production widths (Di 3072, F 1536)
+    (4, 512, 1.0, 4),
+    (8, 1024, 1.0, 4),     # F 4096: the longest fp32 staged row at batch 5-8
+])
+def test_decoder_fp32_model_matches_fp64_oracle(B, dim, expansion, ff_mult):
+    """An fp32 model (reference generate.py:277 --use-f32) decodes on the *_f32 steps: fp32
+    weights and activations, no rounding point. Against the fp64 restatement of the generation
+    calls (generate.py:184-207, mingru/minLM.py:101-102, minGRU.py:47-52,69-71): logits and
+    states within 1e-4 over 6 tokens (fp32 sums in another order)."""
+    m = _model_f32(dim, 3, seed=40 + B, expansion=expansion, ff_mult=ff_mult)
+    _against_oracle(m, B, 6, f"fp32 d{dim} exp{expansion} ff{ff_mult}", tol=1e-4)
+
+
+def test_fp32_model_calls_run_on_the_decoder():
+    """An fp32 model's one-token calls under no_grad route to the fp32 decode steps (their
+    logits are fp32 and equal Decoder.step's bit for bit) and agree with the parallel path
+    (minLM.decode_kernels off: the fp32-accurate three-limb products) within 1e-5."""
+    from gruboros_amd.decode import Decoder
+
+    B = 2
+    m = _model_f32(512, 2, seed=51, expansion=1.5, ff_mult=1.5)
+    gen = torch.Generator(device=DEV).manual_seed(52)
+    prompt = torch.randint(0, 256, (B, 7), device=DEV, generator=gen)
+    toks = [torch.randint(0, 256, (B,), device=DEV, generator=gen) for _ in range(3)]
+    dec = Decoder(m, B)
+    assert dec.f32
+    with torch.no_grad():
+        _, hid = m(prompt, return_prev_hiddens=True)
+        dec.prefill(prompt)
+        ref_hid = hid
+        for t in toks:
+            logits, hid = m(t[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+            assert logits.dtype == torch.float32
+            assert torch.equal(logits[:, 0], dec.step(t))
+            m.decode_kernels = False
+            ref, ref_hid = m(t[:, None], return_prev_hiddens=True, prev_hiddens=ref_hid)
+            m.decode_kernels = True
+            e = _rel(logits, ref)
+            print(f"fp32 routed vs parallel path: {e:.2e}", flush=True)
+            assert e < 1e-5

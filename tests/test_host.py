@@ -169,3 +169,20 @@ def test_build_refuses_spills_in_inline_assembly_kernels():
     ])
     bad = _spilled_kernels(remarks)
     assert [n for _, n in bad] == [41] and "persist_w4m" in bad[0][0]
+
+
+def test_decoder_applies_to_fp32_models_within_their_staged_limit():
+    """gruboros_amd.decode.unsupported_reason (host logic only): an fp32 model (generate.py
+    --use-f32) is served by the fp32 decode steps, whose staged rows are at most 4096 long at
+    batch 5-8 (twice the LDS of bf16 rows); a float16 model stays on the parallel path."""
+    import torch
+
+    from gruboros_amd.decode import unsupported_reason
+    from gruboros_amd.mingru.minLM import minLM
+
+    m = minLM(num_tokens=256, dim=64, depth=1, ff_mult=64)  # FeedForward width 4096
+    assert unsupported_reason(m, 8) is None
+    m2 = minLM(num_tokens=256, dim=64, depth=1, ff_mult=128)  # 8192
+    assert unsupported_reason(m2, 4) is None
+    assert "4096" in unsupported_reason(m2, 8)
+    assert "float16" in unsupported_reason(m.half(), 1)
