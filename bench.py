@@ -193,7 +193,7 @@ def bench_ceilings(n=1 << 28, reps=10):
 
 
 def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64, expansion=1.0, ff_mult=4, cast=False,
-                 f32=False):
+                 f32=False, f16=False):
     """Generation (reference generate.py:184-212): tokens/s of the per-token step,
     greedy sampling on the device, no host sync per token.
     `model_call`: the drop-in model called once per token as generate.py does (its
@@ -202,8 +202,8 @@ def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64, expans
     `decoder_graph`: gruboros_amd.decode.Decoder (decode kernels, one HIP graph
     replay per token). `weight_GBs`: bf16 weight bytes read per step / step time.
     cast: the model's parameters cast with .to(torch.bfloat16) as generate.py:140-141
-    does; f32: the model kept in fp32 (generate.py --use-f32); else fp32 masters with
-    compute_dtype bf16. `weight_GBs` counts the weights at their stored width."""
+    does; f32: the model kept in fp32 (generate.py --use-f32); f16: cast with
+    .to(torch.float16) (--use-f32 --use-fp16); else fp32 masters with compute_dtype bf16. `weight_GBs` counts the weights at their stored width."""
     import torch
 
     from gruboros_amd.decode import Decoder
@@ -212,13 +212,15 @@ def bench_decode(steps=200, batches=(1, 8), dim=1024, depth=8, prompt=64, expans
     torch.manual_seed(0)
     with torch.device("cuda"):
         model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion,
-                      compute_dtype=None if (cast or f32) else torch.bfloat16).eval()
+                      compute_dtype=None if (cast or f32 or f16) else torch.bfloat16).eval()
     if cast:
         model = model.to(torch.bfloat16)
+    if f16:
+        model = model.to(torch.float16)
     wbytes = (4 if f32 else 2) * sum(p.numel() for n, p in model.named_parameters()
                                      if p.dim() == 2 and "token_emb" not in n)
     res = {"model": f"minLM d{dim} L{depth} expansion {expansion} ff_mult {ff_mult} "
-                    f"{'cast to bf16' if cast else 'fp32' if f32 else 'bf16 activations'}",
+                    f"{'cast to bf16' if cast else 'fp32' if f32 else 'cast to fp16' if f16 else 'bf16 activations'}",
            "steps": steps, "weight_bytes_per_step": wbytes}
     gen = torch.Generator(device="cuda").manual_seed(0)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -530,6 +532,8 @@ def main():
         # the same model as generate.py --use-f32 leaves it (fp32, no cast), batch 1
         dec_prod32 = bench_decode(steps=50, batches=(1,), dim=1024, depth=79, expansion=3.0, ff_mult=1.5, f32=True)
         print(f"[bench] decode production fp32 {json.dumps(dec_prod32)}", file=sys.stderr, flush=True)
+        dec_prod16 = bench_decode(steps=50, batches=(1,), dim=1024, depth=79, expansion=3.0, ff_mult=1.5, f16=True)
+        print(f"[bench] decode production fp16 {json.dumps(dec_prod16)}", file=sys.stderr, flush=True)
     cfg1 = None
     if args.only in (None, "cfg1"):
         cfg1 = bench_cfg1()
@@ -606,6 +610,7 @@ def main():
         out["decode"] = dec
         out["decode_production"] = dec_prod
         out["decode_production_fp32"] = dec_prod32
+        out["decode_production_fp16"] = dec_prod16
     if ref:
         out["reference_loop"] = ref
     if cfg1:

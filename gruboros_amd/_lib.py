@@ -41,6 +41,12 @@ SIGNATURES = {
     "mg_decode_ff_f32": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                                   _vp]),
     "mg_decode_head_f32": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
+    "mg_decode_mingru_f16": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      ctypes.c_float, _vp]),
+    "mg_decode_to_out_f16": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mg_decode_ff_f16": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                  _vp]),
+    "mg_decode_head_f16": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp]),
     "mg_scan_ckpt_elems": (_c_size, [_c_int, _c_int, _c_int]),
     "mg_scan_fwd_noalloc_max_bytes": (_c_size, []),
     "mg_scan_fwd_noalloc": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _fp, _c_int, _vp, _c_i64, _c_i64, _fp, _fp,

@@ -35,6 +35,7 @@
 // the staged rows are at most 4096 long).
 
 #include <algorithm>
+#include <type_traits>
 
 #include "mg_common.h"
 
@@ -42,6 +43,8 @@ namespace mg {
 namespace decode {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16_t;  // fp16 element (a model cast with .to(torch.float16))
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -50,19 +53,44 @@ constexpr int kMaxStaged = 8192;  // longest bf16 input row a workgroup stages i
 
 enum Mode { MINGRU = 0, FF1 = 1, FF2 = 2, HEAD = 3, TO_OUT = 4 };
 
-// Element type of a decode path (weights, biases, staged rows, branch outputs).
+// Element type of a decode path (weights, biases, staged rows, branch outputs):
+// round (the rounding point), get/put one element, load4/store4 four.
 template <typename T> struct Elem;
 template <> struct Elem<bf16_t> {
   static constexpr int kVec = 1;  // uint4 per 8 elements
   __device__ __forceinline__ static float round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
   __device__ __forceinline__ static float get(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
   __device__ __forceinline__ static void put(bf16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+  __device__ __forceinline__ static f4 load4(const bf16_t* p) { return io4<bf16_t>::load(p); }
+  __device__ __forceinline__ static void store4(bf16_t* p, const f4& v) { io4<bf16_t>::store(p, v); }
 };
 template <> struct Elem<float> {
   static constexpr int kVec = 2;
   __device__ __forceinline__ static float round(float x) { return x; }
   __device__ __forceinline__ static float get(const float* p, int64_t i) { return p[i]; }
   __device__ __forceinline__ static void put(float* p, int64_t i, float v) { p[i] = v; }
+  __device__ __forceinline__ static f4 load4(const float* p) { return io4<float>::load(p); }
+  __device__ __forceinline__ static void store4(float* p, const f4& v) { io4<float>::store(p, v); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kVec = 1;
+  __device__ __forceinline__ static float round(float x) { return static_cast<float>(static_cast<f16_t>(x)); }
+  __device__ __forceinline__ static float get(const f16_t* p, int64_t i) { return static_cast<float>(p[i]); }
+  __device__ __forceinline__ static void put(f16_t* p, int64_t i, float v) { p[i] = static_cast<f16_t>(v); }
+  __device__ __forceinline__ static f4 load4(const f16_t* p) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    const f16x4 x = *reinterpret_cast<const f16x4*>(p);
+    f4 r;
+    r.v[0] = static_cast<float>(x[0]); r.v[1] = static_cast<float>(x[1]);
+    r.v[2] = static_cast<float>(x[2]); r.v[3] = static_cast<float>(x[3]);
+    return r;
+  }
+  __device__ __forceinline__ static void store4(f16_t* p, const f4& v) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    const f16x4 x = {static_cast<f16_t>(v.v[0]), static_cast<f16_t>(v.v[1]), static_cast<f16_t>(v.v[2]),
+                     static_cast<f16_t>(v.v[3])};
+    *reinterpret_cast<f16x4*>(p) = x;
+  }
 };
 // 8 consecutive elements of a row
 template <typename T> struct Vec8 {
@@ -165,7 +193,7 @@ __device__ __forceinline__ f4 stream4_at(const Args& a, int b, int c) {
     x = io4<float>::load(a.x_in + static_cast<int64_t>(b) * a.D + c);
   }
   if constexpr (SRC == SRC_X_PENDING) {
-    const f4 p = io4<T>::load(static_cast<const T*>(a.pending) + static_cast<int64_t>(b) * a.D + c);
+    const f4 p = Elem<T>::load4(static_cast<const T*>(a.pending) + static_cast<int64_t>(b) * a.D + c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) x.v[e] += p.v[e];
   }
@@ -282,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
           f4 y;
 #pragma unroll
           for (int e = 0; e < 4; ++e) y.v[e] = xr[b][4 * q + e] * s_rstd[b] * w.v[e];
-          io4<T>::store(s_in + b * K + c, y);
+          Elem<T>::store4(s_in + b * K + c, y);
         }
       }
     }
@@ -310,9 +338,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(Args a) {
           const uint4 wq = wv[c][r].q[0];
           const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
-          for (int q = 0; q < 4; ++q)  // two bf16 products per instruction, fp32 accumulation
-            acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, ww[q]),
-                                                        __builtin_bit_cast(bf16x2, xw[q]), acc[r][b], false);
+          for (int q = 0; q < 4; ++q) {  // two 16-bit products per instruction, fp32 accumulation
+            if constexpr (sizeof(T) == 2 && !std::is_same<T, f16_t>::value)
+              acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, ww[q]),
+                                                          __builtin_bit_cast(bf16x2, xw[q]), acc[r][b], false);
+            else
+              acc[r][b] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, ww[q]), __builtin_bit_cast(f16x2, xw[q]),
+                                                 acc[r][b], false);
+          }
         }
       } else {
         const float4 x0 = reinterpret_cast<const float4*>(s_in + b * K + k0)[0];
@@ -572,4 +605,35 @@ extern "C" int mg_decode_ff_f32(int B, int D, int F, const float* x, const float
 extern "C" int mg_decode_head_f32(int B, int D, int V, const float* x_in, const float* pending, const float* norm_w,
                                   const float* w_out, float* logits, float eps, void* stream) {
   return decode::head_impl<float>("mg_decode_head_f32", B, D, V, x_in, pending, norm_w, w_out, logits, eps, stream);
+}
+
+// fp16 models (reference generate.py:143-144, --use-fp16 with --use-f32): the
+// bf16 steps with fp16 weights and fp16 rounding points.
+extern "C" int mg_decode_mingru_f16(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                    const float* x_in, const void* pending, float* x_out, void* h_out,
+                                    const float* norm_w, const void* w_hg, float* state, float eps, void* stream) {
+  if (!x_out == !h_out) return fail(MG_ERR_ARG, "mg_decode_mingru_f16: exactly one of x_out and h_out");
+  if (!h_out && Di != D) return fail(MG_ERR_ARG, "mg_decode_mingru_f16: Di %d != D %d needs h_out", Di, D);
+  return decode::mingru_impl<decode::f16_t>("mg_decode_mingru_f16", B, D, Di, tokens, emb, V, x_in, pending, x_out,
+                                            h_out, norm_w, w_hg, state, eps, stream);
+}
+
+extern "C" int mg_decode_to_out_f16(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                                    const float* x_in, const void* pending, const void* h, const void* w_out,
+                                    float* x_out, void* stream) {
+  return decode::to_out_impl<decode::f16_t>("mg_decode_to_out_f16", B, D, Di, tokens, emb, V, x_in, pending, h, w_out,
+                                            x_out, stream);
+}
+
+extern "C" int mg_decode_ff_f16(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
+                                const void* b1, void* act, const void* w2, const void* b2, void* pending_out,
+                                float eps, void* stream) {
+  return decode::ff_impl<decode::f16_t>("mg_decode_ff_f16", B, D, F, x, norm_w, w1, b1, act, w2, b2, pending_out, eps,
+                                        stream);
+}
+
+extern "C" int mg_decode_head_f16(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
+                                  const void* w_out, void* logits, float eps, void* stream) {
+  return decode::head_impl<decode::f16_t>("mg_decode_head_f16", B, D, V, x_in, pending, norm_w, w_out, logits, eps,
+                                          stream);
 }

@@ -19,7 +19,8 @@ with ``compute_dtype=torch.bfloat16`` over fp32 parameters, or one whose
 parameters were cast with ``.to(torch.bfloat16)`` (generate.py:140-141); or
 a model kept in fp32 (generate.py --use-f32: fp32 parameters and no
 compute_dtype), which runs the *_f32 steps (fp32 weights and activations, no
-rounding point); no conv; dropout only in eval mode (where it is the
+rounding point); or a model cast with .to(torch.float16) (--use-f32
+--use-fp16), which runs the *_f16 steps (the bf16 steps at fp16); no conv; dropout only in eval mode (where it is the
 identity); batch 1..8; dim a multiple of 8 and at most 2048; the scan width
 Di = dim * expansion and the FeedForward width multiples of 8 and at most
 8192 (4096 for an fp32 model at batch 5-8).
@@ -43,15 +44,29 @@ def _widths(model):
             model.token_emb.weight.shape[0])
 
 
+def _kind(model):
+    """Which decode steps serve the model: "bf16" (bf16 activations), "f32" (an fp32 model),
+    "f16" (parameters cast to float16), or None."""
+    cd, _ = model._dtypes()
+    pd = model.token_emb.weight.dtype
+    if cd == torch.bfloat16:
+        return "bf16"
+    if pd == torch.float16:
+        return "f16"
+    if cd == torch.float32 and pd == torch.float32:
+        return "f32"
+    return None
+
+
 def unsupported_reason(model, batch_size):
     """None if Decoder(model, batch_size) applies, else why not."""
     from .mingru.minGRU import minGRU
 
-    cd, _ = model._dtypes()
-    f32 = cd == torch.float32 and model.token_emb.weight.dtype == torch.float32
-    if cd != torch.bfloat16 and not f32:
+    kind = _kind(model)
+    f32 = kind == "f32"
+    if kind is None:
         return ("Decoder needs bf16 activations (a minLM built with compute_dtype=torch.bfloat16, or one cast "
-                "with .to(torch.bfloat16)) or an fp32 model; float16 parameters run the parallel path")
+                "with .to(torch.bfloat16)), an fp32 model or a float16 one")
     if not 1 <= batch_size <= MAX_BATCH:
         return f"Decoder batch {batch_size} outside [1, {MAX_BATCH}]"
     D, Di, F, V = _widths(model)
@@ -109,8 +124,9 @@ class Decoder:
         self._model = weakref.ref(model) if _weak else (lambda m=model: m)
         self.B, self.graph_enabled = batch_size, graph
         self.D, self.Di, self.F, self.V = _widths(model)
-        self.f32 = model._dtypes()[0] == torch.float32  # an fp32 model: the *_f32 steps
-        et = torch.float32 if self.f32 else torch.bfloat16  # weights, branch outputs, logits
+        self.kind = _kind(model)  # "bf16", "f32" (the *_f32 steps) or "f16" (the *_f16 steps)
+        self.f32 = self.kind == "f32"
+        et = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[self.kind]  # weights, outputs
         self.expanded = self.Di != self.D
         B, D, Di, F, V, L = self.B, self.D, self.Di, self.F, self.V, len(model.layers)
         self.device = dev
@@ -138,13 +154,13 @@ class Decoder:
     # -- weights: the bf16 copies the training path also uses; fp32 norm weights and embedding
     def _current_weights(self):
         m = self.model
-        if self.f32:  # the parameters themselves
+        if self.kind != "bf16":  # the parameters themselves (fp32 norm weights and embedding)
             ws = []
             for _, norm, gru, ff_norm, ff, _ in m.layers:
-                ws += [norm.weight, gru.to_hidden_and_gate.weight, gru.to_out.weight if self.expanded else None,
-                       ff_norm.weight, ff[0].weight, ff[0].bias, ff[2].weight, ff[2].bias]
-            return [w if w is None else w.detach() for w in ws] + \
-                [m.token_emb.weight.detach(), m.norm.weight.detach(), m.to_logits.weight.detach()]
+                ws += [_f32(norm.weight), gru.to_hidden_and_gate.weight.detach(),
+                       gru.to_out.weight.detach() if self.expanded else None, _f32(ff_norm.weight),
+                       ff[0].weight.detach(), ff[0].bias.detach(), ff[2].weight.detach(), ff[2].bias.detach()]
+            return ws + [_f32(m.token_emb.weight), _f32(m.norm.weight), m.to_logits.weight.detach()]
         ws = []
         for _, norm, gru, ff_norm, ff, _ in m.layers:
             ws += [_f32(norm.weight), bf16_copy(gru.to_hidden_and_gate.weight, dense=True),
@@ -197,17 +213,18 @@ class Decoder:
                 src = (ptr(self.tokens), ptr(emb), V, None, None)
             else:
                 src = (None, None, 0, ptr(self.x[cur]), ptr(self.pending))
-            if self.f32:
+            if self.kind != "bf16":
+                sfx = "_" + self.kind
+                mingru, to_out, ff = (getattr(L, "mg_decode_" + n + sfx) for n in ("mingru", "to_out", "ff"))
                 if self.expanded:
-                    check(L.mg_decode_mingru_f32(B, D, Di, *src, None, ptr(self.h), ptr(norm_w), ptr(whg),
-                                                 ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_f32")
-                    check(L.mg_decode_to_out_f32(B, D, Di, *src, ptr(self.h), ptr(w_to), ptr(self.x[nxt]), st),
-                          "mg_decode_to_out_f32")
+                    check(mingru(B, D, Di, *src, None, ptr(self.h), ptr(norm_w), ptr(whg), ptr(self.state[i]),
+                                 FP32_EPS, st), "mg_decode_mingru" + sfx)
+                    check(to_out(B, D, Di, *src, ptr(self.h), ptr(w_to), ptr(self.x[nxt]), st), "mg_decode_to_out" + sfx)
                 else:
-                    check(L.mg_decode_mingru_f32(B, D, Di, *src, ptr(self.x[nxt]), None, ptr(norm_w), ptr(whg),
-                                                 ptr(self.state[i]), FP32_EPS, st), "mg_decode_mingru_f32")
-                check(L.mg_decode_ff_f32(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act),
-                                         ptr(w2), ptr(b2), ptr(self.pending), FP32_EPS, st), "mg_decode_ff_f32")
+                    check(mingru(B, D, Di, *src, ptr(self.x[nxt]), None, ptr(norm_w), ptr(whg), ptr(self.state[i]),
+                                 FP32_EPS, st), "mg_decode_mingru" + sfx)
+                check(ff(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act), ptr(w2), ptr(b2),
+                         ptr(self.pending), FP32_EPS, st), "mg_decode_ff" + sfx)
             else:
                 if self.expanded:
                     check(L.mg_decode_mingru_expanded(B, D, Di, *src, ptr(self.h), ptr(norm_w), ptr(whg),
@@ -220,7 +237,7 @@ class Decoder:
                 check(L.mg_decode_ff(B, D, F, ptr(self.x[nxt]), ptr(ff_norm_w), ptr(w1), ptr(b1), ptr(self.act),
                                      ptr(w2), ptr(b2), ptr(self.pending), FP32_EPS, st), "mg_decode_ff")
             cur = nxt
-        head = L.mg_decode_head_f32 if self.f32 else L.mg_decode_head
+        head = L.mg_decode_head if self.kind == "bf16" else getattr(L, "mg_decode_head_" + self.kind)
         check(head(B, D, V, ptr(self.x[cur]), ptr(self.pending), ptr(final_norm), ptr(w_logits), ptr(self.logits),
                    FP32_EPS, st), "mg_decode_head")
 
@@ -275,8 +292,8 @@ class Decoder:
     @torch.no_grad()
     def step(self, tokens):
         """One token per batch row (tokens [B] int64, on the device) -> logits [B, V] (bf16;
-        fp32 for an fp32 model). The returned tensor is the decoder's buffer, overwritten by the
-        next step."""
+        fp32 for an fp32 model, fp16 for a float16 one). The returned tensor is the decoder's
+        buffer, overwritten by the next step."""
         self.tokens.copy_(tokens.reshape(self.B))
         self._returned = None
         self._run()

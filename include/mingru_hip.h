@@ -44,8 +44,8 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch): 204 = 0.2.4, the ABI
- * declared in this file (0.2.1 to 0.2.4 add entry points to 0.2.0 and change
+/* Library version (major*10000 + minor*100 + patch): 205 = 0.2.5, the ABI
+ * declared in this file (0.2.1 to 0.2.5 add entry points to 0.2.0 and change
  * none). */
 int mg_version(void);
 
@@ -562,6 +562,22 @@ int mg_decode_ff_f32(int B, int D, int F, const float* x, const float* norm_w, c
                      float eps, void* stream);
 int mg_decode_head_f32(int B, int D, int V, const float* x_in, const float* pending, const float* norm_w,
                        const float* w_out, float* logits, float eps, void* stream);
+
+/* The same steps for a model cast with .to(torch.float16) (reference
+ * generate.py:143-144, --use-f32 --use-fp16): fp16 weights, biases, pending,
+ * act, h and logits (void* here: IEEE binary16), and the bf16 steps' rounding
+ * points at fp16; limits and alignments as the bf16 steps. */
+int mg_decode_mingru_f16(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                         const float* x_in, const void* pending, float* x_out, void* h_out,
+                         const float* norm_w, const void* w_hg, float* state, float eps, void* stream);
+int mg_decode_to_out_f16(int B, int D, int Di, const int64_t* tokens, const float* emb, int V,
+                         const float* x_in, const void* pending, const void* h, const void* w_out,
+                         float* x_out, void* stream);
+int mg_decode_ff_f16(int B, int D, int F, const float* x, const float* norm_w, const void* w1,
+                     const void* b1, void* act, const void* w2, const void* b2, void* pending_out,
+                     float eps, void* stream);
+int mg_decode_head_f16(int B, int D, int V, const float* x_in, const void* pending, const float* norm_w,
+                       const void* w_out, void* logits, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -324,3 +324,42 @@ def test_fp32_model_calls_run_on_the_decoder():
             e = _rel(logits, ref)
             print(f"fp32 routed vs parallel path: {e:.2e}", flush=True)
             assert e < 1e-5
+
+
+@pytest.mark.parametrize("B,dim,expansion,ff_mult", [(1, 1024, 3.0, 1.5), (8, 512, 1.0, 4)])
+def test_decoder_fp16_model_matches_fp64_oracle(B, dim, expansion, ff_mult):
+    """A model cast with .to(torch.float16) (reference generate.py:143-144, --use-f32
+    --use-fp16) decodes on the *_f16 steps (fp16 weights, the bf16 steps' rounding points at
+    fp16). Against the fp64 restatement on the same (fp16-valued) parameters: logits and
+    states within 1e-2 over 6 tokens."""
+    m = _model_f32(dim, 3, seed=60 + B, expansion=expansion, ff_mult=ff_mult).half()
+    _against_oracle(m, B, 6, f"fp16 d{dim} exp{expansion} ff{ff_mult}", tol=1e-2)
+
+
+def test_fp16_model_calls_run_on_the_decoder():
+    """A float16 model's one-token calls route to the fp16 steps: fp16 logits equal to
+    Decoder.step's, and within 1e-2 of the model's own parallel path (its products in fp16,
+    its kernels in fp32)."""
+    from gruboros_amd.decode import Decoder
+
+    B = 2
+    m = _model_f32(512, 2, seed=61, expansion=1.5, ff_mult=1.5).half()
+    gen = torch.Generator(device=DEV).manual_seed(62)
+    prompt = torch.randint(0, 256, (B, 7), device=DEV, generator=gen)
+    toks = [torch.randint(0, 256, (B,), device=DEV, generator=gen) for _ in range(3)]
+    dec = Decoder(m, B)
+    assert dec.kind == "f16"
+    with torch.no_grad():
+        _, hid = m(prompt, return_prev_hiddens=True)
+        dec.prefill(prompt)
+        ref_hid = hid
+        for t in toks:
+            logits, hid = m(t[:, None], return_prev_hiddens=True, prev_hiddens=hid)
+            assert logits.dtype == torch.float16
+            assert torch.equal(logits[:, 0], dec.step(t))
+            m.decode_kernels = False
+            ref, ref_hid = m(t[:, None], return_prev_hiddens=True, prev_hiddens=ref_hid)
+            m.decode_kernels = True
+            e = _rel(logits, ref)
+            print(f"fp16 routed vs parallel path: {e:.2e}", flush=True)
+            assert e < 1e-2

@@ -174,7 +174,8 @@ def test_build_refuses_spills_in_inline_assembly_kernels():
 def test_decoder_applies_to_fp32_models_within_their_staged_limit():
     """gruboros_amd.decode.unsupported_reason (host logic only): an fp32 model (generate.py
     --use-f32) is served by the fp32 decode steps, whose staged rows are at most 4096 long at
-    batch 5-8 (twice the LDS of bf16 rows); a float16 model stays on the parallel path."""
+    batch 5-8 (twice the LDS of bf16 rows); a float16 model (--use-fp16) by the fp16 steps; a
+    float64 model stays on the parallel path."""
     import torch
 
     from gruboros_amd.decode import unsupported_reason
@@ -185,4 +186,5 @@ def test_decoder_applies_to_fp32_models_within_their_staged_limit():
     m2 = minLM(num_tokens=256, dim=64, depth=1, ff_mult=128)  # 8192
     assert unsupported_reason(m2, 4) is None
     assert "4096" in unsupported_reason(m2, 8)
-    assert "float16" in unsupported_reason(m.half(), 1)
+    assert unsupported_reason(m2.half(), 8) is None  # 16-bit rows: the full 8192
+    assert "fp32 model" in unsupported_reason(m.double(), 1)

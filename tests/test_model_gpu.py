@@ -677,8 +677,8 @@ def test_generate_py_load_and_decode_path(cast):
     train.cuda.sh:60-61). Checked per step against the fp64 restatement
     evaluated on the same cast parameter values (the cast model's parameters
     are what it computes with): logits and hiddens within 2e-2 (bf16
-    activations) / 5e-3 (fp16 products, fp32 kernels). The bf16 model's
-    one-token calls run on the decode kernels (gruboros_amd.decode), which
+    activations) / 5e-3 (fp16). Both models' one-token calls run on the
+    decode kernels (gruboros_amd.decode: the bf16 steps, the fp16 steps), which
     the test asserts, and hiddens a call returned keep their values after the
     next call."""
     from gruboros_amd import decode
@@ -714,7 +714,7 @@ def test_generate_py_load_and_decode_path(cast):
             kept = (hidden_states, [h.clone() for h in hidden_states])
             prev_token = logits[:, -1, :].float().argmax(-1, keepdim=True)
     routed = [d for d in decode._CACHE.get(model, {}).values() if isinstance(d, decode.Decoder)]
-    assert len(routed) == (1 if cast == torch.bfloat16 else 0)
+    assert len(routed) == 1 and routed[0].kind == ("bf16" if cast == torch.bfloat16 else "f16")
 
 
 @pytest.mark.parametrize("expansion", [1.0, 1.5])
