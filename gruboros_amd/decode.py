@@ -1,4 +1,4 @@
-"""Token-by-token generation for a bf16 minLM on the decode kernels.
+"""Token-by-token generation for a minLM on the decode kernels (bf16, fp32 or float16 models).
 
 Reference generate.py:184-212 processes the prompt with one parallel forward
 and then calls ``model(prev_token, return_prev_hiddens=True,
