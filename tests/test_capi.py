@@ -168,6 +168,29 @@ def test_decode_argument_errors(L):
     assert L.mg_decode_ff(1, 64, 256, 24, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1  # x
     assert L.mg_decode_head(1, 64, 256, 16, None, 24, 16, 16, eps, None) == 1  # norm weight
     assert b"aligned" in L.mg_last_error()
+    # the fp32 and float16 steps: exactly one of x_out / h_out, Di == D without h_out, the fp32
+    # staged-row limit at batch 5-8 (4096), 16-byte fp32 pending
+    assert L.mg_decode_mingru_f32(1, 64, 64, None, None, 0, 16, None, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru_f32(1, 64, 64, None, None, 0, 16, None, None, None, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_mingru_f32(1, 64, 96, None, None, 0, 16, None, 16, None, 16, 16, 16, eps, None) == 1
+    assert b"h_out" in L.mg_last_error()
+    assert L.mg_decode_ff_f32(5, 64, 4104, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_to_out_f32(8, 64, 8192, None, None, 0, 16, None, 16, 16, 16, None) == 1
+    assert L.mg_decode_mingru_f32(1, 64, 64, None, None, 0, 16, 24, 16, None, 16, 16, 16, eps, None) == 1  # pending
+    assert L.mg_decode_mingru_f16(1, 64, 64, None, None, 0, 16, None, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_ff_f16(9, 64, 256, 16, 16, 16, 16, 16, 16, 16, 16, eps, None) == 1
+    assert L.mg_decode_head_f16(1, 64, 0, 16, None, 16, 16, 16, eps, None) == 1
+
+
+def test_scaled_norm_bwd_argument_errors(L):
+    # mg_add_rmsnorm_bwd_scaled: the scale is a 4-byte-aligned device float (NULL: 1); the
+    # other checks are mg_add_rmsnorm_bwd's, which forwards to it
+    args = dict(xn=16, w=16, rstd=16, dydt=1, dy=16, scale=None, dres=None, dx=16, dddt=0, dd=None, dw=16, N=4, D=64,
+                ws=None, wsb=0, stream=None)
+    assert L.mg_add_rmsnorm_bwd_scaled(*{**args, "scale": 18}.values()) == 1
+    assert b"dy_scale" in L.mg_last_error()
+    assert L.mg_add_rmsnorm_bwd_scaled(*args.values()) == 3  # no workspace
+    assert L.mg_add_rmsnorm_bwd(16, 16, 16, 1, 16, None, 16, 0, None, 16, 4, 62, None, 0, None) == 1  # D % 4
 
 
 def test_product_refuses_cpu_tensors():
