@@ -2274,6 +2274,31 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   }
 }
 
+// C[m, n] = bf16 of the sum over the S split partials (in split order): rounded to
+// nearest, or stochastically with the unsplit epilogue's hash of the element index
+// (EPI_SR), so only the fp32 sum's order differs from the unsplit product.
+__global__ __launch_bounds__(256) void split_reduce_bf16_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                               bf16_t* __restrict__ C, int64_t ldc, int stochastic) {
+  const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
+  const int64_t slice = static_cast<int64_t>(M) * N;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n4;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t m = i / (N / 4), n = (i % (N / 4)) * 4;
+    const float* pp = part + m * N + n;
+    f4 sum = io4<float>::fill(0.0f);
+    for (int s = 0; s < S; ++s) {
+      const f4 v = load4_stream(pp + s * slice);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
+    }
+    bf16_t* cp = C + m * ldc + n;
+    if (stochastic)
+      io4<bf16_t>::store_grad(cp, sum, static_cast<uint32_t>(m * N + n), 0x9e5bu);
+    else
+      io4<bf16_t>::store(cp, sum);
+  }
+}
+
 constexpr int kCUs = 256;
 
 // Tile size and K split of a product (measured on MI355X): weight gradients
@@ -2307,7 +2332,12 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   const int nkt = (hilo ? 3 : 1) * ((K + BK - 1) / BK);
   const int64_t want_wgs = wgrad && !wgrad_big ? 2 * kCUs : kCUs;
   int splits = 1;
-  if (c_dtype == MG_F32 && epilogue == MG_EPI_NONE && tiles < want_wgs && !deterministic)
+  // fp32 outputs and plain bf16 outputs (no epilogue, no hi/lo operands; a stochastically
+  // rounded gradient among them) split K when the tiles leave CUs idle: partials in fp32, then
+  // split_reduce_kernel (fp32) or split_reduce_bf16_kernel (rounded as the unsplit epilogue
+  // would). Hi/lo bf16 products stay whole, equal to mg_gemm_hilo_prefix's columns.
+  const bool split_ok = c_dtype == MG_F32 || (c_dtype == MG_BF16 && !hilo);
+  if (epilogue == MG_EPI_NONE && split_ok && tiles < want_wgs && !deterministic)
     splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
   pl.kt_per_split = std::max((nkt + splits - 1) / splits, 1);
   pl.ysplits = std::max((nkt + pl.kt_per_split - 1) / pl.kt_per_split, 1);
@@ -2406,6 +2436,7 @@ int dispatch_epi(const Params& p, const Plan& pl, int epi, int c_dtype, hipStrea
     if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, float, C_STORE>(p, pl, s);
   } else {
+    if (pl.ysplits > 1) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, float, C_SPLIT>(p, pl, s);
     if (epi == EPI_NONE) return launch<BM, BN, WM, WN, AK, BKM, EPI_NONE, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS, bf16_t, C_STORE>(p, pl, s);
     if (epi == EPI_BIAS_GELU) return launch<BM, BN, WM, WN, AK, BKM, EPI_BIAS_GELU, bf16_t, C_STORE>(p, pl, s);
@@ -2596,8 +2627,13 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
                         : gemm::dispatch_layout<128, 128>(p, pl, ak, bk, epi, c_dtype, s);
   if (rc || pl.ysplits <= 1) return rc;
   const int64_t n4 = int64_t(M) * (N / 4);
-  hipLaunchKernelGGL(gemm::split_reduce_kernel, dim3(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048))),
-                     dim3(256), 0, s, p.part, pl.ysplits, M, N, static_cast<float*>(C), ldc, p.accumulate);
+  const dim3 rgrid(static_cast<int>(std::min<int64_t>((n4 + 255) / 256, 2048)));
+  if (c_dtype == MG_F32)
+    hipLaunchKernelGGL(gemm::split_reduce_kernel, rgrid, dim3(256), 0, s, p.part, pl.ysplits, M, N,
+                       static_cast<float*>(C), ldc, p.accumulate);
+  else
+    hipLaunchKernelGGL(gemm::split_reduce_bf16_kernel, rgrid, dim3(256), 0, s, p.part, pl.ysplits, M, N,
+                       static_cast<bf16_t*>(C), ldc, (flags & MG_GEMM_STOCHASTIC) ? 1 : 0);
   return check_launch(fn);
 }
 

@@ -513,6 +513,50 @@ def test_gemm_split_layout_matches(al, bl, M, N, K, monkeypatch):
     assert _rel(outs[0], a.double() @ b.double().t()) < 1e-5
 
 
+@pytest.mark.parametrize("al,bl,M,N,K", [
+    (0, 1, 2048, 1024, 6144),    # to_hidden_and_gate input gradient at one [1, 2048] chunk: 128 tiles x 2 splits
+    (0, 0, 512, 520, 4000),      # ragged N, 20 tiles x 12 splits
+    (1, 1, 256, 264, 3000),      # both MN-contiguous (weight-gradient layout), ragged K
+    (0, 1, 37, 64, 2000),        # one ragged tile, 8 splits
+])
+def test_gemm_bf16_split_rounds_the_fp32_split_sum(al, bl, M, N, K):
+    """bf16 products with no epilogue whose tiles leave CUs idle split along K as the fp32
+    products do (fp32 partials, summed in split order by the reduction pass), and the pass rounds
+    the sum once: to nearest, or stochastically with the unsplit epilogue's hash of the element
+    index. So they equal the fp32 split product rounded by torch (to nearest) or by
+    mg_round_bf16_sr with the gradient salt 0x9e5b, bit for bit; and the unsplit product
+    (deterministic flag) and the split one are both within one bf16 rounding of the fp64 product."""
+    from gruboros_amd import _lib
+    from gruboros_amd.gemm import gemm, round_bf16_sr
+
+    L = _lib.lib()
+    assert L.mg_gemm_workspace_bytes(al, bl, M, N, K, 0, _lib.dtype_code(torch.bfloat16), 0) > 0, "plan not split"
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + 7 * al + 11 * bl)
+    a, ad = _dev_operand(M, K, al, g)
+    b, bd = _dev_operand(N, K, bl, g, scale=0.05)
+    f32 = torch.empty(M, N, device=DEV)
+    gemm(ad, al, bd, bl, M, N, K, f32)
+    rn = torch.full((M, N), 3.0, device=DEV, dtype=torch.bfloat16)
+    gemm(ad, al, bd, bl, M, N, K, rn)
+    sr = torch.full_like(rn, 3.0)
+    gemm(ad, al, bd, bl, M, N, K, sr, stochastic=True)
+    sr2 = torch.full_like(rn, 3.0)
+    gemm(ad, al, bd, bl, M, N, K, sr2, stochastic=True)
+    whole = torch.full_like(rn, 3.0)
+    gemm(ad, al, bd, bl, M, N, K, whole, deterministic=True)
+    torch.cuda.synchronize()
+    print(f"bf16 split {al}{bl} {M}x{N}x{K}", flush=True)
+    assert torch.equal(rn, f32.to(torch.bfloat16))
+    assert torch.equal(sr, round_bf16_sr(f32, salt=0x9e5b)) and torch.equal(sr, sr2)
+    ref = a.double() @ b.double().t()
+    floor = 1e-5 * float(ref.abs().max())
+    for got, ulps in ((rn, 2.0 ** -8), (whole, 2.0 ** -8), (sr, 2.0 ** -7)):
+        assert bool(((got.double() - ref).abs() <= ref.abs() * ulps + floor).all())
+    if M * N >= 1 << 16:  # stochastic rounding is unbiased: the signed errors average out
+        err = sr.double() - f32.double()
+        assert abs(float(err.mean())) <= 0.05 * float(err.abs().mean())
+
+
 @pytest.mark.parametrize("shapes,K,paired,strided", [
     (((1024, 4096), (4096, 1024)), 16376, True, False),    # cfg3 FeedForward weight gradients: 128 tiles x 2 splits
     (((1024, 1024), (1024, 2048)), 3000, True, False),     # 48 tiles x 5 splits, ragged K
