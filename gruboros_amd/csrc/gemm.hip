@@ -2274,11 +2274,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   }
 }
 
-// C[m, n] = bf16 of the sum over the S split partials (in split order): rounded to
-// nearest, or stochastically with the unsplit epilogue's hash of the element index
-// (EPI_SR), so only the fp32 sum's order differs from the unsplit product.
+// C[m, n] = bf16 of the sum over the S split partials (in split order), plus bias[n] when
+// given (EPI_BIAS): rounded to nearest, or stochastically with the unsplit epilogue's hash of
+// the element index (EPI_SR), so only the fp32 sum's order differs from the unsplit product.
 __global__ __launch_bounds__(256) void split_reduce_bf16_kernel(const float* __restrict__ part, int S, int M, int N,
-                                                               bf16_t* __restrict__ C, int64_t ldc, int stochastic) {
+                                                               bf16_t* __restrict__ C, int64_t ldc, int stochastic,
+                                                               const float* __restrict__ bias) {
   const int64_t n4 = static_cast<int64_t>(M) * (N / 4);
   const int64_t slice = static_cast<int64_t>(M) * N;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n4;
@@ -2290,6 +2291,11 @@ __global__ __launch_bounds__(256) void split_reduce_bf16_kernel(const float* __r
       const f4 v = load4_stream(pp + s * slice);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sum.v[e] += v.v[e];
+    }
+    if (bias) {
+      const f4 bv = io4<float>::load(bias + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum.v[e] += bv.v[e];
     }
     bf16_t* cp = C + m * ldc + n;
     if (stochastic)
@@ -2304,8 +2310,9 @@ constexpr int kCUs = 256;
 // Tile size and K split of a product (measured on MI355X): weight gradients
 // (both operands MN-contiguous, long K) run 128 x 128 tiles split along K
 // into about two workgroups per CU; the other layouts run 256 x 256 when
-// that still gives every CU a workgroup, else 128 x 128 (fp32 outputs then
-// split K). `ysplits` is the split count the launch uses (gridDim.y).
+// that still gives every CU a workgroup, else 128 x 128 (plain fp32 and bf16
+// outputs then split K to about two workgroups per CU as well).
+// `ysplits` is the split count the launch uses (gridDim.y).
 struct Plan {
   bool big;
   int tiles, kt_per_split, ysplits;
@@ -2330,14 +2337,17 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   const int64_t tiles = pl.big ? t256 : t128;
   pl.tiles = static_cast<int>(tiles);
   const int nkt = (hilo ? 3 : 1) * ((K + BK - 1) / BK);
-  const int64_t want_wgs = wgrad && !wgrad_big ? 2 * kCUs : kCUs;
+  const int64_t want_wgs = !pl.big ? 2 * kCUs : kCUs;
   int splits = 1;
-  // fp32 outputs and plain bf16 outputs (no epilogue, no hi/lo operands; a stochastically
-  // rounded gradient among them) split K when the tiles leave CUs idle: partials in fp32, then
-  // split_reduce_kernel (fp32) or split_reduce_bf16_kernel (rounded as the unsplit epilogue
-  // would). Hi/lo bf16 products stay whole, equal to mg_gemm_hilo_prefix's columns.
+  // fp32 outputs and plain bf16 outputs (no epilogue or a bias, no hi/lo operands; a
+  // stochastically rounded gradient among them) split K when the tiles leave CUs idle: partials
+  // in fp32, then split_reduce_kernel (fp32) or split_reduce_bf16_kernel (bias added, rounded as
+  // the unsplit epilogue would). Hi/lo bf16 products stay whole, equal to mg_gemm_hilo_prefix's
+  // columns. 128 x 128 tiles aim at two workgroups per CU (measured at [1, 2048] chunks of the
+  // d1024 expansion-3 model: 369 -> 351 ms per optimizer step against one; four: 378 ms).
   const bool split_ok = c_dtype == MG_F32 || (c_dtype == MG_BF16 && !hilo);
-  if (epilogue == MG_EPI_NONE && split_ok && tiles < want_wgs && !deterministic)
+  const bool epi_ok = epilogue == MG_EPI_NONE || (epilogue == MG_EPI_BIAS && c_dtype == MG_BF16 && !hilo);
+  if (epi_ok && split_ok && tiles < want_wgs && !deterministic)
     splits = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want_wgs / tiles, 1), std::max(nkt / 4, 1)));
   pl.kt_per_split = std::max((nkt + splits - 1) / splits, 1);
   pl.ysplits = std::max((nkt + pl.kt_per_split - 1) / pl.kt_per_split, 1);
@@ -2633,7 +2643,8 @@ extern "C" int mg_gemm(int a_layout, const void* A, int64_t lda, int b_layout, c
                        static_cast<float*>(C), ldc, p.accumulate);
   else
     hipLaunchKernelGGL(gemm::split_reduce_bf16_kernel, rgrid, dim3(256), 0, s, p.part, pl.ysplits, M, N,
-                       static_cast<bf16_t*>(C), ldc, (flags & MG_GEMM_STOCHASTIC) ? 1 : 0);
+                       static_cast<bf16_t*>(C), ldc, (flags & MG_GEMM_STOCHASTIC) ? 1 : 0,
+                       epilogue == MG_EPI_BIAS ? bias : nullptr);
   return check_launch(fn);
 }
 

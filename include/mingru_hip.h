@@ -337,11 +337,13 @@ int mg_sf_adamw_step(const void* tensors, int ntensors, int64_t nchunks,
  *     the dropped A_lo B_lo term is ~2^-16 relative). Used where bf16
  *     rounding of a product would move a result across the kink of the
  *     reference's g(x) at 0 (the hidden half of to_hidden_and_gate, to_out).
- * Split along K: fp32 outputs with few output tiles are split along K over
- *   several workgroups when a workspace is given. Each writes its partial
- *   tile there and a second kernel adds the partials, in split order, into C
- *   (plus C's old value when accumulating), so results repeat bit for bit
- *   either way (split and unsplit sums differ in order).
+ * Split along K: products with few output tiles (fp32 outputs with no
+ *   epilogue; bf16 outputs with none or MG_EPI_BIAS, not hi/lo) are split along
+ *   K over several workgroups when a workspace is given. Each writes its fp32
+ *   partial tile there and a second kernel adds the partials, in split order,
+ *   into C (plus C's old value when accumulating; plus the bias, then one
+ *   rounding to bf16, nearest or stochastic as the flags ask), so results
+ *   repeat bit for bit either way (split and unsplit sums differ in order).
  *   workspace: mg_gemm_workspace_bytes(...) bytes (0: the product never
  *   splits), 16-byte aligned; NULL runs unsplit. Calls sharing a workspace
  *   must be ordered on one stream.

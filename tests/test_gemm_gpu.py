@@ -524,13 +524,15 @@ def test_gemm_bf16_split_rounds_the_fp32_split_sum(al, bl, M, N, K):
     products do (fp32 partials, summed in split order by the reduction pass), and the pass rounds
     the sum once: to nearest, or stochastically with the unsplit epilogue's hash of the element
     index. So they equal the fp32 split product rounded by torch (to nearest) or by
-    mg_round_bf16_sr with the gradient salt 0x9e5b, bit for bit; and the unsplit product
+    mg_round_bf16_sr with the gradient salt 0x9e5b, bit for bit; with a bias epilogue, the bias
+    is added to that fp32 sum before the rounding to nearest; and the unsplit product
     (deterministic flag) and the split one are both within one bf16 rounding of the fp64 product."""
     from gruboros_amd import _lib
-    from gruboros_amd.gemm import gemm, round_bf16_sr
+    from gruboros_amd.gemm import EPI_BIAS, EPI_NONE, gemm, round_bf16_sr
 
     L = _lib.lib()
-    assert L.mg_gemm_workspace_bytes(al, bl, M, N, K, 0, _lib.dtype_code(torch.bfloat16), 0) > 0, "plan not split"
+    for epi in (EPI_NONE, EPI_BIAS):
+        assert L.mg_gemm_workspace_bytes(al, bl, M, N, K, epi, _lib.dtype_code(torch.bfloat16), 0) > 0, "not split"
     g = torch.Generator(device=DEV).manual_seed(M + N + K + 7 * al + 11 * bl)
     a, ad = _dev_operand(M, K, al, g)
     b, bd = _dev_operand(N, K, bl, g, scale=0.05)
@@ -544,9 +546,13 @@ def test_gemm_bf16_split_rounds_the_fp32_split_sum(al, bl, M, N, K):
     gemm(ad, al, bd, bl, M, N, K, sr2, stochastic=True)
     whole = torch.full_like(rn, 3.0)
     gemm(ad, al, bd, bl, M, N, K, whole, deterministic=True)
+    bias = torch.randn(N, device=DEV, generator=g)
+    rb = torch.full_like(rn, 3.0)
+    gemm(ad, al, bd, bl, M, N, K, rb, epilogue=EPI_BIAS, bias=bias)
     torch.cuda.synchronize()
     print(f"bf16 split {al}{bl} {M}x{N}x{K}", flush=True)
     assert torch.equal(rn, f32.to(torch.bfloat16))
+    assert torch.equal(rb, (f32 + bias).to(torch.bfloat16))
     assert torch.equal(sr, round_bf16_sr(f32, salt=0x9e5b)) and torch.equal(sr, sr2)
     ref = a.double() @ b.double().t()
     floor = 1e-5 * float(ref.abs().max())
