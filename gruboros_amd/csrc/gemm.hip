@@ -2327,9 +2327,12 @@ inline Plan plan(int M, int N, int K, bool ak, bool bk, int c_dtype, int epilogu
   // tiles (half the L2 traffic per flop of 128 x 128), split along K to about
   // one workgroup per CU; with fewer than 16 such tiles (the logits' 256 x 1024:
   // 4 tiles, 64 splits of 4 k-tiles) the splits get too short and their
-  // partials too many, and 128 x 128 tiles are faster (measured 27 against 40 us)
+  // partials too many, and 128 x 128 tiles are faster (measured 27 against 40 us).
+  // Below K 4096 (a [1, 2048] chunk's weight gradients, added into .grad) the
+  // 128 x 128 tiles need fewer splits or none, so fewer partials to write and add
+  // (d1024 expansion-3 optimizer step 348.4 -> 343.7 ms)
 #ifndef MG_GEMM_WGRAD128
-  const bool wgrad_big = wgrad && M % 256 == 0 && N % 256 == 0 && t256 >= 16;
+  const bool wgrad_big = wgrad && M % 256 == 0 && N % 256 == 0 && t256 >= 16 && K >= 4096;
 #else
   const bool wgrad_big = false;
 #endif

@@ -334,12 +334,14 @@ def _dev_operand(rows, k, layout, g, scale=1.0):
     (0, 1, 16376, 1024, 2048),   # input gradients (B read through the transposed LDS read)
     (1, 0, 4096, 4096, 1024),    # MN-contiguous A
     (1, 1, 2048, 1024, 16376),   # weight gradients: ragged K tail, split along K
-    (1, 1, 4096, 1024, 1000),    # short ragged K
+    (1, 1, 4096, 1024, 4104),    # the shortest K on 256 x 256 weight-gradient tiles, ragged
+    (1, 1, 4096, 1024, 1000),    # short ragged K: 128 x 128 tiles
 ])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_gemm_four_wave_tiles(al, bl, M, N, K, out_dtype):
     """The four-wave 256 x 256 loop (mainloop_w4: every operand layout, no masked
-    loads) against fp64 products of the same bf16 operands."""
+    loads; weight gradients below K 4096 take 128 x 128 tiles) against fp64 products
+    of the same bf16 operands."""
     from gruboros_amd.gemm import gemm
 
     g = torch.Generator(device=DEV).manual_seed(M + N + K + al + 2 * bl)
