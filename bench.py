@@ -106,6 +106,57 @@ def bench_train(steps, warmup, B=8, S=2048, dim=1024, depth=8, accum=1, ref_loop
             "params": sum(p.numel() for p in model.parameters())}
 
 
+def bench_production_train(steps=3, warmup=2, chunks=8, S=2048):
+    """The reference's production training run (train.cuda.sh:60-62: dim 1024, expansion 3.0,
+    ff_mult 1.5, --params 1g -> depth 79; train.cuda.sh:71-73: grad_accum 8, chunk_size 2048,
+    context_chunks 8; batch 1), as train.py:782-809 runs it: each optimizer step backpropagates
+    8 consecutive [1, 2048] chunks of one sequence, the hiddens carried from chunk to chunk
+    (detached), the loss scaled by 1 / grad_accum. Tokens counted as train.py:745 does
+    (batch x chunk_size per chunk)."""
+    import torch
+
+    from gruboros_amd.mingru.minLM import minLM
+    from gruboros_amd.optim import AdamWScheduleFree
+
+    torch.manual_seed(0)
+    dim, depth, expansion, ff_mult = 1024, 79, 3.0, 1.5
+    model = minLM(num_tokens=256, dim=dim, depth=depth, ff_mult=ff_mult, expansion=expansion,
+                  compute_dtype=torch.bfloat16).cuda()
+    opt = AdamWScheduleFree(model.parameters(), lr=1e-3, betas=(0.9, 0.995), weight_decay=1e-4)
+    opt.train()
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    ids = [torch.randint(0, 256, (1, S), device="cuda", generator=gen) for _ in range(chunks)]
+
+    def step():
+        hid = None
+        for i in range(chunks):
+            loss, hid = model(ids[i], return_loss=True, return_prev_hiddens=True, prev_hiddens=hid)
+            hid = [h.detach() for h in hid]
+            (loss / chunks).backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    tokens = chunks * S
+    flops = 6.0 * cfg3_matmul_params(dim, depth, ff_mult=ff_mult, expansion=expansion) * tokens
+    params = sum(p.numel() for p in model.parameters())
+    del model, opt
+    return {"workload": f"production run shape: minLM d{dim} L{depth} exp{expansion} ff{ff_mult} "
+                        f"({params / 1e9:.2f} B params, bf16 compute), {chunks} chunks of [1, {S}] per optimizer "
+                        "step, hiddens carried, SF-AdamW",
+            "steps": steps, "warmup": warmup, "ms_per_step": ms, "tokens_per_s": tokens / (ms * 1e-3),
+            "TFLOPs": flops / (ms * 1e-3) / 1e12, "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "loss": float(loss.detach())}
+
+
 def bench_scan(reps=20, B=16, T=8192, Di=2048):
     import torch
 
@@ -538,7 +589,7 @@ def main():
     if args.only in (None, "cfg1"):
         cfg1 = bench_cfg1()
         print(f"[bench] cfg1 {json.dumps(cfg1)}", file=sys.stderr, flush=True)
-    cfg5 = None
+    cfg5 = prod = None
     if args.only is None and args.workload == "cfg3":
         # the ~1B-parameter configuration beside the headline: a few optimizer
         # steps of 4 accumulated [4, 4096] micro-batches (d2048, L24)
@@ -549,6 +600,9 @@ def main():
                 "ms_per_step": t5["ms_per_step"], "tokens_per_s": t5["tokens_per_step"] / (t5["ms_per_step"] * 1e-3),
                 "TFLOPs": t5["tflops"], "frac_bf16_peak": t5["tflops"] / BF16_PEAK_TFLOPS}
         print(f"[bench] cfg5 {json.dumps(cfg5)}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        prod = bench_production_train()
+        print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
     cpu = cpu_scan = None
     if not args.no_cpu_baseline:
@@ -617,6 +671,8 @@ def main():
         out["cfg1"] = cfg1
     if cfg5:
         out["cfg5"] = cfg5
+    if prod:
+        out["production_train"] = prod
     if cpu:
         out["cpu_baseline"] = cpu
     if cpu_scan:

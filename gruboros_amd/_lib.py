@@ -133,12 +133,24 @@ def dtype_code(dt: torch.dtype) -> int:
                          "(cast a float16 model with .to(torch.bfloat16) instead)")
 
 
+# Pointer and stream arguments go to the library as plain integers (every one is
+# declared c_void_p, which takes an int; None is NULL): the per-call cost of
+# building ctypes objects and torch.cuda.Stream wrappers is measurable at the
+# ~20 k library calls of a [1, 2048]-chunk optimizer step of a 79-layer model.
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
 def ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    return None if t is None else t.data_ptr()
 
 
-def stream_of(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+def raw_stream(device: torch.device) -> int:
+    """Handle of the current HIP stream of a CUDA device (0 for the null stream)."""
+    return _raw_stream(device.index)
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return _raw_stream(t.device.index)
 
 
 def require_cuda(*tensors):

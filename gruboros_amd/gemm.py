@@ -50,11 +50,13 @@ def fits(a, w):
 
 # Split-K partial buffers, one per (device, stream), grown on demand.
 _WORKSPACES = {}
+# mg_gemm_workspace_bytes by (layouts, shape, epilogue, output dtype, flags): a pure function
+# of its arguments, asked once per shape instead of once per call.
+_WS_BYTES = {}
 
 
 def _workspace(device, nbytes):
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+    key = (device.index, _lib.raw_stream(device))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -82,7 +84,10 @@ def gemm(a, a_layout, b, b_layout, M, N, K, out, *, epilogue=EPI_NONE, bias=None
         raise _lib.MingruHipError("mg_gemm bias must be contiguous float32")
     L = _lib.lib()
     cd = _lib.dtype_code(out.dtype)
-    wsb = L.mg_gemm_workspace_bytes(a_layout, b_layout, M, N, K, epilogue, cd, flags)
+    wkey = (a_layout, b_layout, M, N, K, epilogue, cd, flags)
+    wsb = _WS_BYTES.get(wkey)
+    if wsb is None:
+        wsb = _WS_BYTES[wkey] = L.mg_gemm_workspace_bytes(a_layout, b_layout, M, N, K, epilogue, cd, flags)
     ws = _workspace(out.device, wsb) if wsb else None
     rc = L.mg_gemm(a_layout, _lib.ptr(a), lda, b_layout, _lib.ptr(b), ldb, M, N, K, epilogue,
                    _lib.ptr(bias) if bias is not None else None, _lib.ptr(aux) if aux is not None else None, ldaux,

@@ -9,7 +9,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import check, dtype_code, lib, ptr, require_cuda, stream_of
+from ._lib import check, dtype_code, lib, ptr, raw_stream, require_cuda, stream_of
 
 
 # Look-back workspaces, one per (device, stream, B, T, Di): initialised
@@ -24,8 +24,7 @@ _USED = set()
 
 
 def _workspace(device, B, T, Di):
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream, B, T, Di)
+    key = (device.index, raw_stream(device), B, T, Di)
     _USED.add(key)
     ws = _WORKSPACES.get(key)
     if ws is None:
