@@ -514,7 +514,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--scan-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode", "ceilings", "cfg1"], default=None)
+    ap.add_argument("--only", choices=["train", "scan", "kernels", "decode", "ceilings", "cfg1", "production"],
+                    default=None)
     ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
                     help="training workload for `value`: cfg3 (the BASELINE metric, default) or cfg5 "
                          "(~1B params: d2048 L24, batch 4 x seq 4096, gradient accumulation 4)")
@@ -604,6 +605,9 @@ def main():
         prod = bench_production_train()
         print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+    if args.only == "production":
+        prod = bench_production_train()
+        print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
     cpu = cpu_scan = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
