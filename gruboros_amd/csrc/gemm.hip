@@ -2307,12 +2307,12 @@ __global__ __launch_bounds__(256) void split_reduce_bf16_kernel(const float* __r
 
 constexpr int kCUs = 256;
 
-// Tile size and K split of a product (measured on MI355X): weight gradients
-// (both operands MN-contiguous, long K) run 128 x 128 tiles split along K
-// into about two workgroups per CU; the other layouts run 256 x 256 when
-// that still gives every CU a workgroup, else 128 x 128 (plain fp32 and bf16
-// outputs then split K to about two workgroups per CU as well).
-// `ysplits` is the split count the launch uses (gridDim.y).
+// Tile size and K split of a product (measured on MI355X): 256 x 256 tiles for
+// weight gradients (both operands MN-contiguous) of whole 256 x 256 tiles, at
+// least 16 of them, K >= 4096, split along K to about one workgroup per CU, and
+// for the other layouts when that still gives every CU a tile; everything else
+// 128 x 128, split along K (outputs and epilogues that allow it) to about two
+// workgroups per CU. `ysplits` is the split count the launch uses (gridDim.y).
 struct Plan {
   bool big;
   int tiles, kt_per_split, ysplits;
