@@ -411,6 +411,29 @@ def test_tbptt_training_chunk_with_carried_state_cfg4():
     torch.cuda.empty_cache()
 
 
+def test_tbptt_training_chunk_at_production_widths():
+    """The reference's production run widths (train.cuda.sh:60-62: d1024, expansion 3.0,
+    ff_mult 1.5; train.cuda.sh:71-73: batch 1, chunk 2048) at depth 2: two consecutive [1, 2048]
+    chunks, the second seeded with the first's detached hiddens. With 2047 rows per product the
+    small-output K-split plans run (bf16 input gradients and bias products rounded after the
+    split reduction, to_out's hi/lo forward split, weight gradients below K 4096 on 128 x 128
+    tiles). Loss, next hiddens and every parameter gradient within 2e-2 of the fp64 oracle."""
+    from gruboros_amd import _lib
+    from gruboros_amd.gemm import FLAG_STOCHASTIC, KCONTIG, MNCONTIG
+
+    L = _lib.lib()  # to_hidden_and_gate's input gradient at this shape is a split product
+    assert L.mg_gemm_workspace_bytes(KCONTIG, MNCONTIG, 2047, 1024, 6144, 0, _lib.MG_BF16, FLAG_STOCHASTIC) > 0
+    torch.cuda.empty_cache()
+    m, sd = _model(1024, 2, 3.0, torch.bfloat16, seed=8, ff_mult=1.5)
+    ids = torch.randint(0, 256, (1, 4096), device=DEV, generator=torch.Generator(device=DEV).manual_seed(8))
+    e_loss, e_hid, errs, cold = _tbptt_second_chunk(m, sd, ids, 2, 3.0, 2048)
+    print(f"tbptt production widths: loss {e_loss:.2e}, hiddens {e_hid:.2e}, worst grads "
+          f"{[(f'{e:.2e}', n) for e, n in errs[:3]]}, cold-start loss gap {cold:.2e}", flush=True)
+    assert e_loss <= 2e-2 and e_hid <= 2e-2 and errs[0][0] <= 2e-2, errs[:3]
+    del m
+    torch.cuda.empty_cache()
+
+
 def test_cfg5_shapes_match_fp64_oracle():
     """cfg5's shapes against the oracle: a d2048 ff4 bf16
     minLM slice of two layers, batch 1 x 4096 ids (a 4095-step scan, K = 2048
