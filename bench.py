@@ -564,6 +564,14 @@ def main():
                            "prev_hiddens=None); loss.detach().item(); (loss / grad_accum).backward(); "
                            "optimizer.step(); optimizer.zero_grad() (grad_accum 1)"}
             print(f"[bench] reference loop {json.dumps(ref)}", file=sys.stderr, flush=True)
+    prod = None
+    if args.only == "production" or (args.only is None and args.workload == "cfg3"):
+        # before the decode phase, for the reason given above: this step is host-heavy (~22 k
+        # launches) and measured 343-346 ms alone against 359-370 ms after the decode phase
+        torch.cuda.empty_cache()
+        prod = bench_production_train()
+        print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     if args.only in (None, "ceilings"):
         ceil = bench_ceilings()
         print(f"[bench] ceilings {json.dumps(ceil)}", file=sys.stderr, flush=True)
@@ -590,7 +598,7 @@ def main():
     if args.only in (None, "cfg1"):
         cfg1 = bench_cfg1()
         print(f"[bench] cfg1 {json.dumps(cfg1)}", file=sys.stderr, flush=True)
-    cfg5 = prod = None
+    cfg5 = None
     if args.only is None and args.workload == "cfg3":
         # the ~1B-parameter configuration beside the headline: a few optimizer
         # steps of 4 accumulated [4, 4096] micro-batches (d2048, L24)
@@ -602,12 +610,6 @@ def main():
                 "TFLOPs": t5["tflops"], "frac_bf16_peak": t5["tflops"] / BF16_PEAK_TFLOPS}
         print(f"[bench] cfg5 {json.dumps(cfg5)}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
-        prod = bench_production_train()
-        print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
-        torch.cuda.empty_cache()
-    if args.only == "production":
-        prod = bench_production_train()
-        print(f"[bench] production train {json.dumps(prod)}", file=sys.stderr, flush=True)
     cpu = cpu_scan = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
