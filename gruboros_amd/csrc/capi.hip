@@ -8,6 +8,6 @@ char* last_error_buf() {
 }
 }  // namespace mg
 
-extern "C" int mg_version(void) { return 205; }  // 0.2.5
+extern "C" int mg_version(void) { return 206; }  // 0.2.6
 
 extern "C" const char* mg_last_error(void) { return mg::last_error_buf(); }

@@ -44,9 +44,10 @@ extern "C" {
 #define MG_ERR_HIP 4      /* a HIP runtime call or kernel launch failed */
 #define MG_ERR_STALL 5    /* a scan's look-back wait gave up (see mg_scan_workspace_check) */
 
-/* Library version (major*10000 + minor*100 + patch): 205 = 0.2.5, the ABI
+/* Library version (major*10000 + minor*100 + patch): 206 = 0.2.6, the ABI
  * declared in this file (0.2.1 to 0.2.5 add entry points to 0.2.0 and change
- * none). */
+ * none; 0.2.6 changes no signature: mg_gemm also splits small bf16 products
+ * along K, see mg_gemm). */
 int mg_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */

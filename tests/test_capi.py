@@ -39,7 +39,7 @@ def test_every_declared_symbol_is_exported(L):
 
 
 def test_version_and_queries(L):
-    assert L.mg_version() == 205  # 0.2.5: the ABI of include/mingru_hip.h
+    assert L.mg_version() == 206  # 0.2.6: the ABI of include/mingru_hip.h
     # a 256-byte header, ticket counters per chain and direction (rounded to
     # 256 B) + one 8-byte look-back word per (tile, channel) for the forward
     # (128-step tiles) and the backward (64-step tiles)
